@@ -1,0 +1,1023 @@
+// libfirewing_hip_moe: the sparse-MoE block hot path for MI355X (gfx950)
+// behind the C ABI of include/firewing_hip_moe.h.
+//
+// Stateless entry points (linear, SwiGLU, sigmoid, top-k, route, expert) copy
+// host buffers in, run exact-order kernels and copy out. The resident context
+// keeps every layer's weights in HBM and runs a whole block, or a whole
+// 48-layer decode step, as one persistent launch (fw_decode.h).
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <new>
+#include <string>
+#include <vector>
+
+#include "../../include/firewing_hip_moe.h"
+#include "fw_decode.h"
+#include "fw_device.h"
+#include "fw_numerics.h"
+#include "fw_synth.h"
+
+using namespace fw;
+
+// ---- error reporting ------------------------------------------------------------------
+
+namespace {
+
+thread_local std::string g_last_error;
+
+bool fail(const std::string& message) {
+    g_last_error = message;
+    return false;
+}
+
+struct HipError {
+    std::string message;
+};
+
+void check(hipError_t status, const char* what) {
+    if (status != hipSuccess) {
+        throw HipError{std::string(what) + ": " + hipGetErrorString(status)};
+    }
+}
+
+template <typename F>
+bool guarded(F&& body) {
+    try {
+        return body();
+    } catch (const HipError& e) {
+        return fail(e.message);
+    } catch (const std::bad_alloc&) {
+        return fail("host allocation failed");
+    } catch (const std::exception& e) {
+        return fail(e.what());
+    } catch (...) {
+        return fail("unexpected failure");
+    }
+}
+
+// Host copy of the 2^(i/32) table (same constants as c_exp2_table).
+const uint64_t kExp2TableHost[32] = {
+    0x3ff0000000000000ULL, 0x3fefd9b0d3158574ULL, 0x3fefb5586cf9890fULL, 0x3fef9301d0125b51ULL,
+    0x3fef72b83c7d517bULL, 0x3fef54873168b9aaULL, 0x3fef387a6e756238ULL, 0x3fef1e9df51fdee1ULL,
+    0x3fef06fe0a31b715ULL, 0x3feef1a7373aa9cbULL, 0x3feedea64c123422ULL, 0x3feece086061892dULL,
+    0x3feebfdad5362a27ULL, 0x3feeb42b569d4f82ULL, 0x3feeab07dd485429ULL, 0x3feea47eb03a5585ULL,
+    0x3feea09e667f3bcdULL, 0x3fee9f75e8ec5f74ULL, 0x3feea11473eb0187ULL, 0x3feea589994cce13ULL,
+    0x3feeace5422aa0dbULL, 0x3feeb737b0cdc5e5ULL, 0x3feec49182a3f090ULL, 0x3feed503b23e255dULL,
+    0x3feee89f995ad3adULL, 0x3feeff76f2fb5e47ULL, 0x3fef199bdd85529cULL, 0x3fef3720dcef9069ULL,
+    0x3fef5818dcfba487ULL, 0x3fef7c97337b9b5fULL, 0x3fefa4afa2a490daULL, 0x3fefd0765b6e4540ULL,
+};
+
+// RAII device buffer for the stateless entry points.
+struct DeviceBuffer {
+    void* ptr = nullptr;
+    explicit DeviceBuffer(size_t bytes) {
+        if (bytes) check(hipMalloc(&ptr, bytes), "hipMalloc");
+    }
+    ~DeviceBuffer() {
+        if (ptr) (void)hipFree(ptr);
+    }
+    DeviceBuffer(const DeviceBuffer&) = delete;
+    DeviceBuffer& operator=(const DeviceBuffer&) = delete;
+    template <typename T>
+    T* as() const {
+        return static_cast<T*>(ptr);
+    }
+};
+
+void upload(void* dst, const void* src, size_t bytes, hipStream_t s) {
+    if (bytes) check(hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, s), "hipMemcpyAsync H2D");
+}
+void download(void* dst, const void* src, size_t bytes, hipStream_t s) {
+    if (bytes) check(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, s), "hipMemcpyAsync D2H");
+}
+
+}  // namespace
+
+// ---- standalone kernels -----------------------------------------------------------------
+
+namespace fw {
+
+// out[t][r] = bf16(tree32(W[r,:], x[t,:])) for NT tokens; 4 rows per wave,
+// 16 rows per 256-thread block; x staged in LDS as f32 (dynamic shared).
+template <int NT>
+__global__ void __launch_bounds__(256) k_linear_tree32(const uint16_t* __restrict__ w,
+                                                       const uint16_t* __restrict__ x, int rows,
+                                                       int K, uint16_t* __restrict__ out) {
+    extern __shared__ float xs[];
+    for (int i = threadIdx.x; i < NT * K; i += blockDim.x) xs[i] = from_bf16(x[i]);
+    __syncthreads();
+    const int row0 = blockIdx.x * 16 + wave_id() * kRowsPerWave;
+    const int valid = rows - row0;
+    if (valid <= 0) return;
+    const int lane = lane_id();
+    const int g = lane / kLanesPerRow;
+    const int q = lane % kLanesPerRow;
+    const bool ok = g < valid;
+    const int r = ok ? row0 + g : row0;
+    float acc[NT][2];
+    tree32_sweep<NT, 8>(reinterpret_cast<const uint32_t*>(w + (size_t)r * K), K / 32, xs, K, q,
+                        ok ? (1u << NT) - 1u : 0u, acc);
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
+        float d = tree32_reduce(acc[t][0], acc[t][1]);
+        if (q == 0 && ok) {
+            d = tree32_finish(d, w + (size_t)r * K, xs + t * K, K);
+            out[(size_t)t * rows + r] = to_bf16(d);
+        }
+    }
+}
+
+// out[t][r] = bf16(fold(W[r,:], x[t,:])): one thread per (row, token).
+__global__ void k_linear_fold(const uint16_t* __restrict__ w, const uint16_t* __restrict__ x,
+                              int rows, int K, int T, uint16_t* __restrict__ out) {
+    extern __shared__ float xs[];
+    for (int i = threadIdx.x; i < T * K; i += blockDim.x) xs[i] = from_bf16(x[i]);
+    __syncthreads();
+    int r = blockIdx.x * blockDim.x + threadIdx.x;
+    if (r >= rows) return;
+    for (int t = 0; t < T; ++t) out[(size_t)t * rows + r] = to_bf16(fold_row(w + (size_t)r * K, xs + t * K, K));
+}
+
+__global__ void k_swiglu(const uint16_t* gate, const uint16_t* up, size_t n, uint16_t* out) {
+    size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) out[i] = swiglu_bf16(gate[i], up[i], c_exp2_table);
+}
+
+__global__ void k_sigmoid(const uint16_t* in, size_t n, uint16_t* out) {
+    size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) out[i] = sigmoid_bf16(in[i], c_exp2_table);
+}
+
+__global__ void k_expf(const float* in, float* out, size_t n) {
+    size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) out[i] = expf_glibc(in[i], c_exp2_table);
+}
+
+__global__ void k_scale_bf16(const uint16_t* in, uint16_t weight, size_t n, uint16_t* out) {
+    size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) out[i] = to_bf16(mul_rn(from_bf16(in[i]), from_bf16(weight)));
+}
+
+// Top-k (and optionally scores) of T rows of `count` logits: one wave per row.
+// With scores: max, exp(v - max), sequential sum, renormalised selection
+// (src/router.rs:248-262). reject_nan: src/decoder_layer.rs:279-281.
+__global__ void __launch_bounds__(64) k_select(const uint16_t* __restrict__ logits, int count,
+                                               int k, int32_t* __restrict__ ids,
+                                               uint16_t* __restrict__ scores, int reject_nan,
+                                               int32_t* __restrict__ error) {
+    __shared__ float ex[kMaxExperts];
+    __shared__ int32_t sid[kMaxTopK];
+    const uint16_t* lt = logits + (size_t)blockIdx.x * count;
+    const int lane = lane_id();
+    if (reject_nan) {
+        int nan = 0;
+        for (int e = lane; e < count; e += kWave) nan |= ((lt[e] & 0x7fffu) > 0x7f80u);
+        if (__any(nan)) {
+            if (lane == 0) atomicExch(error, 2);
+            return;
+        }
+    }
+    wave_topk<kMaxExperts / kWave>(lt, count, k, sid);
+    __syncthreads();
+    if (lane < k) ids[(size_t)blockIdx.x * k + lane] = sid[lane];
+    if (scores == nullptr) return;
+    float mx = -__builtin_inff();
+    for (int e = lane; e < count; e += kWave) mx = fmaxf(mx, from_bf16(lt[e]));
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off, kWave));
+    for (int e = lane; e < count; e += kWave) ex[e] = expf_glibc(add_rn(from_bf16(lt[e]), -mx), c_exp2_table);
+    __syncthreads();
+    if (lane == 0) {
+        float den = -0.0f;
+        for (int e = 0; e < count; ++e) den = add_rn(den, ex[e]);
+        float sel = -0.0f;
+        for (int r = 0; r < k; ++r) sel = add_rn(sel, ex[sid[r]] / den);
+        for (int r = 0; r < k; ++r) scores[(size_t)blockIdx.x * k + r] = to_bf16((ex[sid[r]] / den) / sel);
+    }
+}
+
+// Ordered bf16 mixture of n weighted rows: mix = 0; for i: mix = bf16(mix + w_i)
+// (src/expert.rs:953-955).
+__global__ void k_mixture(const uint16_t* __restrict__ weighted, int n, int H,
+                          uint16_t* __restrict__ out) {
+    int h = blockIdx.x * blockDim.x + threadIdx.x;
+    if (h >= H) return;
+    uint32_t mix = to_bf16(0.0f);
+    for (int i = 0; i < n; ++i) mix = add_bf16(mix, weighted[(size_t)i * H + h]);
+    out[h] = (uint16_t)mix;
+}
+
+// Synthetic weights: dst[i] = table[u16(stream, first + i)] (fw_synth.h).
+__global__ void k_generate(uint16_t* __restrict__ dst, size_t count, uint64_t stream,
+                           uint64_t first, const uint16_t* __restrict__ table) {
+    size_t quad = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    size_t i0 = quad * 4;
+    if (i0 >= count) return;
+    // first is a multiple of 4, so one hash serves four elements
+    uint64_t h = fw_mix64(stream + ((first + i0) >> 2));
+    uint16_t v[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) v[j] = table[(uint32_t)(h >> (16 * j)) & 0xffffu];
+    if (i0 + 4 <= count) {
+        uint2 packed;
+        packed.x = (uint32_t)v[0] | ((uint32_t)v[1] << 16);
+        packed.y = (uint32_t)v[2] | ((uint32_t)v[3] << 16);
+        *reinterpret_cast<uint2*>(dst + i0) = packed;
+    } else {
+        for (size_t j = 0; i0 + j < count; ++j) dst[i0 + j] = v[j];
+    }
+}
+
+// Router bias column: router[e][H-1] = bias[e].
+__global__ void k_router_bias(uint16_t* router, int E, int H, const uint16_t* bias) {
+    int e = blockIdx.x * blockDim.x + threadIdx.x;
+    if (e < E) router[(size_t)e * H + H - 1] = bias[e];
+}
+
+}  // namespace fw
+
+// ---- launch helpers ---------------------------------------------------------------------
+
+namespace {
+
+bool shape_ok_for_linear(size_t rows, size_t columns, std::string* why) {
+    if (rows == 0 || columns == 0) {
+        *why = "linear: rows and columns must be nonzero";
+        return false;
+    }
+    if (rows > (1u << 30) || columns > 16384) {
+        *why = "linear: rows must be < 2^30 and columns <= 16384";
+        return false;
+    }
+    return true;
+}
+
+void launch_linear(const uint16_t* w, const uint16_t* x, int rows, int K, int T, uint16_t* out,
+                   hipStream_t s) {
+    dim3 grid((rows + 15) / 16);
+    size_t shmem = (size_t)T * K * sizeof(float);
+    // columns that are not a multiple of 32 still work (tail by one lane), but
+    // the 16-lane sweep needs 4-byte aligned rows, so K must be even there.
+    switch (T) {
+        case 1: hipLaunchKernelGGL(k_linear_tree32<1>, grid, dim3(256), shmem, s, w, x, rows, K, out); break;
+        case 2: hipLaunchKernelGGL(k_linear_tree32<2>, grid, dim3(256), shmem, s, w, x, rows, K, out); break;
+        case 3: hipLaunchKernelGGL(k_linear_tree32<3>, grid, dim3(256), shmem, s, w, x, rows, K, out); break;
+        default: hipLaunchKernelGGL(k_linear_tree32<4>, grid, dim3(256), shmem, s, w, x, rows, K, out); break;
+    }
+    check(hipGetLastError(), "k_linear_tree32 launch");
+}
+
+}  // namespace
+
+// ---- resident context ---------------------------------------------------------------------
+
+struct firewing_hip_context {
+    firewing_hip_shape shape{};
+    int device = 0;
+    char device_name[256] = {0};
+    int cu_count = 0;
+    uint64_t wall_clock_hz = 100000000ULL;
+    hipStream_t stream = nullptr;
+    // resident banks
+    std::vector<uint16_t*> router;  // [E + 1][H] per layer
+    std::vector<uint16_t*> gate_up, down, shared_gate, shared_up, shared_down;
+    DecodeLayer* d_layers = nullptr;  // [L]
+    uint16_t* d_weight_table = nullptr;
+    // decode scratch sized for L layers and T <= 4
+    uint16_t *x = nullptr, *out = nullptr, *logits = nullptr, *scores = nullptr, *sig = nullptr;
+    uint16_t *shared_act = nullptr, *act = nullptr, *token_weights = nullptr;
+    int32_t *ids = nullptr, *slot_expert = nullptr, *union_count = nullptr, *token_slots = nullptr;
+    uint32_t *slot_tokens = nullptr, *counters = nullptr;
+    int32_t* error = nullptr;
+    int grid[kMaxTokens + 1] = {0};
+    double timeout_seconds = 10.0;  // per dependency wait (FIREWING_WAIT_TIMEOUT_S)
+};
+
+namespace {
+
+template <typename T>
+T* dalloc(size_t count) {
+    void* p = nullptr;
+    check(hipMalloc(&p, std::max<size_t>(count, 1) * sizeof(T)), "hipMalloc");
+    return static_cast<T*>(p);
+}
+
+bool validate_shape(const firewing_hip_shape& s, std::string* why) {
+    auto bad = [&](const char* m) {
+        *why = m;
+        return false;
+    };
+    if (s.hidden == 0 || s.hidden % 32 || s.hidden > (size_t)kMaxHidden)
+        return bad("hidden must be a nonzero multiple of 32 and <= 2560");
+    if (s.intermediate == 0 || s.intermediate % 32 || s.intermediate > 4096)
+        return bad("intermediate must be a nonzero multiple of 32 and <= 4096");
+    if (s.shared_intermediate == 0 || s.shared_intermediate % 32 || s.shared_intermediate > 4096)
+        return bad("shared_intermediate must be a nonzero multiple of 32 and <= 4096");
+    if (s.experts == 0 || s.experts > (size_t)kMaxExperts) return bad("experts must be in [1, 1024]");
+    if (s.top_k == 0 || s.top_k > (size_t)kMaxTopK || s.top_k > s.experts)
+        return bad("top_k must be in [1, min(32, experts)]");
+    if (s.layers == 0 || s.layers > 4096) return bad("layers must be in [1, 4096]");
+    return true;
+}
+
+template <int NT>
+int decode_grid(const firewing_hip_context* c) {
+    int per_cu = 0;
+    check(hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, k_moe_decode<NT>, 256, 0),
+          "hipOccupancyMaxActiveBlocksPerMultiprocessor");
+    if (per_cu < 1) throw HipError{"decode kernel cannot be resident"};
+    return per_cu * c->cu_count;
+}
+
+// Launch the persistent kernel over layers [first, first + n) for T tokens.
+// x[0] of the scratch must already hold the input.
+void launch_decode(firewing_hip_context* c, size_t first, size_t n, int T, int order,
+                   bool bias_feature, const uint16_t* x_in, uint16_t* x_final, hipStream_t s) {
+    const firewing_hip_shape& sh = c->shape;
+    DecodeParams p{};
+    p.layers = c->d_layers + first;
+    p.nlayers = (int)n;
+    p.T = T;
+    p.H = (int)sh.hidden;
+    p.I = (int)sh.intermediate;
+    p.E = (int)sh.experts;
+    p.K = (int)sh.top_k;
+    p.Is = (int)sh.shared_intermediate;
+    p.order = order;
+    p.bias_feature = bias_feature ? 1 : 0;
+    p.S = p.K * T;
+    const size_t L = n, Tn = (size_t)T, H = sh.hidden, E = sh.experts, K = sh.top_k;
+    const size_t S = (size_t)p.S, I = sh.intermediate, Is = sh.shared_intermediate;
+    p.x_in = x_in;
+    p.x = c->x;
+    p.x_final = x_final;
+    p.out = c->out;
+    p.logits = c->logits;
+    p.ids = c->ids;
+    p.scores = c->scores;
+    p.slot_expert = c->slot_expert;
+    p.slot_tokens = c->slot_tokens;
+    p.union_count = c->union_count;
+    p.token_slots = c->token_slots;
+    p.token_weights = c->token_weights;
+    p.sig = c->sig;
+    p.shared_act = c->shared_act;
+    p.act = c->act;
+    p.counters = c->counters;
+    p.error = c->error;
+    p.limit_ticks = (uint64_t)(c->timeout_seconds * (double)c->wall_clock_hz);
+    p.n_router = (int)((E + kRouterRowsPerTask - 1) / kRouterRowsPerTask) + 1;
+    p.n_shared = (int)((Is + kPairsPerTask - 1) / kPairsPerTask);
+    p.n_b = (int)(S * (I / kPairsPerTask));
+    p.n_c = (int)(H / kRowsPerCTask);
+    p.per_layer = p.n_router + p.n_shared + 1 + p.n_b + p.n_c;
+    (void)L;
+    (void)Tn;
+    (void)K;
+    void* args[] = {&p};
+    const void* fn = nullptr;
+    int grid = 0;
+    switch (T) {
+        case 1: fn = reinterpret_cast<const void*>(&k_moe_decode<1>); grid = c->grid[1]; break;
+        case 2: fn = reinterpret_cast<const void*>(&k_moe_decode<2>); grid = c->grid[2]; break;
+        case 3: fn = reinterpret_cast<const void*>(&k_moe_decode<3>); grid = c->grid[3]; break;
+        default: fn = reinterpret_cast<const void*>(&k_moe_decode<4>); grid = c->grid[4]; break;
+    }
+    check(hipLaunchCooperativeKernel(fn, dim3(grid), dim3(256), args, 0, s),
+          "hipLaunchCooperativeKernel(k_moe_decode)");
+}
+
+bool check_device_error(firewing_hip_context* c, hipStream_t s) {
+    int32_t err = 0;
+    check(hipMemcpyAsync(&err, c->error, sizeof err, hipMemcpyDeviceToHost, s), "hipMemcpyAsync error word");
+    check(hipStreamSynchronize(s), "hipStreamSynchronize");
+    if (err != 0) {
+        int32_t zero = 0;
+        check(hipMemcpy(c->error, &zero, sizeof zero, hipMemcpyHostToDevice), "reset error word");
+        if (err == 2) return fail("router produced a NaN logit (rejected, src/decoder_layer.rs:279-281)");
+        return fail("persistent decode kernel: a dependency wait exceeded its time limit");
+    }
+    return true;
+}
+
+}  // namespace
+
+// ---- C ABI ------------------------------------------------------------------------------
+
+extern "C" {
+
+const char* firewing_hip_last_error(void) { return g_last_error.c_str(); }
+
+void firewing_hip_synth_hidden(uint64_t seed, uint32_t first_token, uint32_t tokens,
+                               uint32_t hidden, bool bias_feature, uint16_t* out) {
+    static std::vector<uint16_t> unit_table;
+    if (unit_table.empty()) {
+        std::vector<uint16_t> table(65536);
+        fw_synth_normal_table(1.0, table.data());
+        unit_table.swap(table);
+    }
+    fw_synth_hidden(seed, first_token, tokens, hidden, bias_feature ? 1 : 0, unit_table.data(), out);
+}
+
+void firewing_hip_expf_host(const float* in, float* out, size_t count) {
+    for (size_t i = 0; i < count; ++i) out[i] = expf_glibc(in[i], kExp2TableHost);
+}
+
+bool firewing_hip_expf_device(const float* in, float* out, size_t count) {
+    return guarded([&] {
+        if (!in || !out) return fail("expf_device: null pointer");
+        DeviceBuffer din(count * 4), dout(count * 4);
+        upload(din.ptr, in, count * 4, nullptr);
+        if (count) {
+            hipLaunchKernelGGL(k_expf, dim3((unsigned)((count + 255) / 256)), dim3(256), 0, nullptr,
+                               din.as<float>(), dout.as<float>(), count);
+            check(hipGetLastError(), "k_expf launch");
+        }
+        download(out, dout.ptr, count * 4, nullptr);
+        check(hipStreamSynchronize(nullptr), "hipStreamSynchronize");
+        return true;
+    });
+}
+
+bool firewing_hip_linear_bf16(const uint16_t* weight, const uint16_t* input, size_t rows,
+                              size_t columns, uint16_t* out) {
+    return guarded([&] {
+        if (!weight || !input || !out) return fail("linear_bf16: null pointer");
+        std::string why;
+        if (!shape_ok_for_linear(rows, columns, &why)) return fail(why);
+        if (columns % 2) return fail("linear_bf16: columns must be even");
+        DeviceBuffer dw(rows * columns * 2), dx(columns * 2), dout(rows * 2);
+        upload(dw.ptr, weight, rows * columns * 2, nullptr);
+        upload(dx.ptr, input, columns * 2, nullptr);
+        launch_linear(dw.as<uint16_t>(), dx.as<uint16_t>(), (int)rows, (int)columns, 1,
+                      dout.as<uint16_t>(), nullptr);
+        download(out, dout.ptr, rows * 2, nullptr);
+        check(hipStreamSynchronize(nullptr), "hipStreamSynchronize");
+        return true;
+    });
+}
+
+bool firewing_hip_swiglu_bf16(const uint16_t* gate, const uint16_t* up, size_t count,
+                              uint16_t* out) {
+    return guarded([&] {
+        if (!gate || !up || !out) return fail("swiglu_bf16: null pointer");
+        if (count == 0) return true;
+        DeviceBuffer dg(count * 2), du(count * 2), dout(count * 2);
+        upload(dg.ptr, gate, count * 2, nullptr);
+        upload(du.ptr, up, count * 2, nullptr);
+        hipLaunchKernelGGL(k_swiglu, dim3((unsigned)((count + 255) / 256)), dim3(256), 0, nullptr,
+                           dg.as<uint16_t>(), du.as<uint16_t>(), count, dout.as<uint16_t>());
+        check(hipGetLastError(), "k_swiglu launch");
+        download(out, dout.ptr, count * 2, nullptr);
+        check(hipStreamSynchronize(nullptr), "hipStreamSynchronize");
+        return true;
+    });
+}
+
+bool firewing_hip_sigmoid_bf16(const uint16_t* input, size_t count, uint16_t* out) {
+    return guarded([&] {
+        if (!input || !out) return fail("sigmoid_bf16: null pointer");
+        if (count == 0) return true;
+        DeviceBuffer din(count * 2), dout(count * 2);
+        upload(din.ptr, input, count * 2, nullptr);
+        hipLaunchKernelGGL(k_sigmoid, dim3((unsigned)((count + 255) / 256)), dim3(256), 0, nullptr,
+                           din.as<uint16_t>(), count, dout.as<uint16_t>());
+        check(hipGetLastError(), "k_sigmoid launch");
+        download(out, dout.ptr, count * 2, nullptr);
+        check(hipStreamSynchronize(nullptr), "hipStreamSynchronize");
+        return true;
+    });
+}
+
+bool firewing_hip_topk_bf16(const uint16_t* values, size_t count, size_t k, size_t* indices) {
+    return guarded([&] {
+        if (!values || !indices || k == 0 || k > count) return fail("invalid top-k request");
+        if (count > (size_t)kMaxExperts || k > (size_t)kMaxTopK)
+            return fail("top-k: count must be <= 1024 and k <= 32");
+        DeviceBuffer dv(count * 2), dids(k * 4), derr(4);
+        upload(dv.ptr, values, count * 2, nullptr);
+        check(hipMemsetAsync(derr.ptr, 0, 4, nullptr), "hipMemsetAsync");
+        hipLaunchKernelGGL(k_select, dim3(1), dim3(64), 0, nullptr, dv.as<uint16_t>(), (int)count,
+                           (int)k, dids.as<int32_t>(), (uint16_t*)nullptr, 0, derr.as<int32_t>());
+        check(hipGetLastError(), "k_select launch");
+        std::vector<int32_t> ids(k);
+        download(ids.data(), dids.ptr, k * 4, nullptr);
+        check(hipStreamSynchronize(nullptr), "hipStreamSynchronize");
+        for (size_t i = 0; i < k; ++i) indices[i] = (size_t)ids[i];
+        return true;
+    });
+}
+
+bool firewing_hip_route_bf16(const uint16_t* weight, const uint16_t* hidden, size_t tokens,
+                             size_t experts, size_t width, size_t top_k, int order,
+                             size_t* ids, uint16_t* scores, uint16_t* logits) {
+    return guarded([&] {
+        if (!weight || !hidden || !ids || !scores) return fail("route_bf16: null pointer");
+        if (tokens == 0 || tokens > 4096) return fail("route_bf16: tokens must be in [1, 4096]");
+        if (experts == 0 || experts > (size_t)kMaxExperts) return fail("route_bf16: experts must be in [1, 1024]");
+        if (top_k == 0 || top_k > experts || top_k > (size_t)kMaxTopK)
+            return fail("route_bf16: top_k must be in [1, min(32, experts)]");
+        if (order != FIREWING_HIP_LOGITS_TREE32 && order != FIREWING_HIP_LOGITS_FOLD)
+            return fail("route_bf16: unknown logit order");
+        std::string why;
+        if (!shape_ok_for_linear(experts, width, &why)) return fail(why);
+        if (width % 2) return fail("route_bf16: width must be even");
+        DeviceBuffer dw(experts * width * 2), dx(tokens * width * 2), dl(tokens * experts * 2);
+        DeviceBuffer dids(tokens * top_k * 4), dsc(tokens * top_k * 2), derr(4);
+        upload(dw.ptr, weight, experts * width * 2, nullptr);
+        upload(dx.ptr, hidden, tokens * width * 2, nullptr);
+        check(hipMemsetAsync(derr.ptr, 0, 4, nullptr), "hipMemsetAsync");
+        // up to 4 tokens per launch share each weight read; x stays <= 64 KiB of LDS
+        const size_t per_launch = std::max<size_t>(1, std::min<size_t>(4, 16384 / width));
+        if (order == FIREWING_HIP_LOGITS_TREE32) {
+            for (size_t t0 = 0; t0 < tokens; t0 += per_launch) {
+                int T = (int)std::min<size_t>(per_launch, tokens - t0);
+                launch_linear(dw.as<uint16_t>(), dx.as<uint16_t>() + t0 * width, (int)experts,
+                              (int)width, T, dl.as<uint16_t>() + t0 * experts, nullptr);
+            }
+        } else {
+            for (size_t t0 = 0; t0 < tokens; t0 += per_launch) {
+                int T = (int)std::min<size_t>(per_launch, tokens - t0);
+                size_t shmem = (size_t)T * width * 4;
+                hipLaunchKernelGGL(k_linear_fold, dim3((unsigned)((experts + 63) / 64)), dim3(64),
+                                   shmem, nullptr, dw.as<uint16_t>(), dx.as<uint16_t>() + t0 * width,
+                                   (int)experts, (int)width, T, dl.as<uint16_t>() + t0 * experts);
+                check(hipGetLastError(), "k_linear_fold launch");
+            }
+        }
+        // k_linear_* write token-major [T][rows]: already [tokens][experts]
+        hipLaunchKernelGGL(k_select, dim3((unsigned)tokens), dim3(64), 0, nullptr,
+                           dl.as<uint16_t>(), (int)experts, (int)top_k, dids.as<int32_t>(),
+                           dsc.as<uint16_t>(), order == FIREWING_HIP_LOGITS_TREE32 ? 1 : 0,
+                           derr.as<int32_t>());
+        check(hipGetLastError(), "k_select launch");
+        std::vector<int32_t> hid(tokens * top_k);
+        int32_t err = 0;
+        download(hid.data(), dids.ptr, hid.size() * 4, nullptr);
+        download(scores, dsc.ptr, tokens * top_k * 2, nullptr);
+        if (logits) download(logits, dl.ptr, tokens * experts * 2, nullptr);
+        download(&err, derr.ptr, 4, nullptr);
+        check(hipStreamSynchronize(nullptr), "hipStreamSynchronize");
+        if (err == 2) return fail("decoder-layer router received unsupported logits (NaN)");
+        for (size_t i = 0; i < hid.size(); ++i) ids[i] = (size_t)hid[i];
+        return true;
+    });
+}
+
+bool firewing_hip_expert_bf16(const uint16_t* gate_up_weight, const uint16_t* down_weight,
+                              const uint16_t* hidden, size_t hidden_size,
+                              size_t intermediate, uint16_t route_weight,
+                              uint16_t* gate_up, uint16_t* swiglu, uint16_t* down,
+                              uint16_t* weighted) {
+    return guarded([&] {
+        if (!gate_up_weight || !down_weight || !hidden) return fail("expert_bf16: null pointer");
+        std::string why;
+        if (!shape_ok_for_linear(2 * intermediate, hidden_size, &why)) return fail(why);
+        if (!shape_ok_for_linear(hidden_size, intermediate, &why)) return fail(why);
+        if (hidden_size % 2 || intermediate % 2) return fail("expert_bf16: sizes must be even");
+        const size_t H = hidden_size, I = intermediate;
+        DeviceBuffer dgu(2 * I * H * 2), ddn(H * I * 2), dx(H * 2), dgo(2 * I * 2), dact(I * 2);
+        DeviceBuffer ddo(H * 2), dwo(H * 2);
+        upload(dgu.ptr, gate_up_weight, 2 * I * H * 2, nullptr);
+        upload(ddn.ptr, down_weight, H * I * 2, nullptr);
+        upload(dx.ptr, hidden, H * 2, nullptr);
+        launch_linear(dgu.as<uint16_t>(), dx.as<uint16_t>(), (int)(2 * I), (int)H, 1,
+                      dgo.as<uint16_t>(), nullptr);
+        hipLaunchKernelGGL(k_swiglu, dim3((unsigned)((I + 255) / 256)), dim3(256), 0, nullptr,
+                           dgo.as<uint16_t>(), dgo.as<uint16_t>() + I, I, dact.as<uint16_t>());
+        check(hipGetLastError(), "k_swiglu launch");
+        launch_linear(ddn.as<uint16_t>(), dact.as<uint16_t>(), (int)H, (int)I, 1,
+                      ddo.as<uint16_t>(), nullptr);
+        hipLaunchKernelGGL(k_scale_bf16, dim3((unsigned)((H + 255) / 256)), dim3(256), 0, nullptr,
+                           ddo.as<uint16_t>(), route_weight, H, dwo.as<uint16_t>());
+        check(hipGetLastError(), "k_scale_bf16 launch");
+        if (gate_up) download(gate_up, dgo.ptr, 2 * I * 2, nullptr);
+        if (swiglu) download(swiglu, dact.ptr, I * 2, nullptr);
+        if (down) download(down, ddo.ptr, H * 2, nullptr);
+        if (weighted) download(weighted, dwo.ptr, H * 2, nullptr);
+        check(hipStreamSynchronize(nullptr), "hipStreamSynchronize");
+        return true;
+    });
+}
+
+bool firewing_hip_create(const firewing_hip_shape* shape, firewing_hip_context** out) {
+    if (out) *out = nullptr;
+    firewing_hip_context* c = nullptr;
+    bool ok = guarded([&] {
+        if (!shape || !out) return fail("create: null pointer");
+        std::string why;
+        if (!validate_shape(*shape, &why)) return fail(why);
+        c = new firewing_hip_context();
+        c->shape = *shape;
+        check(hipGetDevice(&c->device), "hipGetDevice");
+        hipDeviceProp_t prop;
+        check(hipGetDeviceProperties(&prop, c->device), "hipGetDeviceProperties");
+        std::snprintf(c->device_name, sizeof c->device_name, "%s (%s)", prop.name, prop.gcnArchName);
+        c->cu_count = prop.multiProcessorCount;
+        int wall_khz = 0;
+        if (hipDeviceGetAttribute(&wall_khz, hipDeviceAttributeWallClockRate, c->device) == hipSuccess &&
+            wall_khz >= 1000 && wall_khz <= 10000000)
+            c->wall_clock_hz = (uint64_t)wall_khz * 1000ULL;
+        if (!prop.cooperativeLaunch) return fail("device does not support cooperative launch");
+        if (const char* env = std::getenv("FIREWING_WAIT_TIMEOUT_S")) {
+            double v = std::atof(env);
+            if (v > 0.0 && v <= 600.0) c->timeout_seconds = v;
+        }
+        check(hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking), "hipStreamCreate");
+        const size_t L = shape->layers, H = shape->hidden, I = shape->intermediate;
+        const size_t E = shape->experts, Is = shape->shared_intermediate, K = shape->top_k;
+        c->router.assign(L, nullptr);
+        c->gate_up.assign(L, nullptr);
+        c->down.assign(L, nullptr);
+        c->shared_gate.assign(L, nullptr);
+        c->shared_up.assign(L, nullptr);
+        c->shared_down.assign(L, nullptr);
+        std::vector<DecodeLayer> layers(L);
+        for (size_t l = 0; l < L; ++l) {
+            c->router[l] = dalloc<uint16_t>((E + 1) * H);
+            c->gate_up[l] = dalloc<uint16_t>(E * 2 * I * H);
+            c->down[l] = dalloc<uint16_t>(E * H * I);
+            c->shared_gate[l] = dalloc<uint16_t>(Is * H);
+            c->shared_up[l] = dalloc<uint16_t>(Is * H);
+            c->shared_down[l] = dalloc<uint16_t>(H * Is);
+            layers[l] = DecodeLayer{c->router[l], c->gate_up[l], c->down[l], c->shared_gate[l],
+                                    c->shared_up[l], c->shared_down[l]};
+        }
+        c->d_layers = dalloc<DecodeLayer>(L);
+        check(hipMemcpy(c->d_layers, layers.data(), L * sizeof(DecodeLayer), hipMemcpyHostToDevice),
+              "hipMemcpy layers");
+        const size_t T = kMaxTokens, S = K * T;
+        c->x = dalloc<uint16_t>((L + 1) * T * H);
+        c->out = dalloc<uint16_t>(L * T * H);
+        c->logits = dalloc<uint16_t>(L * T * (E + 1));
+        c->ids = dalloc<int32_t>(L * T * K);
+        c->scores = dalloc<uint16_t>(L * T * K);
+        c->slot_expert = dalloc<int32_t>(L * S);
+        c->slot_tokens = dalloc<uint32_t>(L * S);
+        c->union_count = dalloc<int32_t>(L);
+        c->token_slots = dalloc<int32_t>(L * T * K);
+        c->token_weights = dalloc<uint16_t>(L * T * K);
+        c->sig = dalloc<uint16_t>(L * T);
+        c->shared_act = dalloc<uint16_t>(L * T * Is);
+        c->act = dalloc<uint16_t>(L * S * T * I);
+        c->counters = dalloc<uint32_t>(L * kCountersPerLayer + 1);
+        c->error = dalloc<int32_t>(1);
+        check(hipMemset(c->counters, 0, (L * kCountersPerLayer + 1) * 4), "hipMemset counters");
+        check(hipMemset(c->error, 0, 4), "hipMemset error");
+        c->grid[1] = decode_grid<1>(c);
+        c->grid[2] = decode_grid<2>(c);
+        c->grid[3] = decode_grid<3>(c);
+        c->grid[4] = decode_grid<4>(c);
+        // zero the banks so uninstalled layers are defined
+        for (size_t l = 0; l < L; ++l) {
+            check(hipMemsetAsync(c->router[l], 0, (E + 1) * H * 2, c->stream), "hipMemsetAsync");
+        }
+        check(hipStreamSynchronize(c->stream), "hipStreamSynchronize");
+        *out = c;
+        return true;
+    });
+    if (!ok && c) {
+        std::string keep = g_last_error;
+        firewing_hip_destroy(c);
+        g_last_error = keep;
+    }
+    return ok;
+}
+
+void firewing_hip_destroy(firewing_hip_context* c) {
+    if (!c) return;
+    if (c->stream) (void)hipStreamSynchronize(c->stream);
+    auto freev = [](std::vector<uint16_t*>& v) {
+        for (auto* p : v)
+            if (p) (void)hipFree(p);
+        v.clear();
+    };
+    freev(c->router);
+    freev(c->gate_up);
+    freev(c->down);
+    freev(c->shared_gate);
+    freev(c->shared_up);
+    freev(c->shared_down);
+    void* bufs[] = {c->d_layers, c->d_weight_table, c->x, c->out, c->logits, c->ids, c->scores,
+                    c->slot_expert, c->slot_tokens, c->union_count, c->token_slots,
+                    c->token_weights, c->sig, c->shared_act, c->act, c->counters, c->error};
+    for (void* b : bufs)
+        if (b) (void)hipFree(b);
+    if (c->stream) (void)hipStreamDestroy(c->stream);
+    delete c;
+}
+
+const char* firewing_hip_device_name(const firewing_hip_context* c) {
+    return c ? c->device_name : "";
+}
+
+bool firewing_hip_install_layer(firewing_hip_context* c, size_t layer, const uint16_t* router,
+                                const uint16_t* gate_up, const uint16_t* down,
+                                const uint16_t* shared_gate, const uint16_t* shared_up,
+                                const uint16_t* shared_down, const uint16_t* shared_expert_gate) {
+    return guarded([&] {
+        if (!c) return fail("install_layer: null context");
+        if (layer >= c->shape.layers) return fail("install_layer: layer out of range");
+        if (!router || !gate_up || !down || !shared_gate || !shared_up || !shared_down ||
+            !shared_expert_gate)
+            return fail("install_layer: null tensor");
+        const size_t H = c->shape.hidden, I = c->shape.intermediate, E = c->shape.experts;
+        const size_t Is = c->shape.shared_intermediate;
+        hipStream_t s = c->stream;
+        upload(c->router[layer], router, E * H * 2, s);
+        upload(c->router[layer] + E * H, shared_expert_gate, H * 2, s);
+        upload(c->gate_up[layer], gate_up, E * 2 * I * H * 2, s);
+        upload(c->down[layer], down, E * H * I * 2, s);
+        upload(c->shared_gate[layer], shared_gate, Is * H * 2, s);
+        upload(c->shared_up[layer], shared_up, Is * H * 2, s);
+        upload(c->shared_down[layer], shared_down, H * Is * 2, s);
+        check(hipStreamSynchronize(s), "hipStreamSynchronize");
+        return true;
+    });
+}
+
+bool firewing_hip_generate_layers(firewing_hip_context* c, size_t first, size_t count,
+                                  uint64_t seed, bool bias_feature) {
+    return guarded([&] {
+        if (!c) return fail("generate_layers: null context");
+        if (first > c->shape.layers || count > c->shape.layers - first)
+            return fail("generate_layers: layer range out of bounds");
+        const size_t H = c->shape.hidden, I = c->shape.intermediate, E = c->shape.experts;
+        const size_t Is = c->shape.shared_intermediate;
+        hipStream_t s = c->stream;
+        if (!c->d_weight_table) {
+            std::vector<uint16_t> table(65536);
+            fw_synth_normal_table(FW_SYNTH_WEIGHT_SIGMA, table.data());
+            c->d_weight_table = dalloc<uint16_t>(65536);
+            check(hipMemcpy(c->d_weight_table, table.data(), 65536 * 2, hipMemcpyHostToDevice),
+                  "hipMemcpy table");
+        }
+        auto gen = [&](uint16_t* dst, size_t n, uint32_t layer, uint32_t tensor) {
+            uint64_t stream = fw_synth_stream(seed, layer, tensor);
+            size_t quads = (n + 3) / 4;
+            const size_t chunk = (size_t)1 << 28;  // quads per launch
+            for (size_t q0 = 0; q0 < quads; q0 += chunk) {
+                size_t nq = std::min(chunk, quads - q0);
+                size_t e0 = q0 * 4;
+                size_t ne = std::min(n - e0, nq * 4);
+                hipLaunchKernelGGL(k_generate, dim3((unsigned)((nq + 255) / 256)), dim3(256), 0, s,
+                                   dst + e0, ne, stream, (uint64_t)e0, c->d_weight_table);
+                check(hipGetLastError(), "k_generate launch");
+            }
+        };
+        std::vector<uint16_t> bias(E);
+        std::vector<uint32_t> rank(E);
+        DeviceBuffer dbias(E * 2);
+        for (size_t l = first; l < first + count; ++l) {
+            const uint32_t li = (uint32_t)l;
+            gen(c->router[l], E * H, li, FW_SYNTH_ROUTER);
+            gen(c->router[l] + E * H, H, li, FW_SYNTH_SHARED_EXPERT_GATE);
+            gen(c->gate_up[l], E * 2 * I * H, li, FW_SYNTH_GATE_UP);
+            gen(c->down[l], E * H * I, li, FW_SYNTH_DOWN);
+            gen(c->shared_gate[l], Is * H, li, FW_SYNTH_SHARED_GATE);
+            gen(c->shared_up[l], Is * H, li, FW_SYNTH_SHARED_UP);
+            gen(c->shared_down[l], H * Is, li, FW_SYNTH_SHARED_DOWN);
+            if (bias_feature) {
+                fw_synth_router_bias(seed, li, (uint32_t)E, FW_SYNTH_ZIPF_BIAS_SLOPE, rank.data(),
+                                     bias.data());
+                check(hipMemcpyAsync(dbias.ptr, bias.data(), E * 2, hipMemcpyHostToDevice, s),
+                      "hipMemcpyAsync bias");
+                hipLaunchKernelGGL(k_router_bias, dim3((unsigned)((E + 255) / 256)), dim3(256), 0, s,
+                                   c->router[l], (int)E, (int)H, dbias.as<uint16_t>());
+                check(hipGetLastError(), "k_router_bias launch");
+                check(hipStreamSynchronize(s), "hipStreamSynchronize");
+            }
+        }
+        check(hipStreamSynchronize(s), "hipStreamSynchronize");
+        return true;
+    });
+}
+
+bool firewing_hip_read_tensor(firewing_hip_context* c, size_t layer, int tensor, size_t first,
+                              size_t count, uint16_t* out) {
+    return guarded([&] {
+        if (!c || !out) return fail("read_tensor: null pointer");
+        if (layer >= c->shape.layers) return fail("read_tensor: layer out of range");
+        const size_t H = c->shape.hidden, I = c->shape.intermediate, E = c->shape.experts;
+        const size_t Is = c->shape.shared_intermediate;
+        const uint16_t* base = nullptr;
+        size_t n = 0;
+        switch (tensor) {
+            case FW_SYNTH_ROUTER: base = c->router[layer]; n = E * H; break;
+            case FW_SYNTH_GATE_UP: base = c->gate_up[layer]; n = E * 2 * I * H; break;
+            case FW_SYNTH_DOWN: base = c->down[layer]; n = E * H * I; break;
+            case FW_SYNTH_SHARED_GATE: base = c->shared_gate[layer]; n = Is * H; break;
+            case FW_SYNTH_SHARED_UP: base = c->shared_up[layer]; n = Is * H; break;
+            case FW_SYNTH_SHARED_DOWN: base = c->shared_down[layer]; n = H * Is; break;
+            case FW_SYNTH_SHARED_EXPERT_GATE: base = c->router[layer] + E * H; n = H; break;
+            default: return fail("read_tensor: unknown tensor id");
+        }
+        if (first > n || count > n - first) return fail("read_tensor: range out of bounds");
+        download(out, base + first, count * 2, c->stream);
+        check(hipStreamSynchronize(c->stream), "hipStreamSynchronize");
+        return true;
+    });
+}
+
+bool firewing_hip_route(firewing_hip_context* c, size_t layer, const uint16_t* hidden,
+                        size_t tokens, int order, size_t* ids, uint16_t* scores,
+                        uint16_t* logits) {
+    return guarded([&] {
+        if (!c || !hidden || !ids || !scores) return fail("route: null pointer");
+        if (layer >= c->shape.layers) return fail("route: layer out of range");
+        if (tokens == 0 || tokens > 4096) return fail("route: tokens must be in [1, 4096]");
+        if (order != FIREWING_HIP_LOGITS_TREE32 && order != FIREWING_HIP_LOGITS_FOLD)
+            return fail("route: unknown logit order");
+        const size_t H = c->shape.hidden, E = c->shape.experts, K = c->shape.top_k;
+        hipStream_t s = c->stream;
+        DeviceBuffer dx(tokens * H * 2), dl(tokens * E * 2), dids(tokens * K * 4),
+            dsc(tokens * K * 2), derr(4);
+        upload(dx.ptr, hidden, tokens * H * 2, s);
+        check(hipMemsetAsync(derr.ptr, 0, 4, s), "hipMemsetAsync");
+        for (size_t t0 = 0; t0 < tokens; t0 += 4) {
+            int T = (int)std::min<size_t>(4, tokens - t0);  // H <= 2560: <= 40 KiB of LDS
+            if (order == FIREWING_HIP_LOGITS_TREE32) {
+                launch_linear(c->router[layer], dx.as<uint16_t>() + t0 * H, (int)E, (int)H, T,
+                              dl.as<uint16_t>() + t0 * E, s);
+            } else {
+                hipLaunchKernelGGL(k_linear_fold, dim3((unsigned)((E + 63) / 64)), dim3(64),
+                                   (size_t)T * H * 4, s, c->router[layer],
+                                   dx.as<uint16_t>() + t0 * H, (int)E, (int)H, T,
+                                   dl.as<uint16_t>() + t0 * E);
+                check(hipGetLastError(), "k_linear_fold launch");
+            }
+        }
+        hipLaunchKernelGGL(k_select, dim3((unsigned)tokens), dim3(64), 0, s, dl.as<uint16_t>(),
+                           (int)E, (int)K, dids.as<int32_t>(), dsc.as<uint16_t>(),
+                           order == FIREWING_HIP_LOGITS_TREE32 ? 1 : 0, derr.as<int32_t>());
+        check(hipGetLastError(), "k_select launch");
+        std::vector<int32_t> hid(tokens * K);
+        int32_t err = 0;
+        download(hid.data(), dids.ptr, hid.size() * 4, s);
+        download(scores, dsc.ptr, tokens * K * 2, s);
+        if (logits) download(logits, dl.ptr, tokens * E * 2, s);
+        download(&err, derr.ptr, 4, s);
+        check(hipStreamSynchronize(s), "hipStreamSynchronize");
+        if (err == 2) return fail("decoder-layer router received unsupported logits (NaN)");
+        for (size_t i = 0; i < hid.size(); ++i) ids[i] = (size_t)hid[i];
+        return true;
+    });
+}
+
+bool firewing_hip_mixture_bf16(firewing_hip_context* c, size_t layer, const uint16_t* hidden,
+                               const size_t* experts, const uint16_t* route_weights,
+                               size_t count, uint16_t* mixture) {
+    return guarded([&] {
+        if (!c || !hidden || !experts || !route_weights || !mixture) return fail("mixture: null pointer");
+        if (layer >= c->shape.layers) return fail("mixture: layer out of range");
+        if (count == 0 || count > 64) return fail("mixture: count must be in [1, 64]");
+        const size_t H = c->shape.hidden, I = c->shape.intermediate, E = c->shape.experts;
+        for (size_t i = 0; i < count; ++i) {
+            if (experts[i] >= E) return fail("mixture: expert index is out of range");
+        }
+        hipStream_t s = c->stream;
+        DeviceBuffer dx(H * 2), dgo(2 * I * 2), dact(I * 2), ddo(H * 2), dw(count * H * 2), dmix(H * 2);
+        upload(dx.ptr, hidden, H * 2, s);
+        for (size_t i = 0; i < count; ++i) {
+            const uint16_t* gu = c->gate_up[layer] + experts[i] * 2 * I * H;
+            const uint16_t* dn = c->down[layer] + experts[i] * H * I;
+            launch_linear(gu, dx.as<uint16_t>(), (int)(2 * I), (int)H, 1, dgo.as<uint16_t>(), s);
+            hipLaunchKernelGGL(k_swiglu, dim3((unsigned)((I + 255) / 256)), dim3(256), 0, s,
+                               dgo.as<uint16_t>(), dgo.as<uint16_t>() + I, I, dact.as<uint16_t>());
+            check(hipGetLastError(), "k_swiglu launch");
+            launch_linear(dn, dact.as<uint16_t>(), (int)H, (int)I, 1, ddo.as<uint16_t>(), s);
+            hipLaunchKernelGGL(k_scale_bf16, dim3((unsigned)((H + 255) / 256)), dim3(256), 0, s,
+                               ddo.as<uint16_t>(), route_weights[i], H, dw.as<uint16_t>() + i * H);
+            check(hipGetLastError(), "k_scale_bf16 launch");
+        }
+        hipLaunchKernelGGL(k_mixture, dim3((unsigned)((H + 255) / 256)), dim3(256), 0, s,
+                           dw.as<uint16_t>(), (int)count, (int)H, dmix.as<uint16_t>());
+        check(hipGetLastError(), "k_mixture launch");
+        download(mixture, dmix.ptr, H * 2, s);
+        check(hipStreamSynchronize(s), "hipStreamSynchronize");
+        return true;
+    });
+}
+
+static bool step_args_ok(firewing_hip_context* c, size_t tokens, int order, std::string* why) {
+    if (!c) {
+        *why = "null context";
+        return false;
+    }
+    if (tokens == 0 || tokens > (size_t)kMaxTokens) {
+        *why = "tokens must be in [1, 4] (decode and MTP verify)";
+        return false;
+    }
+    if (order != FIREWING_HIP_LOGITS_TREE32 && order != FIREWING_HIP_LOGITS_FOLD) {
+        *why = "unknown logit order";
+        return false;
+    }
+    return true;
+}
+
+bool firewing_hip_sparse_moe_block_dev(firewing_hip_context* c, size_t layer,
+                                       const uint16_t* hidden, size_t tokens, int order,
+                                       uint16_t* out, void* stream) {
+    return guarded([&] {
+        std::string why;
+        if (!step_args_ok(c, tokens, order, &why)) return fail("sparse_moe_block: " + why);
+        if (!hidden || !out) return fail("sparse_moe_block: null pointer");
+        if (layer >= c->shape.layers) return fail("sparse_moe_block: layer out of range");
+        hipStream_t s = stream ? static_cast<hipStream_t>(stream) : c->stream;
+        const size_t H = c->shape.hidden;
+        launch_decode(c, layer, 1, (int)tokens, order, false, hidden, nullptr, s);
+        check(hipMemcpyAsync(out, c->out, tokens * H * 2, hipMemcpyDeviceToDevice, s), "copy output");
+        return true;
+    });
+}
+
+bool firewing_hip_sparse_moe_block(firewing_hip_context* c, size_t layer,
+                                   const uint16_t* hidden, size_t tokens, int order,
+                                   uint16_t* out, firewing_hip_block_captures* cap) {
+    return guarded([&] {
+        std::string why;
+        if (!step_args_ok(c, tokens, order, &why)) return fail("sparse_moe_block: " + why);
+        if (!hidden || !out) return fail("sparse_moe_block: null pointer");
+        if (layer >= c->shape.layers) return fail("sparse_moe_block: layer out of range");
+        hipStream_t s = c->stream;
+        const size_t H = c->shape.hidden, E = c->shape.experts, K = c->shape.top_k;
+        upload(c->x, hidden, tokens * H * 2, s);
+        launch_decode(c, layer, 1, (int)tokens, order, false, c->x, nullptr, s);
+        if (!check_device_error(c, s)) return false;
+        download(out, c->out, tokens * H * 2, s);
+        if (cap) {
+            if (cap->router_logits) {
+                for (size_t t = 0; t < tokens; ++t)
+                    download(cap->router_logits + t * E, c->logits + t * (E + 1), E * 2, s);
+            }
+            if (cap->selected_experts) {
+                std::vector<int32_t> ids(tokens * K);
+                download(ids.data(), c->ids, ids.size() * 4, s);
+                check(hipStreamSynchronize(s), "hipStreamSynchronize");
+                for (size_t i = 0; i < ids.size(); ++i) cap->selected_experts[i] = (size_t)ids[i];
+            }
+            if (cap->selected_scores) download(cap->selected_scores, c->scores, tokens * K * 2, s);
+            if (cap->shared_gate_sigmoid) download(cap->shared_gate_sigmoid, c->sig, tokens * 2, s);
+            if (cap->routed_mixture) return fail("sparse_moe_block: routed_mixture capture is not kept by the fused kernel");
+        }
+        check(hipStreamSynchronize(s), "hipStreamSynchronize");
+        return true;
+    });
+}
+
+bool firewing_hip_moe_step_dev(firewing_hip_context* c, const uint16_t* hidden, size_t tokens,
+                               int order, bool bias_feature, uint16_t* residual,
+                               uint16_t* block_out, int32_t* ids, uint16_t* scores,
+                               void* stream) {
+    return guarded([&] {
+        std::string why;
+        if (!step_args_ok(c, tokens, order, &why)) return fail("moe_step: " + why);
+        if (!hidden || !residual) return fail("moe_step: null pointer");
+        hipStream_t s = stream ? static_cast<hipStream_t>(stream) : c->stream;
+        const size_t L = c->shape.layers, H = c->shape.hidden, K = c->shape.top_k;
+        launch_decode(c, 0, L, (int)tokens, order, bias_feature, hidden, residual, s);
+        if (block_out)
+            check(hipMemcpyAsync(block_out, c->out, L * tokens * H * 2, hipMemcpyDeviceToDevice, s),
+                  "copy block outputs");
+        if (ids)
+            check(hipMemcpyAsync(ids, c->ids, L * tokens * K * 4, hipMemcpyDeviceToDevice, s), "copy ids");
+        if (scores)
+            check(hipMemcpyAsync(scores, c->scores, L * tokens * K * 2, hipMemcpyDeviceToDevice, s),
+                  "copy scores");
+        return true;
+    });
+}
+
+bool firewing_hip_moe_step(firewing_hip_context* c, const uint16_t* hidden, size_t tokens,
+                           int order, bool bias_feature, uint16_t* residual,
+                           uint16_t* block_out, int32_t* ids, uint16_t* scores) {
+    return guarded([&] {
+        std::string why;
+        if (!step_args_ok(c, tokens, order, &why)) return fail("moe_step: " + why);
+        if (!hidden || !residual) return fail("moe_step: null pointer");
+        hipStream_t s = c->stream;
+        const size_t L = c->shape.layers, H = c->shape.hidden, K = c->shape.top_k;
+        upload(c->x, hidden, tokens * H * 2, s);
+        launch_decode(c, 0, L, (int)tokens, order, bias_feature, c->x, nullptr, s);
+        if (!check_device_error(c, s)) return false;
+        download(residual, c->x + L * tokens * H, tokens * H * 2, s);
+        if (block_out) download(block_out, c->out, L * tokens * H * 2, s);
+        if (ids) download(ids, c->ids, L * tokens * K * 4, s);
+        if (scores) download(scores, c->scores, L * tokens * K * 2, s);
+        check(hipStreamSynchronize(s), "hipStreamSynchronize");
+        return true;
+    });
+}
+
+bool firewing_hip_synchronize(firewing_hip_context* c) {
+    return guarded([&] {
+        if (!c) return fail("synchronize: null context");
+        return check_device_error(c, c->stream);
+    });
+}
+
+}  // extern "C"

@@ -74,7 +74,7 @@ FW_SYNTH_HD uint16_t fw_synth_round_bf16(uint32_t bits) {
     return (uint16_t)((bits + 0x7fffu + ((bits >> 16) & 1u)) >> 16);
 }
 
-#if !defined(__HIP_DEVICE_COMPILE__)
+/* Host-only helpers (plain static functions: never called from device code). */
 #include <math.h>
 #include <string.h>
 
@@ -190,7 +190,6 @@ static inline void fw_synth_hidden(uint64_t seed, uint32_t first_token, uint32_t
         if (bias_feature) row[hidden - 1] = 0x3f80u;
     }
 }
-#endif /* !__HIP_DEVICE_COMPILE__ */
 
 /* One synthetic weight element: table[u16(stream, index)]. */
 FW_SYNTH_HD uint16_t fw_synth_weight(const uint16_t* table, uint64_t stream, uint64_t index) {

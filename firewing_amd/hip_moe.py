@@ -1,0 +1,343 @@
+"""Host-side mirror of the reference crate's MoE entry points over libfirewing_hip_moe.so.
+
+Names and argument meanings follow the Rust functions they replace:
+
+    linear_bf16(weight, input, rows, columns)        src/expert.rs:554-560
+    swiglu_bf16(gate, up)                            src/expert.rs:562-571
+    sigmoid_bf16(values)                             src/expert.rs:573-576
+    topk_bf16(values, k)                             native/topk_shim.cpp:18-44
+    route(weight, hidden, experts, width, top_k)     src/router.rs:220-265
+    expert_bf16(gate_up, down, hidden, ...)          src/expert.rs:717-751
+    MoeContext.install_layer / mixture / sparse_moe_block / moe_step
+                                                     src/metal_moe.rs:95-447,
+                                                     src/decoder_layer.rs:460-586
+
+Errors come back as ``FirewingError`` carrying the library's message, as the
+Rust wrappers map ``false`` to ``Err(String)`` (src/decoder_layer.rs:28-39).
+bf16 values are numpy ``uint16`` bit patterns; ``*_dev`` methods take device
+addresses (ints or torch tensors on the GPU).
+
+Importing this module loads the HIP library and fails loudly if it is absent:
+there is no CPU fallback.
+"""
+from __future__ import annotations
+
+import ctypes
+from pathlib import Path
+
+import numpy as np
+
+PKG = Path(__file__).resolve().parent
+LIB_PATH = PKG / "libfirewing_hip_moe.so"
+HEADER = PKG.parent / "include" / "firewing_hip_moe.h"
+
+LOGITS_TREE32 = 0
+LOGITS_FOLD = 1
+
+# tensor ids of firewing_hip_read_tensor (fw_synth.h)
+ROUTER, GATE_UP, DOWN, SHARED_GATE, SHARED_UP, SHARED_DOWN, SHARED_EXPERT_GATE = range(1, 8)
+
+
+class FirewingError(RuntimeError):
+    pass
+
+
+class Shape(ctypes.Structure):
+    _fields_ = [("hidden", ctypes.c_size_t), ("intermediate", ctypes.c_size_t),
+                ("experts", ctypes.c_size_t), ("top_k", ctypes.c_size_t),
+                ("shared_intermediate", ctypes.c_size_t), ("layers", ctypes.c_size_t)]
+
+
+class BlockCaptures(ctypes.Structure):
+    _fields_ = [("router_logits", ctypes.c_void_p), ("selected_experts", ctypes.c_void_p),
+                ("selected_scores", ctypes.c_void_p), ("routed_mixture", ctypes.c_void_p),
+                ("shared_gate_sigmoid", ctypes.c_void_p)]
+
+
+_u16p = ctypes.POINTER(ctypes.c_uint16)
+_szp = ctypes.POINTER(ctypes.c_size_t)
+_vp = ctypes.c_void_p
+_sz = ctypes.c_size_t
+_b = ctypes.c_bool
+
+_SIGNATURES = {
+    "firewing_hip_last_error": (ctypes.c_char_p, []),
+    "firewing_hip_linear_bf16": (_b, [_u16p, _u16p, _sz, _sz, _u16p]),
+    "firewing_hip_swiglu_bf16": (_b, [_u16p, _u16p, _sz, _u16p]),
+    "firewing_hip_sigmoid_bf16": (_b, [_u16p, _sz, _u16p]),
+    "firewing_hip_topk_bf16": (_b, [_u16p, _sz, _sz, _szp]),
+    "firewing_hip_route_bf16": (_b, [_u16p, _u16p, _sz, _sz, _sz, _sz, ctypes.c_int, _szp, _u16p, _u16p]),
+    "firewing_hip_expert_bf16": (_b, [_u16p, _u16p, _u16p, _sz, _sz, ctypes.c_uint16, _u16p, _u16p,
+                                      _u16p, _u16p]),
+    "firewing_hip_create": (_b, [ctypes.POINTER(Shape), ctypes.POINTER(_vp)]),
+    "firewing_hip_destroy": (None, [_vp]),
+    "firewing_hip_device_name": (ctypes.c_char_p, [_vp]),
+    "firewing_hip_install_layer": (_b, [_vp, _sz, _u16p, _u16p, _u16p, _u16p, _u16p, _u16p, _u16p]),
+    "firewing_hip_generate_layers": (_b, [_vp, _sz, _sz, ctypes.c_uint64, _b]),
+    "firewing_hip_read_tensor": (_b, [_vp, _sz, ctypes.c_int, _sz, _sz, _u16p]),
+    "firewing_hip_route": (_b, [_vp, _sz, _u16p, _sz, ctypes.c_int, _szp, _u16p, _u16p]),
+    "firewing_hip_mixture_bf16": (_b, [_vp, _sz, _u16p, _szp, _u16p, _sz, _u16p]),
+    "firewing_hip_sparse_moe_block": (_b, [_vp, _sz, _u16p, _sz, ctypes.c_int, _u16p,
+                                           ctypes.POINTER(BlockCaptures)]),
+    "firewing_hip_sparse_moe_block_dev": (_b, [_vp, _sz, _vp, _sz, ctypes.c_int, _vp, _vp]),
+    "firewing_hip_moe_step_dev": (_b, [_vp, _vp, _sz, ctypes.c_int, _b, _vp, _vp, _vp, _vp, _vp]),
+    "firewing_hip_moe_step": (_b, [_vp, _u16p, _sz, ctypes.c_int, _b, _u16p, _u16p, _vp, _u16p]),
+    "firewing_hip_synchronize": (_b, [_vp]),
+    "firewing_hip_synth_hidden": (None, [ctypes.c_uint64, ctypes.c_uint32, ctypes.c_uint32,
+                                         ctypes.c_uint32, _b, _u16p]),
+    "firewing_hip_expf_host": (None, [ctypes.POINTER(ctypes.c_float), ctypes.POINTER(ctypes.c_float), _sz]),
+    "firewing_hip_expf_device": (_b, [ctypes.POINTER(ctypes.c_float), ctypes.POINTER(ctypes.c_float), _sz]),
+}
+
+_lib = None
+
+
+def lib() -> ctypes.CDLL:
+    """Load the HIP library (built by firewing_amd.build)."""
+    global _lib
+    if _lib is None:
+        if not LIB_PATH.is_file():
+            raise FirewingError(
+                f"{LIB_PATH} is missing: build it with `python -m firewing_amd.build` "
+                "(there is no CPU fallback)")
+        L = ctypes.CDLL(str(LIB_PATH))
+        for name, (res, args) in _SIGNATURES.items():
+            fn = getattr(L, name)
+            fn.restype = res
+            fn.argtypes = args
+        _lib = L
+    return _lib
+
+
+def _err() -> FirewingError:
+    msg = lib().firewing_hip_last_error()
+    return FirewingError(msg.decode() if msg else "unknown failure")
+
+
+def _call(name: str, *args) -> None:
+    if not getattr(lib(), name)(*args):
+        raise _err()
+
+
+def _u16(a) -> np.ndarray:
+    return np.ascontiguousarray(a, dtype=np.uint16)
+
+
+def _p16(a: np.ndarray):
+    return a.ctypes.data_as(_u16p)
+
+
+def _pf(a: np.ndarray):
+    return a.ctypes.data_as(ctypes.POINTER(ctypes.c_float))
+
+
+def _addr(x) -> int | None:
+    if x is None:
+        return None
+    if hasattr(x, "data_ptr"):
+        return int(x.data_ptr())
+    return int(x)
+
+
+# ---- stateless entry points ------------------------------------------------------------
+
+def linear_bf16(weight, hidden, rows: int, columns: int) -> np.ndarray:
+    w, x = _u16(weight), _u16(hidden)
+    if w.size != rows * columns or x.size != columns:
+        raise FirewingError("linear_bf16: weight must be [rows, columns] and input [columns]")
+    out = np.empty(rows, dtype=np.uint16)
+    _call("firewing_hip_linear_bf16", _p16(w), _p16(x), rows, columns, _p16(out))
+    return out
+
+
+def swiglu_bf16(gate, up) -> np.ndarray:
+    g, u = _u16(gate), _u16(up)
+    if g.size != u.size:
+        raise FirewingError("swiglu_bf16: gate and up differ in length")
+    out = np.empty(g.size, dtype=np.uint16)
+    _call("firewing_hip_swiglu_bf16", _p16(g), _p16(u), g.size, _p16(out))
+    return out
+
+
+def sigmoid_bf16(values) -> np.ndarray:
+    v = _u16(values)
+    out = np.empty(v.size, dtype=np.uint16)
+    _call("firewing_hip_sigmoid_bf16", _p16(v), v.size, _p16(out))
+    return out
+
+
+def topk_bf16(values, k: int) -> np.ndarray:
+    v = _u16(values)
+    out = (ctypes.c_size_t * max(k, 1))()
+    _call("firewing_hip_topk_bf16", _p16(v), v.size, k, out)
+    return np.array(list(out)[:k], dtype=np.int64)
+
+
+def route(weight, hidden, experts: int, width: int, top_k: int, order: int = LOGITS_TREE32):
+    """(ids [T, K], scores [T, K] bf16, logits [T, E] bf16) for hidden [T, H] or [H]."""
+    w = _u16(weight)
+    x = _u16(hidden)
+    tokens = x.size // width
+    if x.size != tokens * width or w.size != experts * width:
+        raise FirewingError("route: weight must be [experts, width] and hidden [tokens, width]")
+    ids = (ctypes.c_size_t * (tokens * top_k))()
+    scores = np.empty((tokens, top_k), dtype=np.uint16)
+    logits = np.empty((tokens, experts), dtype=np.uint16)
+    _call("firewing_hip_route_bf16", _p16(w), _p16(x), tokens, experts, width, top_k, order, ids,
+          _p16(scores), _p16(logits))
+    return np.array(list(ids), dtype=np.int64).reshape(tokens, top_k), scores, logits
+
+
+def expert_bf16(gate_up_weight, down_weight, hidden, hidden_size: int, intermediate: int,
+                route_weight: int) -> dict:
+    gu, dn, x = _u16(gate_up_weight), _u16(down_weight), _u16(hidden)
+    gate_up = np.empty(2 * intermediate, dtype=np.uint16)
+    swiglu = np.empty(intermediate, dtype=np.uint16)
+    down = np.empty(hidden_size, dtype=np.uint16)
+    weighted = np.empty(hidden_size, dtype=np.uint16)
+    _call("firewing_hip_expert_bf16", _p16(gu), _p16(dn), _p16(x), hidden_size, intermediate,
+          route_weight, _p16(gate_up), _p16(swiglu), _p16(down), _p16(weighted))
+    return {"gate_up": gate_up, "gate": gate_up[:intermediate], "up": gate_up[intermediate:],
+            "swiglu": swiglu, "down": down, "weighted_down": weighted}
+
+
+def synth_hidden(seed: int, tokens: int, hidden: int, bias_feature: bool = True,
+                 first_token: int = 0) -> np.ndarray:
+    """Seeded benchmark inputs [tokens, hidden] (bf16 bits)."""
+    out = np.empty((tokens, hidden), dtype=np.uint16)
+    lib().firewing_hip_synth_hidden(seed, first_token, tokens, hidden, bias_feature, _p16(out))
+    return out
+
+
+def expf_host(values) -> np.ndarray:
+    x = np.ascontiguousarray(values, dtype=np.float32)
+    out = np.empty_like(x)
+    lib().firewing_hip_expf_host(_pf(x), _pf(out), x.size)
+    return out
+
+
+def expf_device(values) -> np.ndarray:
+    x = np.ascontiguousarray(values, dtype=np.float32)
+    out = np.empty_like(x)
+    _call("firewing_hip_expf_device", _pf(x), _pf(out), x.size)
+    return out
+
+
+# ---- resident context ------------------------------------------------------------------
+
+class MoeContext:
+    """Resident banks of `layers` sparse-MoE layers in HBM (metal_moe::Runtime)."""
+
+    def __init__(self, hidden: int, intermediate: int, experts: int, top_k: int,
+                 shared_intermediate: int, layers: int):
+        self.shape = Shape(hidden, intermediate, experts, top_k, shared_intermediate, layers)
+        self.H, self.I, self.E, self.K = hidden, intermediate, experts, top_k
+        self.Is, self.L = shared_intermediate, layers
+        handle = ctypes.c_void_p()
+        _call("firewing_hip_create", ctypes.byref(self.shape), ctypes.byref(handle))
+        self._h = handle
+
+    def close(self) -> None:
+        if self._h:
+            lib().firewing_hip_destroy(self._h)
+            self._h = ctypes.c_void_p()
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    @property
+    def device_name(self) -> str:
+        return lib().firewing_hip_device_name(self._h).decode()
+
+    def install_layer(self, layer: int, router, gate_up, down, shared_gate, shared_up,
+                      shared_down, shared_expert_gate) -> None:
+        arrs = [_u16(a) for a in (router, gate_up, down, shared_gate, shared_up, shared_down,
+                                  shared_expert_gate)]
+        H, I, E, Is = self.H, self.I, self.E, self.Is
+        want = [E * H, E * 2 * I * H, E * H * I, Is * H, Is * H, H * Is, H]
+        if [a.size for a in arrs] != want:
+            raise FirewingError("install_layer: tensor sizes do not match the context shape")
+        _call("firewing_hip_install_layer", self._h, layer, *[_p16(a) for a in arrs])
+
+    def generate_layers(self, first: int, count: int, seed: int, bias_feature: bool = True) -> None:
+        _call("firewing_hip_generate_layers", self._h, first, count, seed, bias_feature)
+
+    def read_tensor(self, layer: int, tensor: int, first: int, count: int) -> np.ndarray:
+        out = np.empty(count, dtype=np.uint16)
+        _call("firewing_hip_read_tensor", self._h, layer, tensor, first, count, _p16(out))
+        return out
+
+    def route(self, layer: int, hidden, order: int = LOGITS_TREE32):
+        x = _u16(hidden).reshape(-1, self.H)
+        T = x.shape[0]
+        ids = (ctypes.c_size_t * (T * self.K))()
+        scores = np.empty((T, self.K), dtype=np.uint16)
+        logits = np.empty((T, self.E), dtype=np.uint16)
+        _call("firewing_hip_route", self._h, layer, _p16(x), T, order, ids, _p16(scores), _p16(logits))
+        return np.array(list(ids), dtype=np.int64).reshape(T, self.K), scores, logits
+
+    def mixture(self, layer: int, hidden, experts, route_weights) -> np.ndarray:
+        x = _u16(hidden)
+        ex = (ctypes.c_size_t * len(experts))(*[int(e) for e in experts])
+        rw = _u16(route_weights)
+        out = np.empty(self.H, dtype=np.uint16)
+        _call("firewing_hip_mixture_bf16", self._h, layer, _p16(x), ex, _p16(rw), len(experts),
+              _p16(out))
+        return out
+
+    def sparse_moe_block(self, layer: int, hidden, order: int = LOGITS_TREE32) -> dict:
+        x = _u16(hidden).reshape(-1, self.H)
+        T = x.shape[0]
+        out = np.empty((T, self.H), dtype=np.uint16)
+        logits = np.empty((T, self.E), dtype=np.uint16)
+        ids = np.empty((T, self.K), dtype=np.uint64)
+        scores = np.empty((T, self.K), dtype=np.uint16)
+        sig = np.empty(T, dtype=np.uint16)
+        cap = BlockCaptures(logits.ctypes.data, ids.ctypes.data, scores.ctypes.data, None,
+                            sig.ctypes.data)
+        _call("firewing_hip_sparse_moe_block", self._h, layer, _p16(x), T, order, _p16(out),
+              ctypes.byref(cap))
+        return {"out": out, "router_logits": logits, "selected_experts": ids.astype(np.int64),
+                "selected_scores": scores, "shared_gate_sigmoid": sig}
+
+    def sparse_moe_block_dev(self, layer: int, hidden, tokens: int, out, order: int = LOGITS_TREE32,
+                             stream=None) -> None:
+        _call("firewing_hip_sparse_moe_block_dev", self._h, layer, _addr(hidden), tokens, order,
+              _addr(out), _addr(stream))
+
+    def moe_step(self, hidden, order: int = LOGITS_TREE32, bias_feature: bool = True):
+        """All resident layers chained; returns (residual [T,H], block outputs [L,T,H],
+        ids [L,T,K], scores [L,T,K])."""
+        x = _u16(hidden).reshape(-1, self.H)
+        T = x.shape[0]
+        resid = np.empty((T, self.H), dtype=np.uint16)
+        blocks = np.empty((self.L, T, self.H), dtype=np.uint16)
+        ids = np.empty((self.L, T, self.K), dtype=np.int32)
+        scores = np.empty((self.L, T, self.K), dtype=np.uint16)
+        _call("firewing_hip_moe_step", self._h, _p16(x), T, order, bias_feature, _p16(resid),
+              _p16(blocks), ids.ctypes.data, _p16(scores))
+        return resid, blocks, ids, scores
+
+    def moe_step_dev(self, hidden, tokens: int, residual, block_out=None, ids=None, scores=None,
+                     order: int = LOGITS_TREE32, bias_feature: bool = True, stream=None) -> None:
+        _call("firewing_hip_moe_step_dev", self._h, _addr(hidden), tokens, order, bias_feature,
+              _addr(residual), _addr(block_out), _addr(ids), _addr(scores), _addr(stream))
+
+    def synchronize(self) -> None:
+        _call("firewing_hip_synchronize", self._h)
+
+
+def header_symbols() -> list[str]:
+    """Every function the public header declares."""
+    import re
+    text = HEADER.read_text()
+    return sorted(set(re.findall(r"\b(firewing_hip_[a-z0-9_]+)\s*\(", text)))

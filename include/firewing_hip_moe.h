@@ -1,0 +1,201 @@
+/*
+ * firewing_hip_moe: MI355X (gfx950) sparse-MoE block hot path behind a C ABI.
+ *
+ * Conventions follow the reference crate's existing FFI,
+ * `firewing_torch_topk_bf16` (src/decoder_layer.rs:19-26,
+ * native/topk_shim.cpp:18-44): `firewing_` prefix, `bool` status, raw pointers
+ * plus `size_t` counts, caller-owned outputs, bf16 as `uint16_t` bit patterns
+ * (little-endian), matrices row-major in the reference's layouts:
+ *   router [E, H], gate_up [E, 2I, H] (gate rows [0, I), up rows [I, 2I)),
+ *   down [E, H, I], shared gate/up [Is, H], shared down [H, Is],
+ *   shared_expert_gate [1, H]                     (src/expert.rs:362-512).
+ * On `false`, firewing_hip_last_error() returns a thread-local message that the
+ * Rust side turns into its `Err(String)`. No C++ exception crosses the ABI.
+ *
+ * Host-pointer entry points are synchronous, like the Metal command buffers
+ * they replace (`wait_until_completed`, src/metal_moe.rs:351-358). `_dev`
+ * entry points take device pointers and an optional stream (`hipStream_t`
+ * passed as void*, NULL = the context's stream) and are asynchronous; their
+ * errors surface at the next firewing_hip_synchronize().
+ *
+ * Arithmetic: every routed/shared expert and router output is bit-identical to
+ * the reference's scalar CPU path (src/expert.rs:514-580, src/router.rs:220-265).
+ * Top-k ties are broken by the total order of src/router.rs:241-247 (value
+ * descending, expert index ascending) in both logit orders.
+ */
+#ifndef FIREWING_HIP_MOE_H
+#define FIREWING_HIP_MOE_H
+
+#include <stdbool.h>
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Router logit order. TREE32: linear_bf16 logits, as the in-model block
+ * computes them (src/decoder_layer.rs:411, src/expert.rs:554-560).
+ * FOLD: one forward f32 fold per expert, as the standalone router
+ * (src/router.rs:228-240). */
+enum firewing_hip_logit_order {
+    FIREWING_HIP_LOGITS_TREE32 = 0,
+    FIREWING_HIP_LOGITS_FOLD = 1
+};
+
+/* Block shape. The reference's real model: H=2560, I=640, E=512, K=10,
+ * Is=640, L=48 (src/metal_moe.rs:15-18, src/decoder_layer.rs:15,40-42). */
+typedef struct firewing_hip_shape {
+    size_t hidden;              /* H; multiple of 32 */
+    size_t intermediate;        /* I; multiple of 32 */
+    size_t experts;             /* E; <= 1024 */
+    size_t top_k;               /* K; <= 32 */
+    size_t shared_intermediate; /* Is; multiple of 32 */
+    size_t layers;              /* L resident layers */
+} firewing_hip_shape;
+
+/* Optional per-call captures of the block (src/expert.rs:1154-1199 names). */
+typedef struct firewing_hip_block_captures {
+    uint16_t* router_logits;       /* [T, E] or NULL */
+    size_t* selected_experts;      /* [T, K] rank order, or NULL */
+    uint16_t* selected_scores;     /* [T, K] rank order, or NULL */
+    uint16_t* routed_mixture;      /* [T, H] or NULL */
+    uint16_t* shared_gate_sigmoid; /* [T] or NULL */
+} firewing_hip_block_captures;
+
+typedef struct firewing_hip_context firewing_hip_context;
+
+/* Thread-local message of the last failed call on this thread. */
+const char* firewing_hip_last_error(void);
+
+/* ---- stateless numeric entry points (host pointers, synchronous) -------- */
+
+/* src/expert.rs:554-560 linear_bf16: out[r] = bf16(tree32 dot of W[r,:], x).
+ * Also the Metal `firewing_bf16_gemv_exact` (kernels/bf16_gemv.metal:19-46,
+ * src/metal_bf16.rs:101-147). */
+bool firewing_hip_linear_bf16(const uint16_t* weight, const uint16_t* input, size_t rows,
+                              size_t columns, uint16_t* out);
+
+/* src/expert.rs:562-571 swiglu_bf16; kernels/bf16_gemv.metal:55-65. */
+bool firewing_hip_swiglu_bf16(const uint16_t* gate, const uint16_t* up, size_t count,
+                              uint16_t* out);
+
+/* src/expert.rs:573-576 sigmoid_bf16, elementwise. */
+bool firewing_hip_sigmoid_bf16(const uint16_t* input, size_t count, uint16_t* out);
+
+/* Top-k of bf16 values: the GPU counterpart of `firewing_torch_topk_bf16`
+ * (native/topk_shim.cpp:18-44) with the total-order tie rule. false for NULL,
+ * k == 0, k > count, count > 1024 or k > 32. */
+bool firewing_hip_topk_bf16(const uint16_t* values, size_t count, size_t k, size_t* indices);
+
+/* src/router.rs:220-265 route (order FOLD) and src/decoder_layer.rs:278-307
+ * (order TREE32) for T tokens: weight [E, H], hidden [T, H] -> ids [T, K]
+ * (rank order), scores [T, K] bf16, logits [T, E] bf16 (NULL to skip). TREE32
+ * rejects NaN logits (src/decoder_layer.rs:279-281). */
+bool firewing_hip_route_bf16(const uint16_t* weight, const uint16_t* hidden, size_t tokens,
+                             size_t experts, size_t width, size_t top_k, int order,
+                             size_t* ids, uint16_t* scores, uint16_t* logits);
+
+/* One routed expert, src/expert.rs:717-751 (gate_up -> SwiGLU -> down ->
+ * route weighting); replaces src/metal_bf16.rs:192-212 execute_expert.
+ * gate_up_weight [2I, H], down_weight [H, I], hidden [H]; every capture may be
+ * NULL: gate_up [2I], swiglu [I], down [H], weighted [H]. */
+bool firewing_hip_expert_bf16(const uint16_t* gate_up_weight, const uint16_t* down_weight,
+                              const uint16_t* hidden, size_t hidden_size,
+                              size_t intermediate, uint16_t route_weight,
+                              uint16_t* gate_up, uint16_t* swiglu, uint16_t* down,
+                              uint16_t* weighted);
+
+/* ---- resident context (replaces metal_moe::Runtime, src/metal_moe.rs:79-447) */
+
+/* Allocates resident banks for `shape->layers` layers in HBM (~3.23 GB per
+ * layer at H=2048, I=512, E=512), a stream and scratch. */
+bool firewing_hip_create(const firewing_hip_shape* shape, firewing_hip_context** out);
+void firewing_hip_destroy(firewing_hip_context* ctx);
+
+/* Device name, as ExactResidentTop10Runner::device_name (src/metal_moe.rs:444-446). */
+const char* firewing_hip_device_name(const firewing_hip_context* ctx);
+
+/* Copy one layer's weights (host pointers, reference layouts) into HBM:
+ * the install step of src/metal_moe.rs:164-207 for every expert of the layer. */
+bool firewing_hip_install_layer(firewing_hip_context* ctx, size_t layer, const uint16_t* router,
+                                const uint16_t* gate_up, const uint16_t* down,
+                                const uint16_t* shared_gate, const uint16_t* shared_up,
+                                const uint16_t* shared_down, const uint16_t* shared_expert_gate);
+
+/* Fill layers [first, first+count) on the device with the seeded synthetic
+ * weights (firewing_amd/csrc/fw_synth.h); bias_feature writes the Zipf router
+ * bias into router column H-1. */
+bool firewing_hip_generate_layers(firewing_hip_context* ctx, size_t first, size_t count,
+                                  uint64_t seed, bool bias_feature);
+
+/* Read back `count` elements from element `first` of one resident tensor
+ * (tensor ids as fw_synth.h: 1 router, 2 gate_up, 3 down, 4 shared_gate,
+ * 5 shared_up, 6 shared_down, 7 shared_expert_gate), for verification. */
+bool firewing_hip_read_tensor(firewing_hip_context* ctx, size_t layer, int tensor,
+                              size_t first, size_t count, uint16_t* out);
+
+/* Route T tokens against a resident layer's router (as firewing_hip_route_bf16). */
+bool firewing_hip_route(firewing_hip_context* ctx, size_t layer, const uint16_t* hidden,
+                        size_t tokens, int order, size_t* ids, uint16_t* scores,
+                        uint16_t* logits);
+
+/* The ordered top-k mixture on a resident layer for one hidden vector, given
+ * the experts in execution (ascending id) order and their bf16 route weights:
+ * src/expert.rs:906-956; replaces execute_one_transaction + capture_mixture
+ * (src/metal_moe.rs:310-383). */
+bool firewing_hip_mixture_bf16(firewing_hip_context* ctx, size_t layer, const uint16_t* hidden,
+                               const size_t* experts, const uint16_t* route_weights,
+                               size_t count, uint16_t* mixture);
+
+/* One sparse-MoE block for T <= 4 tokens (decode and MTP verify): router,
+ * top-k, routed experts, ordered mixture, shared expert and gate, combine
+ * (src/decoder_layer.rs:460-586; src/expert.rs:1109-1153). */
+bool firewing_hip_sparse_moe_block(firewing_hip_context* ctx, size_t layer,
+                                   const uint16_t* hidden, size_t tokens, int order,
+                                   uint16_t* out, firewing_hip_block_captures* captures);
+
+/* Device-pointer variant; hidden [T, H], out [T, H] in HBM. */
+bool firewing_hip_sparse_moe_block_dev(firewing_hip_context* ctx, size_t layer,
+                                       const uint16_t* hidden, size_t tokens, int order,
+                                       uint16_t* out, void* stream);
+
+/* All resident layers for T <= 4 tokens in one persistent launch, chained by
+ * the residual stream x_{l+1} = add_bf16(x_l, block_l(x_l)) (x_{l+1}[H-1] reset
+ * to 1.0 when bias_feature): the 48-layer decode step the overlap benches
+ * emulate with 48 execute_exact() calls (src/overlap_bound.rs:732-734).
+ * Device pointers: hidden [T, H] in, residual [T, H] out; block_out
+ * [L, T, H], ids [L, T, K] (int32) and scores [L, T, K] may be NULL. */
+bool firewing_hip_moe_step_dev(firewing_hip_context* ctx, const uint16_t* hidden, size_t tokens,
+                               int order, bool bias_feature, uint16_t* residual,
+                               uint16_t* block_out, int32_t* ids, uint16_t* scores,
+                               void* stream);
+
+/* Host-pointer variant of the step (synchronous). */
+bool firewing_hip_moe_step(firewing_hip_context* ctx, const uint16_t* hidden, size_t tokens,
+                           int order, bool bias_feature, uint16_t* residual,
+                           uint16_t* block_out, int32_t* ids, uint16_t* scores);
+
+/* Waits for the context's stream and reports any device-side failure
+ * (a persistent-kernel dependency wait that timed out). */
+bool firewing_hip_synchronize(firewing_hip_context* ctx);
+
+/* Seeded synthetic hidden vectors of the benchmark workload (host memory):
+ * bf16(N(0,1)) RMS-normalised, x[H-1] = 1.0 when bias_feature (the constant
+ * feature that carries the Zipf router bias). No counterpart in the reference,
+ * whose inputs come from make_hidden (src/expert.rs:341-360). */
+void firewing_hip_synth_hidden(uint64_t seed, uint32_t first_token, uint32_t tokens,
+                               uint32_t hidden, bool bias_feature, uint16_t* out);
+
+/* Host-side copy of the library's expf (the glibc-equivalent table method the
+ * kernels use), for verification against the platform libm. */
+void firewing_hip_expf_host(const float* in, float* out, size_t count);
+
+/* Device evaluation of the same expf, for verification (synchronous). */
+bool firewing_hip_expf_device(const float* in, float* out, size_t count);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* FIREWING_HIP_MOE_H */

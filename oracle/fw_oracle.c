@@ -20,6 +20,7 @@
 #include <math.h>
 #include <stdlib.h>
 #include <string.h>
+#include <time.h>
 
 #include "../firewing_amd/csrc/fw_synth.h"
 
@@ -48,18 +49,23 @@ void fwo_expf_array(const float* in, float* out, size_t n) {
 
 /* src/expert.rs:514-552 pytorch_bf16_vector_dot: 8 registers x 4 lanes of f32
  * accumulators over 32-value blocks (multiply, then add; no FMA), the register
- * tree 4/2/1, then (a0+a1)+(a2+a3); an 8-wide tail and a scalar tail. */
+ * tree 4/2/1, then (a0+a1)+(a2+a3); an 8-wide tail and a scalar tail.
+ * Accumulator [register][lane] is acc[4 * register + lane], i.e. column j of
+ * each block feeds acc[j]; the flat form lets the compiler use vector lanes,
+ * each of which performs the same f32 multiply and add. */
 float fwo_dot_tree32(const uint16_t* left, const uint16_t* right, size_t n) {
-    float acc[8][4];
-    memset(acc, 0, sizeof acc);
+    float acc[32];
+    for (int j = 0; j < 32; ++j) acc[j] = 0.0f;
     size_t complete_blocks = n / 32 * 32;
     for (size_t block = 0; block < complete_blocks; block += 32) {
-        for (int reg = 0; reg < 8; ++reg) {
-            for (int lane = 0; lane < 4; ++lane) {
-                size_t index = block + (size_t)reg * 4 + (size_t)lane;
-                float product = fwo_from_bf16(left[index]) * fwo_from_bf16(right[index]);
-                acc[reg][lane] = acc[reg][lane] + product;
-            }
+        for (int j = 0; j < 32; ++j) {
+            uint32_t lb = (uint32_t)left[block + j] << 16;
+            uint32_t rb = (uint32_t)right[block + j] << 16;
+            float lf, rf;
+            memcpy(&lf, &lb, sizeof lf);
+            memcpy(&rf, &rb, sizeof rf);
+            float product = lf * rf;
+            acc[j] = acc[j] + product;
         }
     }
     static const int offsets[3] = {4, 2, 1};
@@ -67,11 +73,11 @@ float fwo_dot_tree32(const uint16_t* left, const uint16_t* right, size_t n) {
         int offset = offsets[o];
         for (int reg = 0; reg < offset; ++reg) {
             for (int lane = 0; lane < 4; ++lane) {
-                acc[reg][lane] = acc[reg][lane] + acc[offset + reg][lane];
+                acc[4 * reg + lane] = acc[4 * reg + lane] + acc[4 * (offset + reg) + lane];
             }
         }
     }
-    float reduced = (acc[0][0] + acc[0][1]) + (acc[0][2] + acc[0][3]);
+    float reduced = (acc[0] + acc[1]) + (acc[2] + acc[3]);
     size_t complete_vectors = n / 8 * 8;
     float tail[4] = {0.0f, 0.0f, 0.0f, 0.0f};
     for (size_t block = complete_blocks; block < complete_vectors; block += 8) {
@@ -317,7 +323,8 @@ static int block_core(const fwo_shape* s, const uint16_t* router, const uint16_t
                       const uint16_t* const* down, const uint16_t* shared_gate,
                       const uint16_t* shared_up, const uint16_t* shared_down,
                       const uint16_t* shared_expert_gate, const uint16_t* hidden, int order,
-                      const int32_t* known_ids, uint16_t* out, fwo_block_captures* cap) {
+                      const int32_t* known_ids, const uint16_t* known_logits, uint16_t* out,
+                      fwo_block_captures* cap) {
     size_t H = s->hidden, I = s->intermediate, E = s->experts, K = s->top_k;
     size_t Is = s->shared_intermediate;
     int ok = 1;
@@ -334,7 +341,9 @@ static int block_core(const fwo_shape* s, const uint16_t* router, const uint16_t
         ok = 0;
         goto done;
     }
-    if (order == FWO_ORDER_FOLD) {
+    if (known_logits != NULL) {
+        memcpy(logits, known_logits, E * sizeof(uint16_t));
+    } else if (order == FWO_ORDER_FOLD) {
         fwo_linear_fold_bf16(router, hidden, E, H, logits);
     } else {
         fwo_linear_bf16(router, hidden, E, H, logits);
@@ -419,8 +428,8 @@ int fwo_sparse_moe_block(const fwo_shape* shape, const fwo_layer* layer, const u
         dn[e] = layer->down + e * H * I;
     }
     int ok = block_core(shape, layer->router, gu, dn, layer->shared_gate, layer->shared_up,
-                        layer->shared_down, layer->shared_expert_gate, hidden, order, NULL, out,
-                        captures);
+                        layer->shared_down, layer->shared_expert_gate, hidden, order, NULL, NULL,
+                        out, captures);
     free(gu);
     free(dn);
     return ok;
@@ -589,7 +598,8 @@ int fwo_synth_block(const fwo_shape* shape, const fwo_synth_config* config, uint
             ok = ok && block_core(shape, L.router, (const uint16_t* const*)L.gate_up,
                                   (const uint16_t* const*)L.down, L.shared_gate, L.shared_up,
                                   L.shared_down, L.shared_expert_gate, hidden + (size_t)t * H,
-                                  config->order, sel + (size_t)t * K, out + (size_t)t * H, NULL);
+                                  config->order, sel + (size_t)t * K, lg + (size_t)t * E,
+                                  out + (size_t)t * H, NULL);
         }
     }
     if (ok) {
@@ -634,5 +644,64 @@ int fwo_synth_step(const fwo_shape* shape, const fwo_synth_config* config, uint3
     if (ok && residual_out) memcpy(residual_out, x, tokens * H * sizeof(uint16_t));
     free(x);
     free(o);
+    return ok;
+}
+
+static double now_seconds(void) {
+    struct timespec ts;
+    clock_gettime(CLOCK_MONOTONIC, &ts);
+    return (double)ts.tv_sec + 1e-9 * (double)ts.tv_nsec;
+}
+
+/* The chained step of fwo_synth_step on one thread, timing only the block
+ * arithmetic (router, top-k, scores, experts, mixture, shared expert,
+ * combine, residual add). Regenerating each layer's synthetic weights is
+ * outside the timed region: the reference reads resident weights. */
+int fwo_synth_step_timed(const fwo_shape* shape, const fwo_synth_config* config, uint32_t layers,
+                         const uint16_t* hidden, size_t tokens, uint16_t* residual_out,
+                         double* compute_seconds) {
+    size_t H = shape->hidden, E = shape->experts, K = shape->top_k;
+    if (K == 0 || K > 64 || K > E) return 0;
+    uint16_t* x = (uint16_t*)malloc(tokens * H * sizeof(uint16_t));
+    uint16_t* o = (uint16_t*)malloc(tokens * H * sizeof(uint16_t));
+    int32_t* sel = (int32_t*)malloc(tokens * K * sizeof(int32_t));
+    uint16_t* sc = (uint16_t*)malloc(tokens * K * sizeof(uint16_t));
+    uint16_t* lg = (uint16_t*)malloc(tokens * E * sizeof(uint16_t));
+    int ok = x && o && sel && sc && lg;
+    double timed = 0.0;
+    if (ok) memcpy(x, hidden, tokens * H * sizeof(uint16_t));
+    for (uint32_t l = 0; ok && l < layers; ++l) {
+        synth_layer L;
+        ok = synth_layer_dense(shape, config, l, &L);
+        double t0 = now_seconds();
+        for (size_t t = 0; ok && t < tokens; ++t) {
+            ok = fwo_route(L.router, x + t * H, E, H, K, config->order, sel + t * K, lg + t * E,
+                           sc + t * K);
+        }
+        timed += now_seconds() - t0;
+        for (size_t t = 0; ok && t < tokens; ++t) {
+            for (size_t r = 0; ok && r < K; ++r) ok = synth_layer_expert(shape, config, l, &L, sel[t * K + r]);
+        }
+        t0 = now_seconds();
+        for (size_t t = 0; ok && t < tokens; ++t) {
+            ok = block_core(shape, L.router, (const uint16_t* const*)L.gate_up,
+                            (const uint16_t* const*)L.down, L.shared_gate, L.shared_up,
+                            L.shared_down, L.shared_expert_gate, x + t * H, config->order,
+                            sel + t * K, lg + t * E, o + t * H, NULL);
+        }
+        for (size_t t = 0; ok && t < tokens; ++t) {
+            for (size_t h = 0; h < H; ++h) x[t * H + h] = fwo_add_bf16(x[t * H + h], o[t * H + h]);
+            if (config->bias_feature) x[t * H + H - 1] = 0x3f80u;
+        }
+        timed += now_seconds() - t0;
+        synth_layer_free(&L);
+    }
+    if (ok && residual_out) memcpy(residual_out, x, tokens * H * sizeof(uint16_t));
+    if (compute_seconds) *compute_seconds = timed;
+    free(x);
+    free(o);
+    free(sel);
+    free(sc);
+    free(lg);
     return ok;
 }

@@ -114,6 +114,9 @@ int fwo_synth_block(const fwo_shape* shape, const fwo_synth_config* config, uint
 int fwo_synth_step(const fwo_shape* shape, const fwo_synth_config* config, uint32_t layers,
                    const uint16_t* hidden, size_t tokens, uint16_t* residual_out,
                    uint16_t* block_out, int32_t* ids, uint16_t* scores);
+int fwo_synth_step_timed(const fwo_shape* shape, const fwo_synth_config* config, uint32_t layers,
+                         const uint16_t* hidden, size_t tokens, uint16_t* residual_out,
+                         double* compute_seconds);
 int fwo_synth_route(const fwo_shape* shape, const fwo_synth_config* config, uint32_t layer,
                     const uint16_t* hidden, size_t tokens, int32_t* ids, uint16_t* scores,
                     uint16_t* logits);

@@ -135,6 +135,10 @@ def lib() -> ctypes.CDLL:
         L.fwo_synth_step.restype = ctypes.c_int
         L.fwo_synth_step.argtypes = [ctypes.POINTER(Shape), ctypes.POINTER(SynthConfig),
                                      ctypes.c_uint32, _u16p, _size, _u16p, _u16p, _i32p, _u16p]
+        L.fwo_synth_step_timed.restype = ctypes.c_int
+        L.fwo_synth_step_timed.argtypes = [ctypes.POINTER(Shape), ctypes.POINTER(SynthConfig),
+                                           ctypes.c_uint32, _u16p, _size, _u16p,
+                                           ctypes.POINTER(ctypes.c_double)]
         L.fwo_synth_route.restype = ctypes.c_int
         L.fwo_synth_route.argtypes = [ctypes.POINTER(Shape), ctypes.POINTER(SynthConfig),
                                       ctypes.c_uint32, _u16p, _size, _i32p, _u16p, _u16p]
@@ -418,6 +422,20 @@ def synth_step(shape: dict, seed: int, layers: int, hidden: np.ndarray, bias_fea
                                 _p16(blocks), _p32(ids), _p16(scores)):
         raise ValueError("synthetic step failed")
     return resid, blocks, ids, scores
+
+
+def synth_step_timed(shape: dict, seed: int, layers: int, hidden: np.ndarray, bias_feature=True,
+                     order=ORDER_TREE32):
+    """Single-thread chained step; returns (x_L, seconds spent in block arithmetic)."""
+    h = _u16(hidden)
+    T = h.shape[0]
+    resid = np.empty((T, shape["hidden"]), dtype=np.uint16)
+    secs = ctypes.c_double(0.0)
+    s, c = _shape(shape), _config(seed, bias_feature, order, 1)
+    if not lib().fwo_synth_step_timed(ctypes.byref(s), ctypes.byref(c), layers, _p16(h), T,
+                                      _p16(resid), ctypes.byref(secs)):
+        raise ValueError("timed synthetic step failed")
+    return resid, secs.value
 
 
 # ---- the reference's own top-k shim (built from native/topk_shim.cpp) ---------------
