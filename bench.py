@@ -5,9 +5,10 @@ Workload: a 48-layer stack of sparse-MoE blocks at H=2048, I=512, E=512 routed
 experts (top-10, softmax renormalised) plus one shared expert (Is=512,
 sigmoid-gated), batch-1 decode. All 48 layers' bf16 weights (~155 GB) are
 resident in HBM, seeded synthetic with a Zipf(1.1) router bias. One step = one
-token through all 48 layers, chained through the residual stream
-x_{l+1} = bf16(x_l + block_l(x_l)); the whole step is one persistent kernel
-launch (k_moe_decode), so the timed region is exactly the kernel launches.
+token through all 48 layers, chained through a pre-norm residual stream
+(h_l = rms_norm(r_l), r_{l+1} = bf16(r_l + block_l(h_l))); the whole step is
+one persistent kernel launch (k_moe_decode), so the timed region is exactly
+the kernel launches.
 
 Prints one JSON line (the driver contract) with:
   value       microseconds per token of the 48-layer step (lower is better)
@@ -49,24 +50,27 @@ def layer_bytes(union_experts: int) -> int:
     return 2 * (E * H + union_experts * (2 * I * H + H * I) + 3 * Is * H + H)
 
 
-def time_steps(torch, ctx, x, resid, tokens: int, steps: int, warmup: int):
-    stream = torch.cuda.current_stream()
-    handle = stream.cuda_stream
+def time_steps(rt, ctx, x, resid, tokens: int, steps: int, warmup: int):
+    """Launch the step on a dedicated default-priority stream and bracket every
+    launch with HIP events recorded on that same stream."""
+    stream = rt.Stream()
     for _ in range(warmup):
-        ctx.moe_step_dev(x, tokens, resid, stream=handle)
+        ctx.moe_step_dev(x.ptr, tokens, resid.ptr, stream=stream.handle)
+    stream.synchronize()
     ctx.synchronize()
-    torch.cuda.synchronize()
-    starts = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
-    ends = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
-    torch.cuda.synchronize()
+    starts = [rt.Event() for _ in range(steps)]
+    ends = [rt.Event() for _ in range(steps)]
     for i in range(steps):
         starts[i].record(stream)
-        ctx.moe_step_dev(x, tokens, resid, stream=handle)
+        ctx.moe_step_dev(x.ptr, tokens, resid.ptr, stream=stream.handle)
         ends[i].record(stream)
-    torch.cuda.synchronize()
+    stream.synchronize()
     ctx.synchronize()
-    per_launch_ms = [s.elapsed_time(e) for s, e in zip(starts, ends)]
-    total_ms = starts[0].elapsed_time(ends[-1])
+    per_launch_ms = [s.elapsed_ms(e) for s, e in zip(starts, ends)]
+    total_ms = starts[0].elapsed_ms(ends[-1])
+    for e in starts + ends:
+        e.destroy()
+    stream.destroy()
     return total_ms, per_launch_ms
 
 
@@ -103,11 +107,8 @@ def main() -> int:
               file=sys.stderr)
         return 2
 
-    import torch
-    if not torch.cuda.is_available():
-        print("bench.py needs a ROCm GPU", file=sys.stderr)
-        return 1
     from firewing_amd import hip_moe as hm
+    from firewing_amd import hip_runtime as rt
 
     L = args.layers
     T = 1
@@ -119,8 +120,8 @@ def main() -> int:
     log(f"resident banks ready in {time.time() - t0:.1f} s")
 
     x_host = hm.synth_hidden(args.seed, T, SHAPE["hidden"], True)
-    x = torch.from_numpy(x_host.view(np.int16)).cuda()
-    resid = torch.empty_like(x)
+    x = rt.DeviceArray.from_numpy(x_host)
+    resid = rt.DeviceArray(x_host.shape, np.uint16)
 
     # Routed union per layer (10 for one token) from one captured step.
     r_host, _, ids, _ = ctx.moe_step(x_host)
@@ -128,8 +129,8 @@ def main() -> int:
     bytes_per_launch = sum(layer_bytes(u) for u in unions)
 
     log(f"timing {args.steps} steps after {args.warmup} warm-up steps")
-    total_ms, per_launch = time_steps(torch, ctx, x, resid, T, args.steps, args.warmup)
-    gpu_resid = resid.cpu().numpy().view(np.uint16)
+    total_ms, per_launch = time_steps(rt, ctx, x, resid, T, args.steps, args.warmup)
+    gpu_resid = resid.numpy()
     assert np.array_equal(gpu_resid, r_host), "device-pointer step differs from host-pointer step"
     ms_per_step = total_ms / args.steps
     avg_launch_ms = float(np.mean(per_launch))
@@ -158,7 +159,7 @@ def main() -> int:
             "router": "tree32 logits (in-model order), total-order top-10, f32 softmax, renormalised",
             "accumulate": "f32, reference summation order, no FMA",
             "router_bias": "Zipf(1.1) popularity via constant feature x[H-1]=1",
-            "chaining": "x_{l+1} = bf16(x_l + block_l(x_l)), x[H-1] reset to 1.0",
+            "chaining": "pre-norm residual: h_l = rms_norm(r_l) (h[H-1]=1), r_{l+1} = bf16(r_l + block_l(h_l))",
             "seed": hex(args.seed),
         },
         "hbm_gbps": round(achieved, 1),
@@ -179,12 +180,12 @@ def main() -> int:
         mtp = {}
         for width in (2, 4):
             xw_host = hm.synth_hidden(args.seed, width, SHAPE["hidden"], True, first_token=1000)
-            xw = torch.from_numpy(xw_host.view(np.int16)).cuda()
-            rw = torch.empty_like(xw)
+            xw = rt.DeviceArray.from_numpy(xw_host)
+            rw = rt.DeviceArray(xw_host.shape, np.uint16)
             _, _, idw, _ = ctx.moe_step(xw_host)
             u = union_sizes(idw)
             b = sum(layer_bytes(n) for n in u)
-            tot, per = time_steps(torch, ctx, xw, rw, width, max(5, args.steps // 2), 2)
+            tot, per = time_steps(rt, ctx, xw, rw, width, max(5, args.steps // 2), 2)
             ms = tot / max(5, args.steps // 2)
             gbps = b / (float(np.mean(per)) * 1e-3) / 1e9
             mtp[str(width)] = {"us_per_step": round(ms * 1000, 2),
@@ -196,8 +197,8 @@ def main() -> int:
         result["mtp"] = mtp
 
     ctx.close()
-    del x, resid
-    torch.cuda.empty_cache()
+    x.free()
+    resid.free()
 
     if not args.no_cpu_baseline:
         from oracle import fw_oracle as fo

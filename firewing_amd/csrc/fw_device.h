@@ -4,10 +4,14 @@
 // chains (chain j takes columns j, j+32, j+64, ...), then a fixed tree. Here 16
 // lanes share a row: lane q owns chains 2q and 2q+1, i.e. one packed bf16 pair
 // (a 32-bit load) per 32-column block, so 16 lanes read one 64-byte block per
-// step and a wave covers 4 rows. After the sweep the tree is evaluated across
-// the 16 lanes: +16 is lane q+8, +8 is lane q+4, +4 is lane q+2, and
-// (a0+a1)+(a2+a3) joins lanes 0 and 1. Multiplies and adds stay separate
-// (-ffp-contract=off), so every chain rounds exactly where the CPU's does.
+// step and a wave covers 4 rows. A lane issues the loads of its whole row
+// share before the first multiply (a row of 2048 columns is 64 loads, 16 KB in
+// flight per wave), so a wave pays one memory round trip per row set instead
+// of one per block. After the sweep the tree is evaluated across the 16 lanes
+// of the row with DPP row shifts: +16 is lane q+8, +8 is lane q+4, +4 is lane
+// q+2, and (a0+a1)+(a2+a3) joins lanes 0 and 1. Multiplies and adds stay
+// separate (-ffp-contract=off), so every chain rounds exactly where the CPU's
+// does.
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -22,24 +26,39 @@ constexpr int kLanesPerRow = 16;
 constexpr int kRowsPerWave = kWave / kLanesPerRow;  // 4
 
 __device__ __forceinline__ int lane_id() { return (int)(threadIdx.x & (kWave - 1)); }
-__device__ __forceinline__ int wave_id() { return (int)(threadIdx.x / kWave); }
+__device__ __forceinline__ int wave_id() { return __builtin_amdgcn_readfirstlane((int)(threadIdx.x / kWave)); }
+
+// DPP controls (GFX9 encoding).
+constexpr int kDppRowShl1 = 0x101, kDppRowShl2 = 0x102, kDppRowShl4 = 0x104, kDppRowShl8 = 0x108;
+constexpr int kDppRowMirror = 0x140, kDppRowHalfMirror = 0x141;
+constexpr int kDppRowBcast15 = 0x142, kDppRowBcast31 = 0x143;
+constexpr int kDppQuadXor1 = 0xB1, kDppQuadXor2 = 0x4E;  // quad_perm [1,0,3,2], [2,3,0,1]
+
+// v from lane (i + n) of the same 16-lane row (0 past the row's end).
+template <int CTRL>
+__device__ __forceinline__ float dpp_f32(float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), CTRL, 0xf, 0xf, true));
+}
+template <int CTRL>
+__device__ __forceinline__ uint32_t dpp_u32(uint32_t v) {
+    return (uint32_t)__builtin_amdgcn_mov_dpp((int)v, CTRL, 0xf, 0xf, true);
+}
 
 // Tree of the 32 chains after the sweep: returns (a0+a1)+(a2+a3) in lane
 // q == 0 of every 16-lane row group (other lanes hold partials).
 __device__ __forceinline__ float tree32_reduce(float c0, float c1) {
     // a'[j] = c[j] + c[j+16]   (chains 2q+c and 2q+16+c live in lanes q, q+8)
-    c0 = add_rn(c0, __shfl_down(c0, 8, kLanesPerRow));
-    c1 = add_rn(c1, __shfl_down(c1, 8, kLanesPerRow));
+    c0 = add_rn(c0, dpp_f32<kDppRowShl8>(c0));
+    c1 = add_rn(c1, dpp_f32<kDppRowShl8>(c1));
     // a''[j] = a'[j] + a'[j+8]
-    c0 = add_rn(c0, __shfl_down(c0, 4, kLanesPerRow));
-    c1 = add_rn(c1, __shfl_down(c1, 4, kLanesPerRow));
+    c0 = add_rn(c0, dpp_f32<kDppRowShl4>(c0));
+    c1 = add_rn(c1, dpp_f32<kDppRowShl4>(c1));
     // a'''[j] = a''[j] + a''[j+4]
-    c0 = add_rn(c0, __shfl_down(c0, 2, kLanesPerRow));
-    c1 = add_rn(c1, __shfl_down(c1, 2, kLanesPerRow));
+    c0 = add_rn(c0, dpp_f32<kDppRowShl2>(c0));
+    c1 = add_rn(c1, dpp_f32<kDppRowShl2>(c1));
     // lane 0 holds a0, a1; lane 1 holds a2, a3: (a0 + a1) + (a2 + a3)
     float pair = add_rn(c0, c1);
-    float other = __shfl_down(pair, 1, kLanesPerRow);
-    return add_rn(pair, other);
+    return add_rn(pair, dpp_f32<kDppRowShl1>(pair));
 }
 
 // src/expert.rs:541-550, by one lane after the tree: the 8-wide tail sum is
@@ -61,43 +80,131 @@ __device__ __forceinline__ float tree32_finish(float reduced, const uint16_t* __
     return r;
 }
 
-// Chains of one row for NT tokens. `wrow` points at the row (bf16 pairs as
-// u32), `xs` at NT f32 vectors of stride `xstride` (LDS or registers' source),
-// q is the lane's position in its row group. Only complete 32-blocks.
-template <int NT, int UNROLL>
-__device__ __forceinline__ void tree32_sweep(const uint32_t* __restrict__ wrow, int nblocks,
-                                             const float* __restrict__ xs, int xstride, int q,
-                                             uint32_t token_mask, float (&acc)[NT][2]) {
+// Global-memory view of a pointer (loads through it are global, not flat,
+// instructions: they do not wait on LDS traffic).
+template <typename T>
+__device__ __forceinline__ const __attribute__((address_space(1))) T* as_global(const T* p) {
+    return (const __attribute__((address_space(1))) T*)(p);
+}
+
+// Agent-scope relaxed atomic 32-bit accesses: data exchanged between
+// workgroups of one launch (see the synchronisation notes below).
+template <typename T>
+__device__ __forceinline__ __attribute__((address_space(1))) T* as_global_rw(T* p) {
+    return (__attribute__((address_space(1))) T*)(p);
+}
+__device__ __forceinline__ uint32_t coherent_load(const uint32_t* p) {
+    return __hip_atomic_load(as_global(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ int32_t coherent_load(const int32_t* p) {
+    return __hip_atomic_load(as_global(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void coherent_store(uint32_t* p, uint32_t v) {
+    __hip_atomic_store(as_global_rw(p), v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void coherent_store(int32_t* p, int32_t v) {
+    __hip_atomic_store(as_global_rw(p), v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Wave-uniform value as a scalar (lets the compiler branch on it without
+// exec masks).
+__device__ __forceinline__ int uniform(int v) { return __builtin_amdgcn_readfirstlane(v); }
+
+// The same scalar, opaque to loop-invariant code motion: values derived from
+// it are computed where they are used instead of being hoisted out of the
+// task loop and held in registers for its whole length.
+__device__ __forceinline__ int opaque(int v) {
+    asm volatile("" : "+s"(v));
+    return v;
+}
+
+// A lane's share of one row: the packed bf16 pair of every 32-column block.
+template <int MAXB>
+struct RowShare {
+    uint32_t w[MAXB];
+};
+
+// Issue the loads of a row share: nblocks <= MAXB complete 32-column blocks.
+// Every slot is loaded (slots past nblocks repeat the last block), so the
+// loads carry no branches; the chain sweeps skip the repeats.
+template <int MAXB>
+__device__ __forceinline__ void row_issue(RowShare<MAXB>& r, const uint32_t* wrow, int nblocks, int q) {
+    const auto* g = as_global(wrow) + q;
+    const int last = opaque(nblocks - 1);
 #pragma unroll
-    for (int t = 0; t < NT; ++t) acc[t][0] = acc[t][1] = 0.0f;
-    int b = 0;
-    for (; b + UNROLL <= nblocks; b += UNROLL) {
-        uint32_t w[UNROLL];
+    for (int u = 0; u < MAXB; ++u) {
+        const int b = u < last ? u : last;
+        r.w[u] = __builtin_nontemporal_load(g + b * 16);
+    }
+}
+
+// Chains of one row for NT tokens against f32 vectors in LDS (stride xstride),
+// accumulated onto acc (the caller zeroes it once per row). Every token is
+// computed; the caller discards what it does not need. nblocks is uniform.
+// Scheduling barriers every 8 blocks keep the LDS operand reads next to their
+// use (hoisting all of them would need two registers per block and token).
+template <int NT, int MAXB>
+__device__ __forceinline__ void row_chains_acc(const RowShare<MAXB>& r, int nblocks,
+                                               const float* __restrict__ xs, int xstride, int q,
+                                               float (&acc)[NT][2]) {
+    nblocks = opaque(nblocks);
 #pragma unroll
-        for (int u = 0; u < UNROLL; ++u) w[u] = __builtin_nontemporal_load(wrow + (b + u) * 16 + q);
+    for (int u0 = 0; u0 < MAXB; u0 += 8) {
 #pragma unroll
-        for (int u = 0; u < UNROLL; ++u) {
-            float w0 = bf16_lo(w[u]);
-            float w1 = bf16_hi(w[u]);
+        for (int u = u0; u < u0 + 8 && u < MAXB; ++u) {
+            if (u < nblocks) {
+                float w0 = bf16_lo(r.w[u]);
+                float w1 = bf16_hi(r.w[u]);
 #pragma unroll
-            for (int t = 0; t < NT; ++t) {
-                if (!(token_mask & (1u << t))) continue;
-                float2 xv = *reinterpret_cast<const float2*>(xs + t * xstride + (b + u) * 32 + 2 * q);
-                acc[t][0] = add_rn(acc[t][0], mul_rn(w0, xv.x));
-                acc[t][1] = add_rn(acc[t][1], mul_rn(w1, xv.y));
+                for (int t = 0; t < NT; ++t) {
+                    float2 xv = *reinterpret_cast<const float2*>(xs + t * xstride + u * 32 + 2 * q);
+                    acc[t][0] = add_rn(acc[t][0], mul_rn(w0, xv.x));
+                    acc[t][1] = add_rn(acc[t][1], mul_rn(w1, xv.y));
+                }
             }
         }
+        __builtin_amdgcn_sched_barrier(0);
     }
-    for (; b < nblocks; ++b) {
-        uint32_t w = __builtin_nontemporal_load(wrow + b * 16 + q);
-        float w0 = bf16_lo(w);
-        float w1 = bf16_hi(w);
+}
+
+template <int NT, int MAXB>
+__device__ __forceinline__ void row_chains(const RowShare<MAXB>& r, int nblocks,
+                                           const float* __restrict__ xs, int xstride, int q,
+                                           float (&acc)[NT][2]) {
 #pragma unroll
-        for (int t = 0; t < NT; ++t) {
-            if (!(token_mask & (1u << t))) continue;
-            float2 xv = *reinterpret_cast<const float2*>(xs + t * xstride + b * 32 + 2 * q);
-            acc[t][0] = add_rn(acc[t][0], mul_rn(w0, xv.x));
-            acc[t][1] = add_rn(acc[t][1], mul_rn(w1, xv.y));
+    for (int t = 0; t < NT; ++t) acc[t][0] = acc[t][1] = 0.0f;
+    row_chains_acc<NT, MAXB>(r, nblocks, xs, xstride, q, acc);
+}
+
+// Chains of one row for NT tokens against bf16 vectors that other workgroups
+// wrote in this launch (packed pairs, token stride xstride elements, read with
+// coherent loads). token_mask is wave-uniform:
+// tokens outside it are not loaded. A token's loads are all issued before its
+// first multiply: one memory round trip per token.
+template <int NT, int MAXB>
+__device__ __forceinline__ void row_chains_gx(const RowShare<MAXB>& r, int nblocks,
+                                              const uint16_t* x, int xstride, int q,
+                                              uint32_t token_mask, float (&acc)[NT][2]) {
+#pragma unroll
+    for (int t = 0; t < NT; ++t) acc[t][0] = acc[t][1] = 0.0f;
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
+        if (!(token_mask & (1u << t))) continue;
+        const uint32_t* x2 = reinterpret_cast<const uint32_t*>(x + (size_t)t * xstride) + q;
+        uint32_t xv[MAXB];
+        nblocks = opaque(nblocks);
+        const int last = nblocks - 1;
+#pragma unroll
+        for (int u = 0; u < MAXB; ++u) {
+            const int b = u < last ? u : last;
+            xv[u] = coherent_load(x2 + b * 16);
+        }
+#pragma unroll
+        for (int u = 0; u < MAXB; ++u) {
+            if (u < nblocks) {
+                acc[t][0] = add_rn(acc[t][0], mul_rn(bf16_lo(r.w[u]), bf16_lo(xv[u])));
+                acc[t][1] = add_rn(acc[t][1], mul_rn(bf16_hi(r.w[u]), bf16_hi(xv[u])));
+            }
         }
     }
 }
@@ -123,19 +230,29 @@ __device__ __forceinline__ float fold_row(const uint16_t* __restrict__ w,
     return sum;
 }
 
-// Wave-wide maximum of a 32-bit unsigned key, broadcast to all lanes.
+// Wave-wide maximum of a 32-bit unsigned key, as a wave-uniform value: quad
+// swaps, half-row and row mirrors, then row broadcasts 15 and 31.
 __device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) {
-        uint32_t o = __shfl_xor(v, off, kWave);
-        v = v > o ? v : o;
-    }
-    return v;
+    uint32_t o;
+    o = dpp_u32<kDppQuadXor1>(v);
+    v = v > o ? v : o;
+    o = dpp_u32<kDppQuadXor2>(v);
+    v = v > o ? v : o;
+    o = dpp_u32<kDppRowHalfMirror>(v);
+    v = v > o ? v : o;
+    o = dpp_u32<kDppRowMirror>(v);
+    v = v > o ? v : o;
+    o = (uint32_t)__builtin_amdgcn_update_dpp((int)v, (int)v, kDppRowBcast15, 0xa, 0xf, false);
+    v = v > o ? v : o;
+    o = (uint32_t)__builtin_amdgcn_update_dpp((int)v, (int)v, kDppRowBcast31, 0xc, 0xf, false);
+    v = v > o ? v : o;
+    return (uint32_t)__builtin_amdgcn_readlane((int)v, 63);
 }
 
 // One wave selects the top k of `count` bf16 logits under the total order
-// (value descending, then index ascending; src/router.rs:241-247). Writes ids
-// in rank order to ids[0..k) (all lanes write the same value; lane 0 is enough).
+// (value descending, then index ascending; src/router.rs:241-247). Each lane
+// sorts its MAXPER keys; every round the wave maximum of the lane heads is
+// selected and its lane pops it. Writes ids in rank order (lane 0).
 // count <= 64 * MAXPER, k <= count.
 template <int MAXPER>
 __device__ __forceinline__ void wave_topk(const uint16_t* __restrict__ logits, int count, int k,
@@ -147,35 +264,49 @@ __device__ __forceinline__ void wave_topk(const uint16_t* __restrict__ logits, i
         int e = lane + kWave * m;
         keys[m] = e < count ? topk_key(logits[e], (uint32_t)e) : 0u;  // 0 is below every key
     }
+    // descending odd-even transposition sort of the lane's keys
+#pragma unroll
+    for (int pass = 0; pass < MAXPER; ++pass) {
+#pragma unroll
+        for (int m = pass & 1; m + 1 < MAXPER; m += 2) {
+            uint32_t a = keys[m], b = keys[m + 1];
+            keys[m] = a > b ? a : b;
+            keys[m + 1] = a > b ? b : a;
+        }
+    }
     for (int r = 0; r < k; ++r) {
-        uint32_t best = 0;
+        uint32_t best = wave_max_u32(keys[0]);
+        if (keys[0] == best) {  // keys are unique per expert: exactly one lane
 #pragma unroll
-        for (int m = 0; m < MAXPER; ++m) best = keys[m] > best ? keys[m] : best;
-        best = wave_max_u32(best);
-#pragma unroll
-        for (int m = 0; m < MAXPER; ++m) {
-            if (keys[m] == best) keys[m] = 0u;  // keys are unique per expert
+            for (int m = 0; m + 1 < MAXPER; ++m) keys[m] = keys[m + 1];
+            keys[MAXPER - 1] = 0u;
         }
         if (lane == 0) ids[r] = (int32_t)topk_key_expert(best);
     }
 }
 
 // ---- inter-workgroup synchronisation for the persistent kernel ----------------------
+//
+// Everything one workgroup writes for another (activations, logits, expert
+// lists, the residual stream) and the counters that announce it are accessed
+// only with agent-scope relaxed atomics: 32-bit stores that write through to
+// the device's coherence point and loads that read from it, past the per-XCD
+// L2 caches, which are not coherent with each other. A task publishes by
+// waiting until its own stores are acknowledged (so they are visible at the
+// coherence point), then raising the counter; a waiter reads the data only
+// after it has seen the count. No cache write-back or invalidation is needed:
+// such a fence costs one L2-wide operation, and hundreds of workgroups issuing
+// them at once on one XCD serialise behind each other.
 
-__device__ __forceinline__ uint32_t load_acquire(const uint32_t* p) {
-    return __hip_atomic_load(p, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_AGENT);
-}
+// Wait until this wave's outstanding memory operations have completed (stores
+// acknowledged by the coherence point). The asm is opaque to the compiler, so
+// no memory access moves across it.
+__device__ __forceinline__ void wait_own_stores() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
 
-__device__ __forceinline__ void add_release(uint32_t* p, uint32_t v) {
-    __hip_atomic_fetch_add(p, v, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
-}
-
-// Publish: every wave's stores complete and are made visible at agent scope
-// before thread 0 bumps the counter.
 __device__ __forceinline__ void publish(uint32_t* counter) {
-    __threadfence();
+    wait_own_stores();
     __syncthreads();
-    if (threadIdx.x == 0) add_release(counter, 1u);
+    if (threadIdx.x == 0) __hip_atomic_fetch_add(as_global_rw(counter), 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // Thread 0 spins until *counter >= target, bounded by a wall-clock limit and
@@ -186,10 +317,10 @@ __device__ __forceinline__ bool wait_at_least(const uint32_t* counter, uint32_t 
                                               int32_t* lds_flag) {
     if (threadIdx.x == 0) {
         int32_t ok = 1;
-        if (load_acquire(counter) < target) {
+        if (coherent_load(counter) < target) {
             uint64_t start = wall_clock64();
-            while (load_acquire(counter) < target) {
-                if (__hip_atomic_load(error, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0) {
+            while (coherent_load(counter) < target) {
+                if (coherent_load(error) != 0) {
                     ok = 0;
                     break;
                 }
@@ -207,7 +338,6 @@ __device__ __forceinline__ bool wait_at_least(const uint32_t* counter, uint32_t 
     }
     __syncthreads();
     int32_t ok = *lds_flag;
-    __threadfence();
     __syncthreads();
     return ok != 0;
 }

@@ -102,7 +102,8 @@ void download(void* dst, const void* src, size_t bytes, hipStream_t s) {
 namespace fw {
 
 // out[t][r] = bf16(tree32(W[r,:], x[t,:])) for NT tokens; 4 rows per wave,
-// 16 rows per 256-thread block; x staged in LDS as f32 (dynamic shared).
+// 16 rows per 256-thread block; x staged in LDS as f32 (dynamic shared). The
+// row is swept in chunks of 32 blocks, each chunk's loads issued together.
 template <int NT>
 __global__ void __launch_bounds__(256) k_linear_tree32(const uint16_t* __restrict__ w,
                                                        const uint16_t* __restrict__ x, int rows,
@@ -118,9 +119,17 @@ __global__ void __launch_bounds__(256) k_linear_tree32(const uint16_t* __restric
     const int q = lane % kLanesPerRow;
     const bool ok = g < valid;
     const int r = ok ? row0 + g : row0;
+    const uint32_t* wrow = reinterpret_cast<const uint32_t*>(w + (size_t)r * K);
     float acc[NT][2];
-    tree32_sweep<NT, 8>(reinterpret_cast<const uint32_t*>(w + (size_t)r * K), K / 32, xs, K, q,
-                        ok ? (1u << NT) - 1u : 0u, acc);
+#pragma unroll
+    for (int t = 0; t < NT; ++t) acc[t][0] = acc[t][1] = 0.0f;
+    const int nblocks = K / 32;
+    for (int b0 = 0; b0 < nblocks; b0 += 32) {
+        const int nb = min(32, nblocks - b0);
+        RowShare<32> rs;
+        row_issue(rs, wrow + b0 * 16, nb, q);
+        row_chains_acc<NT, 32>(rs, nb, xs + b0 * 32, K, q, acc);
+    }
 #pragma unroll
     for (int t = 0; t < NT; ++t) {
         float d = tree32_reduce(acc[t][0], acc[t][1]);
@@ -288,12 +297,17 @@ struct firewing_hip_context {
     DecodeLayer* d_layers = nullptr;  // [L]
     uint16_t* d_weight_table = nullptr;
     // decode scratch sized for L layers and T <= 4
-    uint16_t *x = nullptr, *out = nullptr, *logits = nullptr, *scores = nullptr, *sig = nullptr;
-    uint16_t *shared_act = nullptr, *act = nullptr, *token_weights = nullptr;
+    uint16_t *x = nullptr, *out = nullptr, *logits = nullptr, *scores = nullptr;
+    uint16_t *shared_act = nullptr, *act = nullptr, *h = nullptr;
+    uint32_t *token_weights = nullptr, *sig = nullptr;
     int32_t *ids = nullptr, *slot_expert = nullptr, *union_count = nullptr, *token_slots = nullptr;
     uint32_t *slot_tokens = nullptr, *counters = nullptr;
     int32_t* error = nullptr;
     int grid[kMaxTokens + 1] = {0};
+    uint64_t* trace = nullptr;  // profiling builds: per-task timestamps of the next launch
+    DecodeParams* d_params = nullptr;  // device copy of the last launch's parameters
+    DecodeParams last_params{};
+    bool params_valid = false;
     double timeout_seconds = 10.0;  // per dependency wait (FIREWING_WAIT_TIMEOUT_S)
 };
 
@@ -306,6 +320,10 @@ T* dalloc(size_t count) {
     return static_cast<T*>(p);
 }
 
+// Row stride of the logit scratch: the E router logits, padded to an even
+// count, then the shared_expert_gate logit and a zero (32-bit aligned pairs).
+size_t logit_stride(size_t E) { return ((E + 1) & ~(size_t)1) + 2; }
+
 bool validate_shape(const firewing_hip_shape& s, std::string* why) {
     auto bad = [&](const char* m) {
         *why = m;
@@ -313,10 +331,10 @@ bool validate_shape(const firewing_hip_shape& s, std::string* why) {
     };
     if (s.hidden == 0 || s.hidden % 32 || s.hidden > (size_t)kMaxHidden)
         return bad("hidden must be a nonzero multiple of 32 and <= 2560");
-    if (s.intermediate == 0 || s.intermediate % 32 || s.intermediate > 4096)
-        return bad("intermediate must be a nonzero multiple of 32 and <= 4096");
-    if (s.shared_intermediate == 0 || s.shared_intermediate % 32 || s.shared_intermediate > 4096)
-        return bad("shared_intermediate must be a nonzero multiple of 32 and <= 4096");
+    if (s.intermediate == 0 || s.intermediate % 32 || s.intermediate > 1024)
+        return bad("intermediate must be a nonzero multiple of 32 and <= 1024");
+    if (s.shared_intermediate == 0 || s.shared_intermediate % 32 || s.shared_intermediate > 1024)
+        return bad("shared_intermediate must be a nonzero multiple of 32 and <= 1024");
     if (s.experts == 0 || s.experts > (size_t)kMaxExperts) return bad("experts must be in [1, 1024]");
     if (s.top_k == 0 || s.top_k > (size_t)kMaxTopK || s.top_k > s.experts)
         return bad("top_k must be in [1, min(32, experts)]");
@@ -324,10 +342,30 @@ bool validate_shape(const firewing_hip_shape& s, std::string* why) {
     return true;
 }
 
-template <int NT>
-int decode_grid(const firewing_hip_context* c) {
+// Kernel variant for T tokens and the context's block counts: hidden rows of
+// up to 64 blocks (H <= 2048) or 80 (H <= 2560); down rows of up to 16 blocks
+// (I, Is <= 512) or 32 (<= 1024).
+const void* decode_kernel(const firewing_hip_context* c, int T) {
+    const bool wide_h = c->shape.hidden > 2048;
+    const bool wide_i = std::max(c->shape.intermediate, c->shape.shared_intermediate) > 512;
+#define FW_DECODE_VARIANT(NT)                                                                  \
+    if (T == NT) {                                                                             \
+        if (!wide_h && !wide_i) return reinterpret_cast<const void*>(&k_moe_decode<NT, 64, 16>); \
+        if (!wide_h && wide_i) return reinterpret_cast<const void*>(&k_moe_decode<NT, 64, 32>);  \
+        if (wide_h && !wide_i) return reinterpret_cast<const void*>(&k_moe_decode<NT, 80, 16>);  \
+        return reinterpret_cast<const void*>(&k_moe_decode<NT, 80, 32>);                         \
+    }
+    FW_DECODE_VARIANT(1)
+    FW_DECODE_VARIANT(2)
+    FW_DECODE_VARIANT(3)
+    FW_DECODE_VARIANT(4)
+#undef FW_DECODE_VARIANT
+    throw HipError{"no decode kernel for this token count"};
+}
+
+int decode_grid(const firewing_hip_context* c, int T) {
     int per_cu = 0;
-    check(hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, k_moe_decode<NT>, 256, 0),
+    check(hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, decode_kernel(c, T), 256, 0),
           "hipOccupancyMaxActiveBlocksPerMultiprocessor");
     if (per_cu < 1) throw HipError{"decode kernel cannot be resident"};
     return per_cu * c->cu_count;
@@ -336,7 +374,8 @@ int decode_grid(const firewing_hip_context* c) {
 // Launch the persistent kernel over layers [first, first + n) for T tokens.
 // x[0] of the scratch must already hold the input.
 void launch_decode(firewing_hip_context* c, size_t first, size_t n, int T, int order,
-                   bool bias_feature, const uint16_t* x_in, uint16_t* x_final, hipStream_t s) {
+                   bool prenorm, bool bias_feature, const uint16_t* x_in, uint16_t* x_final,
+                   hipStream_t s) {
     const firewing_hip_shape& sh = c->shape;
     DecodeParams p{};
     p.layers = c->d_layers + first;
@@ -348,6 +387,7 @@ void launch_decode(firewing_hip_context* c, size_t first, size_t n, int T, int o
     p.K = (int)sh.top_k;
     p.Is = (int)sh.shared_intermediate;
     p.order = order;
+    p.prenorm = prenorm ? 1 : 0;
     p.bias_feature = bias_feature ? 1 : 0;
     p.S = p.K * T;
     const size_t L = n, Tn = (size_t)T, H = sh.hidden, E = sh.experts, K = sh.top_k;
@@ -355,8 +395,11 @@ void launch_decode(firewing_hip_context* c, size_t first, size_t n, int T, int o
     p.x_in = x_in;
     p.x = c->x;
     p.x_final = x_final;
+    p.h = c->h;
     p.out = c->out;
     p.logits = c->logits;
+    p.ls = (int)logit_stride(E);
+    p.gi = p.ls - 2;
     p.ids = c->ids;
     p.scores = c->scores;
     p.slot_expert = c->slot_expert;
@@ -374,19 +417,28 @@ void launch_decode(firewing_hip_context* c, size_t first, size_t n, int T, int o
     p.n_shared = (int)((Is + kPairsPerTask - 1) / kPairsPerTask);
     p.n_b = (int)(S * (I / kPairsPerTask));
     p.n_c = (int)(H / kRowsPerCTask);
-    p.per_layer = p.n_router + p.n_shared + 1 + p.n_b + p.n_c;
+    p.n_rows = p.n_router + p.n_shared + p.n_b;
     (void)L;
     (void)Tn;
     (void)K;
-    void* args[] = {&p};
-    const void* fn = nullptr;
-    int grid = 0;
-    switch (T) {
-        case 1: fn = reinterpret_cast<const void*>(&k_moe_decode<1>); grid = c->grid[1]; break;
-        case 2: fn = reinterpret_cast<const void*>(&k_moe_decode<2>); grid = c->grid[2]; break;
-        case 3: fn = reinterpret_cast<const void*>(&k_moe_decode<3>); grid = c->grid[3]; break;
-        default: fn = reinterpret_cast<const void*>(&k_moe_decode<4>); grid = c->grid[4]; break;
+    // Roles: one workgroup selects experts; the combine role gets one
+    // workgroup per C task of a layer where the grid allows (so every task's
+    // down rows are in flight before the gate/up phase ends), at most half.
+    const int grid = c->grid[T];
+    p.g_comb = std::min(p.n_c, (grid - 1) / 2);
+    p.g_rows = grid - 1 - p.g_comb;
+    if (p.g_comb < 1 || p.g_rows < 1) throw HipError{"decode grid too small for its roles"};
+    p.trace = c->trace;
+    // The kernel reads its parameters from a device copy; upload only on change
+    // (the copy is stream-ordered before the launch; pageable source, staged).
+    if (std::memcmp(&p, &c->last_params, sizeof p) != 0 || !c->params_valid) {
+        check(hipMemcpyAsync(c->d_params, &p, sizeof p, hipMemcpyHostToDevice, s), "upload decode params");
+        c->last_params = p;
+        c->params_valid = true;
     }
+    const DecodeParams* dp = c->d_params;
+    void* args[] = {&dp};
+    const void* fn = decode_kernel(c, T);
     check(hipLaunchCooperativeKernel(fn, dim3(grid), dim3(256), args, 0, s),
           "hipLaunchCooperativeKernel(k_moe_decode)");
 }
@@ -653,25 +705,24 @@ bool firewing_hip_create(const firewing_hip_shape* shape, firewing_hip_context**
         const size_t T = kMaxTokens, S = K * T;
         c->x = dalloc<uint16_t>((L + 1) * T * H);
         c->out = dalloc<uint16_t>(L * T * H);
-        c->logits = dalloc<uint16_t>(L * T * (E + 1));
+        c->logits = dalloc<uint16_t>(L * T * logit_stride(E));
         c->ids = dalloc<int32_t>(L * T * K);
         c->scores = dalloc<uint16_t>(L * T * K);
         c->slot_expert = dalloc<int32_t>(L * S);
         c->slot_tokens = dalloc<uint32_t>(L * S);
         c->union_count = dalloc<int32_t>(L);
         c->token_slots = dalloc<int32_t>(L * T * K);
-        c->token_weights = dalloc<uint16_t>(L * T * K);
-        c->sig = dalloc<uint16_t>(L * T);
+        c->token_weights = dalloc<uint32_t>(L * T * K);
+        c->sig = dalloc<uint32_t>(L * T);
         c->shared_act = dalloc<uint16_t>(L * T * Is);
+        c->h = dalloc<uint16_t>(L * T * H);
         c->act = dalloc<uint16_t>(L * S * T * I);
         c->counters = dalloc<uint32_t>(L * kCountersPerLayer + 1);
         c->error = dalloc<int32_t>(1);
+        c->d_params = dalloc<DecodeParams>(1);
         check(hipMemset(c->counters, 0, (L * kCountersPerLayer + 1) * 4), "hipMemset counters");
         check(hipMemset(c->error, 0, 4), "hipMemset error");
-        c->grid[1] = decode_grid<1>(c);
-        c->grid[2] = decode_grid<2>(c);
-        c->grid[3] = decode_grid<3>(c);
-        c->grid[4] = decode_grid<4>(c);
+        for (int t = 1; t <= kMaxTokens; ++t) c->grid[t] = decode_grid(c, t);
         // zero the banks so uninstalled layers are defined
         for (size_t l = 0; l < L; ++l) {
             check(hipMemsetAsync(c->router[l], 0, (E + 1) * H * 2, c->stream), "hipMemsetAsync");
@@ -704,7 +755,8 @@ void firewing_hip_destroy(firewing_hip_context* c) {
     freev(c->shared_down);
     void* bufs[] = {c->d_layers, c->d_weight_table, c->x, c->out, c->logits, c->ids, c->scores,
                     c->slot_expert, c->slot_tokens, c->union_count, c->token_slots,
-                    c->token_weights, c->sig, c->shared_act, c->act, c->counters, c->error};
+                    c->token_weights, c->sig, c->shared_act, c->act, c->counters, c->error,
+                    c->d_params, c->h};
     for (void* b : bufs)
         if (b) (void)hipFree(b);
     if (c->stream) (void)hipStreamDestroy(c->stream);
@@ -926,10 +978,11 @@ bool firewing_hip_sparse_moe_block_dev(firewing_hip_context* c, size_t layer,
         std::string why;
         if (!step_args_ok(c, tokens, order, &why)) return fail("sparse_moe_block: " + why);
         if (!hidden || !out) return fail("sparse_moe_block: null pointer");
+        if (reinterpret_cast<uintptr_t>(hidden) % 4) return fail("sparse_moe_block: hidden must be 4-byte aligned");
         if (layer >= c->shape.layers) return fail("sparse_moe_block: layer out of range");
         hipStream_t s = stream ? static_cast<hipStream_t>(stream) : c->stream;
         const size_t H = c->shape.hidden;
-        launch_decode(c, layer, 1, (int)tokens, order, false, hidden, nullptr, s);
+        launch_decode(c, layer, 1, (int)tokens, order, false, false, hidden, nullptr, s);
         check(hipMemcpyAsync(out, c->out, tokens * H * 2, hipMemcpyDeviceToDevice, s), "copy output");
         return true;
     });
@@ -946,13 +999,13 @@ bool firewing_hip_sparse_moe_block(firewing_hip_context* c, size_t layer,
         hipStream_t s = c->stream;
         const size_t H = c->shape.hidden, E = c->shape.experts, K = c->shape.top_k;
         upload(c->x, hidden, tokens * H * 2, s);
-        launch_decode(c, layer, 1, (int)tokens, order, false, c->x, nullptr, s);
+        launch_decode(c, layer, 1, (int)tokens, order, false, false, c->x, nullptr, s);
         if (!check_device_error(c, s)) return false;
         download(out, c->out, tokens * H * 2, s);
         if (cap) {
             if (cap->router_logits) {
                 for (size_t t = 0; t < tokens; ++t)
-                    download(cap->router_logits + t * E, c->logits + t * (E + 1), E * 2, s);
+                    download(cap->router_logits + t * E, c->logits + t * logit_stride(E), E * 2, s);
             }
             if (cap->selected_experts) {
                 std::vector<int32_t> ids(tokens * K);
@@ -961,7 +1014,12 @@ bool firewing_hip_sparse_moe_block(firewing_hip_context* c, size_t layer,
                 for (size_t i = 0; i < ids.size(); ++i) cap->selected_experts[i] = (size_t)ids[i];
             }
             if (cap->selected_scores) download(cap->selected_scores, c->scores, tokens * K * 2, s);
-            if (cap->shared_gate_sigmoid) download(cap->shared_gate_sigmoid, c->sig, tokens * 2, s);
+            if (cap->shared_gate_sigmoid) {
+                uint32_t sig[kMaxTokens];
+                download(sig, c->sig, tokens * 4, s);
+                check(hipStreamSynchronize(s), "hipStreamSynchronize");
+                for (size_t t = 0; t < tokens; ++t) cap->shared_gate_sigmoid[t] = (uint16_t)sig[t];
+            }
             if (cap->routed_mixture) return fail("sparse_moe_block: routed_mixture capture is not kept by the fused kernel");
         }
         check(hipStreamSynchronize(s), "hipStreamSynchronize");
@@ -977,9 +1035,11 @@ bool firewing_hip_moe_step_dev(firewing_hip_context* c, const uint16_t* hidden, 
         std::string why;
         if (!step_args_ok(c, tokens, order, &why)) return fail("moe_step: " + why);
         if (!hidden || !residual) return fail("moe_step: null pointer");
+        if (reinterpret_cast<uintptr_t>(hidden) % 4 || reinterpret_cast<uintptr_t>(residual) % 4)
+            return fail("moe_step: hidden and residual must be 4-byte aligned");
         hipStream_t s = stream ? static_cast<hipStream_t>(stream) : c->stream;
         const size_t L = c->shape.layers, H = c->shape.hidden, K = c->shape.top_k;
-        launch_decode(c, 0, L, (int)tokens, order, bias_feature, hidden, residual, s);
+        launch_decode(c, 0, L, (int)tokens, order, true, bias_feature, hidden, residual, s);
         if (block_out)
             check(hipMemcpyAsync(block_out, c->out, L * tokens * H * 2, hipMemcpyDeviceToDevice, s),
                   "copy block outputs");
@@ -1002,7 +1062,7 @@ bool firewing_hip_moe_step(firewing_hip_context* c, const uint16_t* hidden, size
         hipStream_t s = c->stream;
         const size_t L = c->shape.layers, H = c->shape.hidden, K = c->shape.top_k;
         upload(c->x, hidden, tokens * H * 2, s);
-        launch_decode(c, 0, L, (int)tokens, order, bias_feature, c->x, nullptr, s);
+        launch_decode(c, 0, L, (int)tokens, order, true, bias_feature, c->x, nullptr, s);
         if (!check_device_error(c, s)) return false;
         download(residual, c->x + L * tokens * H, tokens * H * 2, s);
         if (block_out) download(block_out, c->out, L * tokens * H * 2, s);
@@ -1012,6 +1072,34 @@ bool firewing_hip_moe_step(firewing_hip_context* c, const uint16_t* hidden, size
         return true;
     });
 }
+
+#ifdef FW_DECODE_TRACE
+// Profiling builds only: run one step with per-task timestamps and copy them
+// out ([tasks][4]: start, dependency met, end, workgroup << 8 | kind).
+extern "C" bool firewing_hip_debug_traced_step(firewing_hip_context* c, const uint16_t* hidden,
+                                               size_t tokens, uint64_t* out, size_t cap,
+                                               size_t* tasks) {
+    return guarded([&] {
+        const size_t L = c->shape.layers, H = c->shape.hidden;
+        const size_t E = c->shape.experts, K = c->shape.top_k, I = c->shape.intermediate;
+        const size_t Is = c->shape.shared_intermediate;
+        size_t per_layer = (E + 15) / 16 + 1 + (Is + 7) / 8 + 1 + K * tokens * (I / 8) + H / 4;
+        size_t n = L * per_layer;
+        if (cap < n * kTraceWords) return fail("trace buffer too small");
+        c->trace = dalloc<uint64_t>(n * kTraceWords);
+        check(hipMemset(c->trace, 0, n * kTraceWords * 8), "hipMemset trace");
+        upload(c->x, hidden, tokens * H * 2, c->stream);
+        launch_decode(c, 0, L, (int)tokens, 0, true, true, c->x, nullptr, c->stream);
+        bool ok = check_device_error(c, c->stream);
+        download(out, c->trace, n * kTraceWords * 8, c->stream);
+        check(hipStreamSynchronize(c->stream), "hipStreamSynchronize");
+        (void)hipFree(c->trace);
+        c->trace = nullptr;
+        *tasks = n;
+        return ok;
+    });
+}
+#endif
 
 bool firewing_hip_synchronize(firewing_hip_context* c) {
     return guarded([&] {

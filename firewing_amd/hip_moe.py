@@ -15,7 +15,7 @@ Names and argument meanings follow the Rust functions they replace:
 Errors come back as ``FirewingError`` carrying the library's message, as the
 Rust wrappers map ``false`` to ``Err(String)`` (src/decoder_layer.rs:28-39).
 bf16 values are numpy ``uint16`` bit patterns; ``*_dev`` methods take device
-addresses (ints or torch tensors on the GPU).
+addresses (ints, or objects with a ``data_ptr()``).
 
 Importing this module loads the HIP library and fails loudly if it is absent:
 there is no CPU fallback.

@@ -160,11 +160,14 @@ bool firewing_hip_sparse_moe_block_dev(firewing_hip_context* ctx, size_t layer,
                                        const uint16_t* hidden, size_t tokens, int order,
                                        uint16_t* out, void* stream);
 
-/* All resident layers for T <= 4 tokens in one persistent launch, chained by
- * the residual stream x_{l+1} = add_bf16(x_l, block_l(x_l)) (x_{l+1}[H-1] reset
- * to 1.0 when bias_feature): the 48-layer decode step the overlap benches
- * emulate with 48 execute_exact() calls (src/overlap_bound.rs:732-734).
- * Device pointers: hidden [T, H] in, residual [T, H] out; block_out
+/* All resident layers for T <= 4 tokens in one persistent launch: the
+ * 48-layer decode step the overlap benches emulate with 48 execute_exact()
+ * calls (src/overlap_bound.rs:732-734). Layers are chained by a pre-norm
+ * residual stream, r_0 = hidden, h_l = rms_norm(r_l) (h_l[H-1] = 1.0 when
+ * bias_feature), r_{l+1} = add_bf16(r_l, block_l(h_l)), where rms_norm is
+ * bf16(r / sqrt(dot(r, r) / H + 1e-6)) with the reference's dot order; this
+ * glue stands in for the rest of the decoder layer, which is not built here.
+ * Device pointers: hidden [T, H] in, residual r_L [T, H] out; block_out
  * [L, T, H], ids [L, T, K] (int32) and scores [L, T, K] may be NULL. */
 bool firewing_hip_moe_step_dev(firewing_hip_context* ctx, const uint16_t* hidden, size_t tokens,
                                int order, bool bias_feature, uint16_t* residual,

@@ -147,6 +147,18 @@ uint16_t fwo_add_bf16(uint16_t left, uint16_t right) {
     return fwo_to_bf16(fwo_from_bf16(left) + fwo_from_bf16(right));
 }
 
+/* Workload glue, not part of the reference's block: the pre-norm of a decoder
+ * layer, h = bf16(r * 1/sqrt(mean(r^2) + 1e-6)) with mean(r^2) taken through
+ * the reference's own dot (pytorch_bf16_vector_dot(r, r), src/expert.rs:514)
+ * divided by H; h[H-1] = 1.0 when the router-bias feature is on. */
+void fwo_rms_norm_bf16(const uint16_t* r, size_t n, int bias_feature, uint16_t* h) {
+    float ss = fwo_dot_tree32(r, r, n);
+    float ms = ss / (float)n;
+    float inv = 1.0f / sqrtf(ms + 1e-6f);
+    for (size_t i = 0; i < n; ++i) h[i] = fwo_to_bf16(fwo_from_bf16(r[i]) * inv);
+    if (bias_feature) h[n - 1] = 0x3f80u;
+}
+
 /* src/metal_moe.rs:385-392 build_silu_lut: LUT[b] = bf16(silu(from_bf16(b))). */
 void fwo_build_silu_lut(uint16_t* lut) {
     for (uint32_t bits = 0; bits < 65536u; ++bits) {
@@ -615,9 +627,9 @@ int fwo_synth_block(const fwo_shape* shape, const fwo_synth_config* config, uint
 }
 
 /* Chained decode step over `layers` synthetic layers. Workload glue, not in the
- * reference: the residual stream x_{l+1}[h] = add_bf16(x_l[h], block_l(x_l)[h])
- * (the residual add of src/decoder_layer.rs:601-606 with unit injection), with
- * x_{l+1}[H-1] reset to 1.0 when the router-bias feature is on. */
+ * reference: a pre-norm residual stream, h_l = rms_norm(r_l) (fwo_rms_norm_bf16),
+ * r_{l+1}[i] = add_bf16(r_l[i], block_l(h_l)[i]) (the residual add of
+ * src/decoder_layer.rs:601-606 with unit injection). r_0 = hidden. */
 int fwo_synth_step(const fwo_shape* shape, const fwo_synth_config* config, uint32_t layers,
                    const uint16_t* hidden, size_t tokens, uint16_t* residual_out,
                    uint16_t* block_out, int32_t* ids, uint16_t* scores) {
@@ -629,18 +641,20 @@ int fwo_synth_step(const fwo_shape* shape, const fwo_synth_config* config, uint3
         free(o);
         return 0;
     }
+    uint16_t* hn = (uint16_t*)malloc(tokens * H * sizeof(uint16_t));
     memcpy(x, hidden, tokens * H * sizeof(uint16_t));
-    int ok = 1;
+    int ok = hn != NULL;
     for (uint32_t l = 0; ok && l < layers; ++l) {
-        ok = fwo_synth_block(shape, config, l, x, tokens, o, ids ? ids + (size_t)l * tokens * K : NULL,
+        for (size_t t = 0; t < tokens; ++t) fwo_rms_norm_bf16(x + t * H, H, config->bias_feature, hn + t * H);
+        ok = fwo_synth_block(shape, config, l, hn, tokens, o, ids ? ids + (size_t)l * tokens * K : NULL,
                              scores ? scores + (size_t)l * tokens * K : NULL, NULL);
         if (!ok) break;
         if (block_out) memcpy(block_out + (size_t)l * tokens * H, o, tokens * H * sizeof(uint16_t));
         for (size_t t = 0; t < tokens; ++t) {
             for (size_t h = 0; h < H; ++h) x[t * H + h] = fwo_add_bf16(x[t * H + h], o[t * H + h]);
-            if (config->bias_feature) x[t * H + H - 1] = 0x3f80u;
         }
     }
+    free(hn);
     if (ok && residual_out) memcpy(residual_out, x, tokens * H * sizeof(uint16_t));
     free(x);
     free(o);
@@ -667,15 +681,17 @@ int fwo_synth_step_timed(const fwo_shape* shape, const fwo_synth_config* config,
     int32_t* sel = (int32_t*)malloc(tokens * K * sizeof(int32_t));
     uint16_t* sc = (uint16_t*)malloc(tokens * K * sizeof(uint16_t));
     uint16_t* lg = (uint16_t*)malloc(tokens * E * sizeof(uint16_t));
-    int ok = x && o && sel && sc && lg;
+    uint16_t* hn = (uint16_t*)malloc(tokens * H * sizeof(uint16_t));
+    int ok = x && o && sel && sc && lg && hn;
     double timed = 0.0;
     if (ok) memcpy(x, hidden, tokens * H * sizeof(uint16_t));
     for (uint32_t l = 0; ok && l < layers; ++l) {
         synth_layer L;
         ok = synth_layer_dense(shape, config, l, &L);
         double t0 = now_seconds();
+        for (size_t t = 0; t < tokens; ++t) fwo_rms_norm_bf16(x + t * H, H, config->bias_feature, hn + t * H);
         for (size_t t = 0; ok && t < tokens; ++t) {
-            ok = fwo_route(L.router, x + t * H, E, H, K, config->order, sel + t * K, lg + t * E,
+            ok = fwo_route(L.router, hn + t * H, E, H, K, config->order, sel + t * K, lg + t * E,
                            sc + t * K);
         }
         timed += now_seconds() - t0;
@@ -686,12 +702,11 @@ int fwo_synth_step_timed(const fwo_shape* shape, const fwo_synth_config* config,
         for (size_t t = 0; ok && t < tokens; ++t) {
             ok = block_core(shape, L.router, (const uint16_t* const*)L.gate_up,
                             (const uint16_t* const*)L.down, L.shared_gate, L.shared_up,
-                            L.shared_down, L.shared_expert_gate, x + t * H, config->order,
+                            L.shared_down, L.shared_expert_gate, hn + t * H, config->order,
                             sel + t * K, lg + t * E, o + t * H, NULL);
         }
         for (size_t t = 0; ok && t < tokens; ++t) {
             for (size_t h = 0; h < H; ++h) x[t * H + h] = fwo_add_bf16(x[t * H + h], o[t * H + h]);
-            if (config->bias_feature) x[t * H + H - 1] = 0x3f80u;
         }
         timed += now_seconds() - t0;
         synth_layer_free(&L);
@@ -703,5 +718,6 @@ int fwo_synth_step_timed(const fwo_shape* shape, const fwo_synth_config* config,
     free(sel);
     free(sc);
     free(lg);
+    free(hn);
     return ok;
 }

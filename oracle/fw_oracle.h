@@ -43,6 +43,7 @@ void fwo_swiglu_bf16(const uint16_t* gate, const uint16_t* up, size_t n, uint16_
 uint16_t fwo_sigmoid_bf16(uint16_t value);
 uint16_t fwo_add_bf16(uint16_t left, uint16_t right);
 void fwo_build_silu_lut(uint16_t* lut);
+void fwo_rms_norm_bf16(const uint16_t* r, size_t n, int bias_feature, uint16_t* h);
 int fwo_make_hidden(size_t size, int64_t multiplier, int64_t add, int64_t modulus,
                     int64_t center, int64_t divisor, size_t sparse_stride, uint16_t* out);
 

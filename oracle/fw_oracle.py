@@ -105,6 +105,7 @@ def lib() -> ctypes.CDLL:
         L.fwo_add_bf16.restype = ctypes.c_uint16
         L.fwo_add_bf16.argtypes = [ctypes.c_uint16, ctypes.c_uint16]
         L.fwo_build_silu_lut.argtypes = [_u16p]
+        L.fwo_rms_norm_bf16.argtypes = [_u16p, _size, ctypes.c_int, _u16p]
         L.fwo_make_hidden.restype = ctypes.c_int
         L.fwo_make_hidden.argtypes = [_size] + [ctypes.c_int64] * 5 + [_size, _u16p]
         L.fwo_topk_total_order.restype = ctypes.c_int
@@ -232,6 +233,14 @@ def add_bf16(left: int, right: int) -> int:
 def silu_lut() -> np.ndarray:
     out = np.empty(65536, dtype=np.uint16)
     lib().fwo_build_silu_lut(_p16(out))
+    return out
+
+
+def rms_norm_bf16(r, bias_feature: bool = False) -> np.ndarray:
+    """Pre-norm of the chained workload (not part of the reference block)."""
+    a = _u16(r)
+    out = np.empty(a.size, dtype=np.uint16)
+    lib().fwo_rms_norm_bf16(_p16(a), a.size, int(bias_feature), _p16(out))
     return out
 
 
@@ -409,7 +418,7 @@ def synth_block(shape: dict, seed: int, layer: int, hidden: np.ndarray, bias_fea
 
 def synth_step(shape: dict, seed: int, layers: int, hidden: np.ndarray, bias_feature=True,
                order=ORDER_TREE32, threads: int | None = None):
-    """Chained residual decode step; returns (x_L, block outputs, ids, scores)."""
+    """Pre-norm residual decode step; returns (r_L, block outputs, ids, scores)."""
     h = _u16(hidden)
     T = h.shape[0]
     H, K = shape["hidden"], shape["top_k"]
