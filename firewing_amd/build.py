@@ -39,16 +39,34 @@ def hipcc() -> str:
     return path
 
 
-def build(verbose: bool = False) -> Path:
-    sources = [CSRC / "fw_moe.hip"]
-    tmp = LIB.with_suffix(".so.tmp")
-    cmd = [hipcc(), *HIPCC_FLAGS, "-I", str(ROOT / "include"), "-I", str(CSRC),
-           *map(str, sources), "-o", str(tmp)]
+def _compile(args: list[str], verbose: bool) -> None:
     if verbose:
-        print(" ".join(cmd), flush=True)
-    res = subprocess.run(cmd, capture_output=True, text=True)
+        print(" ".join(args), flush=True)
+    res = subprocess.run(args, capture_output=True, text=True)
     if res.returncode != 0:
         raise RuntimeError(f"hipcc failed ({res.returncode}):\n{res.stderr[-6000:]}")
+
+
+def build(verbose: bool = False) -> Path:
+    """Compile the host/stateless translation unit and one decode-kernel unit
+    per token count in parallel, then link the shared library in place."""
+    from concurrent.futures import ThreadPoolExecutor
+
+    out_dir = PKG / "_build"
+    out_dir.mkdir(exist_ok=True)
+    include = ["-I", str(ROOT / "include"), "-I", str(CSRC)]
+    compile_flags = [f for f in HIPCC_FLAGS if f != "-shared"]
+    units = [(CSRC / "fw_moe.hip", [], out_dir / "fw_moe.o")]
+    for nt in (1, 2, 3, 4):
+        units.append((CSRC / "fw_decode_kernels.hip", [f"-DFW_NT={nt}"], out_dir / f"fw_decode_t{nt}.o"))
+    jobs = [[hipcc(), *compile_flags, *include, *defs, "-c", str(src), "-o", str(obj)] for src, defs, obj in units]
+    workers = max(1, min(len(jobs), os.cpu_count() or 1))
+    with ThreadPoolExecutor(max_workers=workers) as pool:
+        for f in [pool.submit(_compile, j, verbose) for j in jobs]:
+            f.result()
+    tmp = LIB.with_suffix(".so.tmp")
+    _compile([hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", *[str(o) for _, _, o in units], "-o", str(tmp)],
+             verbose)
     os.replace(tmp, LIB)
     return LIB
 

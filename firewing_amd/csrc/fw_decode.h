@@ -2,27 +2,32 @@
 // launch (router -> top-k -> routed and shared SwiGLU experts -> ordered
 // mixture -> combine, chained through the residual stream).
 //
-// The co-resident workgroups (cooperative launch) are split into three roles,
+// The co-resident workgroups (cooperative launch) are split into two roles,
 // each walking its own task list in (layer, phase) order:
 //
 //   rows     R  router rows, 16 per task (rows [0, E)), plus one task for the
-//               shared_expert_gate row                -> logits[t][0..E]
+//               shared_expert_gate row                  -> logits
 //            S  shared gate/up pairs, 8 per task, fused SwiGLU -> shared_act
-//            B  routed gate/up pairs, 8 per task per slot, fused SwiGLU -> act
-//   combine  C  4 hidden rows per task: the down rows of every selected
-//               expert ("slot") and of the shared expert, route weighting, the
-//               ascending-id bf16 mixture, the gated shared output, the block
-//               output and the next residual
-//   top-k    K  one workgroup: ids, the union of selected experts, scores and
-//               the shared-gate sigmoid of every layer
+//            B  routed gate/up pairs, 8 per task of one selected expert
+//               ("slot"), fused SwiGLU                 -> act
+//   combine  C  4 hidden rows per task: the down rows of the shared expert and
+//               of every slot, route weighting, the ascending-id bf16 mixture,
+//               the gated shared output, the block output and the next
+//               residual                                -> out, residual
 //
-// R and S of layer l wait for C of layer l-1; K waits for R; B for K's ids; C
-// for B, S and K's scores. Every wait points to an earlier phase, and within
-// a role earlier phases come first, so with all workgroups resident the
-// earliest unfinished task can always run. Weight loads never depend on
-// activations, so tasks issue them before they wait: R and S stream their rows
-// while the previous layer finishes, C its down rows while B runs. Waits are
-// counters in HBM (fw_device.h), each bounded by a wall-clock limit and by a
+// Expert selection (top-k, the union of the tokens' experts in ascending id,
+// scores, the shared-gate sigmoid) is recomputed from the logits by every B
+// and C workgroup that needs it: a few microseconds of LDS work instead of a
+// further hop through memory.
+//
+// R and S of layer l wait for C of layer l-1; B and C for R; C also for B and
+// S. Every wait points to an earlier phase, and within a role earlier phases
+// come first, so with all workgroups resident the earliest unfinished task can
+// always run. Weight loads never depend on activations, so tasks issue them
+// before they wait: R and S stream their rows while the previous layer
+// finishes, C its shared down rows at once and its routed down rows as soon as
+// the selection is known, while B runs. Phase counters and tagged data words
+// follow fw_device.h; every wait is bounded by a wall-clock limit and by a
 // shared error word, so a failure ends the launch instead of hanging it. The
 // last workgroup to finish zeroes the counters for the next launch.
 #pragma once
@@ -43,14 +48,12 @@ struct DecodeLayer {
 enum DecodeCounter : int {
     kCntRouter = 0,
     kCntShared = 1,
-    kCntIds = 2,
-    kCntScores = 3,
-    kCntB = 4,
-    kCntC = 5,
-    kCountersPerLayer = 8
+    kCntB = 2,
+    kCntC = 3,
+    kCountersPerLayer = 4
 };
 
-enum DecodeTaskKind : int { kTaskRouter = 0, kTaskShared = 1, kTaskTopk = 2, kTaskGateUp = 3, kTaskDown = 4 };
+enum DecodeTaskKind : int { kTaskRouter = 0, kTaskShared = 1, kTaskGateUp = 3, kTaskDown = 4 };
 
 constexpr int kRouterRowsPerTask = 16;
 constexpr int kPairsPerTask = 8;
@@ -61,7 +64,11 @@ constexpr int kMaxSlots = kMaxTopK * kMaxTokens;
 constexpr int kMaxHidden = 2560;
 constexpr int kMaxExperts = 1024;
 constexpr int kThreads = 256;
-constexpr int kXRegs = kMaxHidden / 2 / kThreads;  // bf16 pairs of x per thread and token
+constexpr int kXWords = kMaxHidden / 2 / kThreads;  // residual words per thread and token
+
+// Row stride of the logit words: the E router logits padded to an even count,
+// then the shared_expert_gate logit and a zero.
+__host__ __device__ constexpr int logit_stride(int E) { return ((E + 1) & ~1) + 2; }
 
 struct DecodeParams {
     const DecodeLayer* layers;  // [nlayers], already offset to the first layer
@@ -70,35 +77,31 @@ struct DecodeParams {
     int order;         // 0 TREE32, 1 FOLD
     int prenorm;       // block input = rms_norm(residual) (chained step), else the input
     int bias_feature;  // with prenorm: block input [H-1] = 1.0
-    // per-layer buffers (index 0 = first layer of the launch)
-    const uint16_t* x_in;     // [T][H] input of the first layer
-    uint16_t* x;              // [nlayers + 1][T][H] residual stream (x[0] unused)
-    uint16_t* x_final;        // [T][H] residual after the last layer, or null
-    uint16_t* h;              // [nlayers][T][H] normalised block input (chained step)
-    uint16_t* out;            // [nlayers][T][H]
-    uint16_t* logits;         // [nlayers][T][ls]: router rows [0, E), shared_expert_gate at gi
-    int ls, gi;               // logit row stride (even) and shared_expert_gate index (even)
-    int32_t* ids;             // [nlayers][T][K]
-    uint16_t* scores;         // [nlayers][T][K]
-    int32_t* slot_expert;     // [nlayers][S]
-    uint32_t* slot_tokens;    // [nlayers][S]
-    int32_t* union_count;     // [nlayers]
-    int32_t* token_slots;     // [nlayers][T][K] slots in ascending expert id
-    uint32_t* token_weights;  // [nlayers][T][K] bf16 score of that slot (low half)
-    uint32_t* sig;            // [nlayers][T] bf16 sigmoid of the shared gate logit (low half)
-    uint16_t* shared_act;     // [nlayers][T][Is]
-    uint16_t* act;            // [nlayers][S][T][I]
-    uint32_t* counters;       // [nlayers][kCountersPerLayer] then 1 done counter
-    int32_t* error;           // 0 ok, 1 timeout, 2 NaN router logit
+    int ls, gi;        // logit row stride (even) and shared_expert_gate index (even)
+    const uint16_t* x_in;  // [T][H] input of the first layer
+    // tagged words (payload = two bf16, or one bf16 in the low half)
+    uint64_t* xw;          // [nlayers + 1][T][H / 2] residual stream (index 0 unused)
+    uint64_t* logits;      // [nlayers][T][ls / 2]
+    uint64_t* shared_act;  // [nlayers][T][Is / 2]
+    uint64_t* act;         // [nlayers][S][T][I / 2]
+    // plain outputs, read after the launch
+    uint16_t* x_final;  // [T][H] residual after the last layer, or null
+    uint16_t* out;      // [nlayers][T][H] block outputs
+    int32_t* ids;       // [nlayers][T][K] rank order
+    uint16_t* scores;   // [nlayers][T][K]
+    uint16_t* sig;      // [nlayers][T] sigmoid of the shared_expert_gate logit
+    uint32_t* counters;  // [nlayers][kCountersPerLayer] then 1 done counter
+    uint32_t* flags;     // [nlayers][kCountersPerLayer][kFlagCopies] epoch of the completed phase
+    int32_t* error;      // 0 ok, 1 timeout, 2 NaN router logit
     uint64_t limit_ticks;
     int n_router, n_shared, n_b, n_c, S;
-    int n_rows;               // R + S + B tasks per layer
-    int g_rows, g_comb;       // workgroups of the rows and combine roles; one more runs top-k
-    uint64_t* trace;          // profiling builds only
+    int n_rows;          // R + S + B tasks per layer
+    int g_rows, g_comb;  // workgroups of the rows and combine roles
+    uint64_t* trace;     // profiling builds only
 };
 
 // Task timing (wall clock) for profiling builds only. Trace slot of a task:
-// layer * (n_rows + 1 + n_c) + [R, S, B | K | C] index.
+// layer * (n_rows + n_c) + [R, S, B | C] index.
 #ifdef FW_DECODE_TRACE
 constexpr int kTraceWords = 8;  // start, dependency met, end, wg << 8 | kind, 4 stage marks
 #define FW_TRACE_STAMP(var) const uint64_t var = wall_clock64()
@@ -123,7 +126,8 @@ constexpr int kTraceWords = 8;  // start, dependency met, end, wg << 8 | kind, 4
 #define FW_TRACE_WRITE(slot_, kind, a, b, c)
 #endif
 
-__device__ __constant__ uint64_t c_exp2_table[32] = {
+// 2^(i/32) as f64 bits (the expf table); one copy per translation unit.
+static __device__ __constant__ uint64_t c_exp2_table[32] = {
     0x3ff0000000000000ULL, 0x3fefd9b0d3158574ULL, 0x3fefb5586cf9890fULL, 0x3fef9301d0125b51ULL,
     0x3fef72b83c7d517bULL, 0x3fef54873168b9aaULL, 0x3fef387a6e756238ULL, 0x3fef1e9df51fdee1ULL,
     0x3fef06fe0a31b715ULL, 0x3feef1a7373aa9cbULL, 0x3feedea64c123422ULL, 0x3feece086061892dULL,
@@ -136,54 +140,75 @@ __device__ __constant__ uint64_t c_exp2_table[32] = {
 
 template <int NT>
 struct DecodeShared {
-    float xs[NT * kMaxHidden];  // rows: block input as f32; top-k: logits then exponentials
+    float xs[NT * kMaxHidden];  // rows: block input as f32; combine: exponentials
+    uint16_t lg[NT * logit_stride(kMaxExperts)];  // logits of the selected layer
     uint64_t exp2tab[32];
-    uint16_t res[(kMaxSlots + 1) * kMaxTokens * kRowsPerCTask];
-    int32_t ids[kMaxTokens * kMaxTopK];
-    int32_t sorted[kMaxSlots];
-    int32_t slot_of[kMaxTokens * kMaxTopK];
-    int32_t first[kMaxTokens * kMaxTopK];
-    int32_t tslot[kMaxTokens * kMaxTopK];
-    uint16_t tweight[kMaxTokens * kMaxTopK];
-    uint16_t sig[kMaxTokens];
-    float inv[kMaxTokens];
+    uint16_t res[(kMaxTopK * NT + 1) * NT * kRowsPerCTask];  // down-row dots [matrix][token][row]
+    int32_t ids[NT * kMaxTopK];                               // rank order per token
+    int32_t sorted[kMaxTopK * NT];                            // union, ascending id
+    uint32_t slot_tokens[kMaxTopK * NT];
+    int32_t slot_of[NT * kMaxTopK];
+    int32_t first[NT * kMaxTopK];
+    int32_t tslot[NT * kMaxTopK];     // [t][k]: slot of the token's k-th expert in ascending id
+    uint16_t tweight[NT * kMaxTopK];  // [t][k]: its bf16 score
+    uint16_t sig[NT];
+    float inv[NT];
     int32_t nunion;
     int32_t flag;
 };
 
-// Residual-stream input of layer li of the launch.
-__device__ __forceinline__ const uint16_t* layer_input(const DecodeParams& p, int li) {
-    return li == 0 ? p.x_in : p.x + (size_t)li * p.T * p.H;
+__device__ __forceinline__ uint32_t* phase_flags(const DecodeParams& p, int li, int phase) {
+    return p.flags + ((size_t)li * kCountersPerLayer + phase) * kFlagCopies;
 }
 
-// Block input of layer li into LDS as f32, [T][H]. In the chained step the
-// block input is the pre-norm of the residual (workload glue, not the
-// reference's block): h = bf16(r * 1/sqrt(mean(r^2) + 1e-6)), mean(r^2)
-// through the reference's dot order (32 chains, tree, +0.0) divided by H;
-// h[H-1] = 1.0 with the bias feature. Wave t normalises token t. With
-// from_h the normalised input is read from p.h (written by the layer's first
-// router task) instead of being recomputed.
+// ---- block input ---------------------------------------------------------------------
+
+// The residual of layer li ([T][H] bf16) into LDS as f32: the caller's input
+// for the first layer of the launch, else the tagged residual words.
 template <int NT>
-__device__ __forceinline__ void stage_input(const DecodeParams& p, int li, bool from_h, DecodeShared<NT>& sh) {
-    const int T = p.T, n = p.H;
-    const bool norm = p.prenorm && !from_h;
-    const uint16_t* src = from_h ? p.h + (size_t)li * T * n : layer_input(p, li);
-    const uint32_t* x2 = reinterpret_cast<const uint32_t*>(src);
+__device__ __forceinline__ bool load_input(const DecodeParams& p, int li, uint32_t epoch, DecodeShared<NT>& sh) {
+    const int pairs = p.T * p.H / 2;
     float* xs = sh.xs;
-    const int pairs = T * n / 2;
-    uint32_t v[NT * kXRegs];
+    bool ok = true;
+    if (li == 0) {
+        const auto* x2 = as_global(reinterpret_cast<const uint32_t*>(p.x_in));
+        uint32_t v[NT * kXWords];
 #pragma unroll
-    for (int k = 0; k < NT * kXRegs; ++k) {
-        const int i = (int)threadIdx.x + k * kThreads;
-        v[k] = coherent_load(x2 + (i < pairs ? i : pairs - 1));
-    }
+        for (int k = 0; k < NT * kXWords; ++k) {
+            const int i = (int)threadIdx.x + k * kThreads;
+            v[k] = x2[i < pairs ? i : pairs - 1];
+        }
 #pragma unroll
-    for (int k = 0; k < NT * kXRegs; ++k) {
-        const int i = (int)threadIdx.x + k * kThreads;
-        if (i < pairs) *reinterpret_cast<float2*>(xs + 2 * i) = make_float2(bf16_lo(v[k]), bf16_hi(v[k]));
+        for (int k = 0; k < NT * kXWords; ++k) {
+            const int i = (int)threadIdx.x + k * kThreads;
+            if (i < pairs) *reinterpret_cast<float2*>(xs + 2 * i) = make_float2(bf16_lo(v[k]), bf16_hi(v[k]));
+        }
+    } else {
+        // this thread's words: tid, tid + 256, ... below pairs
+        const int n = (pairs - (int)threadIdx.x + kThreads - 1) / kThreads;
+        uint64_t v[NT * kXWords];
+        ok = load_tagged<NT * kXWords, kThreads>(v, p.xw + (size_t)li * pairs + threadIdx.x, n, epoch, p.error,
+                                                 p.limit_ticks);
+#pragma unroll
+        for (int k = 0; k < NT * kXWords; ++k) {
+            const int i = (int)threadIdx.x + k * kThreads;
+            const uint32_t w = (uint32_t)v[k];
+            if (k < n) *reinterpret_cast<float2*>(xs + 2 * i) = make_float2(bf16_lo(w), bf16_hi(w));
+        }
     }
-    __syncthreads();
-    if (!norm) return;
+    return __syncthreads_and(ok) != 0;
+}
+
+// In the chained step the block input is the pre-norm of the residual
+// (workload glue, not the reference's block): h = bf16(r * 1/sqrt(mean(r^2) +
+// 1e-6)), mean(r^2) through the reference's dot order (32 chains, tree, +0.0)
+// divided by H; h[H-1] = 1.0 with the bias feature. Wave t normalises token t,
+// in place in LDS.
+template <int NT>
+__device__ __forceinline__ void normalise_input(const DecodeParams& p, DecodeShared<NT>& sh) {
+    if (!p.prenorm) return;
+    const int T = p.T, n = p.H;
+    float* xs = sh.xs;
     const int w = wave_id(), lane = lane_id();
     if (w < T) {
         const float* r = xs + w * n;
@@ -194,9 +219,9 @@ __device__ __forceinline__ void stage_input(const DecodeParams& p, int li, bool 
                 c = add_rn(c, mul_rn(e, e));
             }
         }
-        c = add_rn(c, __shfl_down(c, 16, kWave));  // a'[j] = c[j] + c[j+16]
-        c = add_rn(c, __shfl_down(c, 8, kWave));   // a''[j] = a'[j] + a'[j+8]
-        c = add_rn(c, __shfl_down(c, 4, kWave));   // a3[j] = a''[j] + a''[j+4]
+        c = add_rn(c, __shfl_down(c, 16, kWave));  // a1[j] = c[j] + c[j+16]
+        c = add_rn(c, __shfl_down(c, 8, kWave));   // a2[j] = a1[j] + a1[j+8]
+        c = add_rn(c, __shfl_down(c, 4, kWave));   // a3[j] = a2[j] + a2[j+4]
         float pair = add_rn(c, __shfl_down(c, 1, kWave));  // (a0+a1) in lane 0, (a2+a3) in lane 2
         float ss = add_rn(add_rn(pair, __shfl_down(pair, 2, kWave)), 0.0f);
         if (lane == 0) sh.inv[w] = 1.0f / sqrtf(add_rn(ss / (float)n, 1e-6f));
@@ -210,42 +235,172 @@ __device__ __forceinline__ void stage_input(const DecodeParams& p, int li, bool 
     __syncthreads();
 }
 
+// ---- expert selection ------------------------------------------------------------------
+
+// The layer's logits into LDS (after the router tasks): tagged words, T rows
+// of ls bf16.
+template <int NT>
+__device__ __forceinline__ bool load_logits(const DecodeParams& p, int li, uint32_t epoch, DecodeShared<NT>& sh) {
+    constexpr int kWords = (NT * logit_stride(kMaxExperts) / 2 + kThreads - 1) / kThreads;
+    const int words = p.T * p.ls / 2;
+    const int n = (words - (int)threadIdx.x + kThreads - 1) / kThreads;
+    uint64_t v[kWords];
+    bool ok = load_tagged<kWords, kThreads>(v, p.logits + (size_t)li * words + threadIdx.x, n, epoch, p.error,
+                                            p.limit_ticks);
+    uint32_t* lg2 = reinterpret_cast<uint32_t*>(sh.lg);
+#pragma unroll
+    for (int k = 0; k < kWords; ++k) {
+        if (k < n) lg2[threadIdx.x + k * kThreads] = (uint32_t)v[k];
+    }
+    return __syncthreads_and(ok) != 0;
+}
+
+// Top-k of every token (src/router.rs:241-247 total order) and the union of
+// the selections in ascending expert id, the execution order of
+// src/decoder_layer.rs:422-424: sorted[slot], slot_tokens[slot] (token mask),
+// tslot[t][k] (slot of the token's k-th expert in ascending id), nunion.
+// Requires the logits in LDS. reject_nan: src/decoder_layer.rs:279-281 (the
+// error word is set; the launch then completes and reports it). TK: logits per
+// lane in the top-k (E <= 64 * TK).
+template <int NT, int TK>
+__device__ __forceinline__ void select_experts(const DecodeParams& p, DecodeShared<NT>& sh, bool reject_nan) {
+    const int T = p.T, E = p.E, K = p.K, S = p.S, LS = p.ls;
+    const int lane = lane_id(), w = wave_id(), tid = threadIdx.x;
+    if (w < T) {
+        const uint16_t* lt = sh.lg + w * LS;
+        if (reject_nan) {
+            int nan = 0;
+            for (int e = lane; e < E; e += kWave) nan |= ((lt[e] & 0x7fffu) > 0x7f80u);
+            if (__any(nan) && lane == 0) atomicCAS(p.error, 0, 2);
+        }
+        wave_topk<TK>(lt, E, K, sh.ids + w * kMaxTopK);
+    }
+    __syncthreads();
+    // entry i = (token i / K, rank i % K)
+    const int n_sel = T * K;
+    int my_id = -1;
+    if (tid < n_sel) {
+        my_id = sh.ids[(tid / K) * kMaxTopK + tid % K];
+        int first = 1;
+        for (int i = 0; i < tid; ++i) first &= (sh.ids[(i / K) * kMaxTopK + i % K] != my_id);
+        sh.first[tid] = first;
+    }
+    __syncthreads();
+    if (tid < n_sel) {
+        int slot = 0;
+        for (int i = 0; i < n_sel; ++i) slot += (sh.first[i] && sh.ids[(i / K) * kMaxTopK + i % K] < my_id) ? 1 : 0;
+        sh.slot_of[tid] = slot;
+        if (sh.first[tid]) sh.sorted[slot] = my_id;
+        // position of this expert among the token's own ids, ascending
+        const int tt = tid / K;
+        int k = 0;
+        for (int r = 0; r < K; ++r) k += (sh.ids[tt * kMaxTopK + r] < my_id) ? 1 : 0;
+        sh.tslot[tt * K + k] = slot;
+    }
+    if (tid == 0) {
+        int n = 0;
+        for (int i = 0; i < n_sel; ++i) n += sh.first[i];
+        sh.nunion = n;
+    }
+    __syncthreads();
+    if (tid < S) {
+        uint32_t mask = 0;
+        for (int i = 0; i < n_sel; ++i) mask |= (sh.slot_of[i] == tid) ? (1u << (i / K)) : 0u;
+        sh.slot_tokens[tid] = tid < sh.nunion ? mask : 0u;
+    }
+    __syncthreads();
+}
+
+// Scores of the selected experts: src/router.rs:248-262 /
+// src/decoder_layer.rs:290-306 (max, exp(v - max), one sequential f32 sum in
+// index order, renormalised over the selection), as tweight[t][k] in the
+// token's ascending-id order, and the shared-gate sigmoid. With host_outputs
+// also the rank-order ids and scores and the sigmoid for the caller.
+template <int NT>
+__device__ __forceinline__ void score_experts(const DecodeParams& p, int li, DecodeShared<NT>& sh, bool host_outputs) {
+    const int T = p.T, E = p.E, K = p.K, LS = p.ls;
+    const int lane = lane_id(), w = wave_id();
+    if (w < T) {
+        const uint16_t* lt = sh.lg + w * LS;
+        float* ew = sh.xs + w * E;
+        float mx = -__builtin_inff();
+        for (int e = lane; e < E; e += kWave) mx = fmaxf(mx, from_bf16(lt[e]));
+#pragma unroll
+        for (int off = 32; off >= 1; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off, kWave));
+        for (int e = lane; e < E; e += kWave) ew[e] = expf_glibc(add_rn(from_bf16(lt[e]), -mx), sh.exp2tab);
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+        if (lane == 0) {
+            float den = -0.0f;
+            int e = 0;
+            for (; e + 32 <= E; e += 32) {
+                float v[32];
+#pragma unroll
+                for (int i = 0; i < 32; ++i) v[i] = ew[e + i];
+#pragma unroll
+                for (int i = 0; i < 32; ++i) den = add_rn(den, v[i]);
+            }
+            for (; e < E; ++e) den = add_rn(den, ew[e]);
+            const int32_t* ids = sh.ids + w * kMaxTopK;
+            float sel = -0.0f;
+            for (int r = 0; r < K; ++r) sel = add_rn(sel, ew[ids[r]] / den);
+            for (int r = 0; r < K; ++r) {
+                const uint16_t score = to_bf16((ew[ids[r]] / den) / sel);
+                int k = 0;
+                for (int r2 = 0; r2 < K; ++r2) k += (ids[r2] < ids[r]) ? 1 : 0;
+                sh.tweight[w * K + k] = score;
+                if (host_outputs) {
+                    p.ids[((size_t)li * T + w) * K + r] = ids[r];
+                    p.scores[((size_t)li * T + w) * K + r] = score;
+                }
+            }
+            const uint16_t sg = sigmoid_bf16(lt[p.gi], sh.exp2tab);
+            sh.sig[w] = sg;
+            if (host_outputs) p.sig[(size_t)li * T + w] = sg;
+        }
+    }
+    __syncthreads();
+}
+
 // ---- rows role: R, S and B tasks ------------------------------------------------------
 //
 // A wave covers 4 rows (16 lanes each). R task: 16 router rows; the last R
 // task of a layer is the shared_expert_gate row alone. S and B tasks: 8
 // gate/up pairs, wave w taking pairs 2w and 2w+1 with its lane groups 0, 1 on
 // the gate rows and 2, 3 on the up rows, so SwiGLU joins lane l and l + 32.
-// Each task has one point where its weight loads are issued: before its
-// dependency wait for R and S, right after it for B (whose expert comes from
-// the top-k).
+// R and S issue their weight loads before waiting for the previous layer; B
+// waits for the router, selects, then issues its expert's rows and
+// normalises the input while they arrive.
 
-template <int NT, int MBH>
-__device__ __forceinline__ void rows_role(const DecodeParams* __restrict__ P, DecodeShared<NT>& sh, int rank) {
+template <int NT, int MBH, int TK>
+__device__ __forceinline__ void rows_role(const DecodeParams* __restrict__ P, uint32_t epoch, DecodeShared<NT>& sh,
+                                          int rank) {
     const DecodeParams& p = *P;
     const int lane = lane_id(), w = wave_id(), g = lane / kLanesPerRow, q = lane % kLanesPerRow;
     const int T = p.T, H = p.H, I = p.I, E = p.E, Is = p.Is;
     const int nbh = H / 32;
     const int per_slot = I / kPairsPerTask;
     const int total = p.nlayers * p.n_rows;
+    int loaded = -1, staged = -1, selected = -1;  // layer whose raw input / block input / selection LDS holds
     for (int t = rank; t < total; t += p.g_rows) {
         FW_TRACE_STAMP(t0);
         const int li = t / p.n_rows;
         const int j = t - li * p.n_rows;
-        const int slot_trace = li * (p.n_rows + 1 + p.n_c) + j;
+        const int slot_trace = li * (p.n_rows + p.n_c) + j;
         (void)slot_trace;
         const DecodeLayer& L = p.layers[li];
         uint32_t* cnt = p.counters + (size_t)li * kCountersPerLayer;
         const int kind = j < p.n_router ? kTaskRouter : (j < p.n_router + p.n_shared ? kTaskShared : kTaskGateUp);
+        const bool gate_task = kind == kTaskRouter && j == p.n_router - 1;
         // rows of this lane group
         const uint16_t* wrow;
         int out_index;
         bool valid = true, wave_active = true, fold = false, work = true;
         uint32_t mask = (1u << T) - 1u;
-        uint16_t* act_out = nullptr;
-        int act_stride = 0;
+        uint64_t* act_out = nullptr;
+        int act_stride = 0;  // words per token
         if (kind == kTaskRouter) {
-            const bool gate_task = j == p.n_router - 1;
             const int row0 = gate_task ? E : j * kRouterRowsPerTask;
             const int rows = gate_task ? 1 : min(kRouterRowsPerTask, E - row0);
             const int rin = w * kRowsPerWave + g;
@@ -258,20 +413,31 @@ __device__ __forceinline__ void rows_role(const DecodeParams* __restrict__ P, De
             int pair0;
             if (kind == kTaskShared) {
                 pair0 = (j - p.n_router) * kPairsPerTask;
-                act_out = p.shared_act + (size_t)li * T * Is;
-                act_stride = Is;
+                act_out = p.shared_act + (size_t)li * T * (Is / 2);
+                act_stride = Is / 2;
                 wrow = g < 2 ? L.shared_gate : L.shared_up;
             } else {
                 const int jb = j - p.n_router - p.n_shared;
                 const int s = jb / per_slot;
-                if (!wait_at_least(cnt + kCntIds, 1u, p.error, p.limit_ticks, &sh.flag)) return;
-                const int e = uniform(coherent_load(p.slot_expert + (size_t)li * p.S + s));
-                work = e >= 0;
-                mask = work ? (uint32_t)uniform((int)coherent_load(p.slot_tokens + (size_t)li * p.S + s)) : 0u;
-                const uint16_t* gate_w = L.gate_up + (size_t)(work ? e : 0) * 2 * I * H;
+                if (selected != li) {
+                    // the router tasks of this layer are done: logits and the
+                    // residual are both in memory
+                    if (!wait_phase(phase_flags(p, li, kCntRouter), epoch, p.error, p.limit_ticks, &sh.flag)) return;
+                    if (!load_logits<NT>(p, li, epoch, sh)) return;
+                    if (loaded != li) {
+                        if (!load_input<NT>(p, li, epoch, sh)) return;
+                        loaded = li;
+                    }
+                    select_experts<NT, TK>(p, sh, false);
+                    selected = li;
+                }
+                work = s < uniform(sh.nunion);
+                const int e = work ? uniform(sh.sorted[s]) : 0;
+                mask = work ? (uint32_t)uniform((int)sh.slot_tokens[s]) : 0u;
+                const uint16_t* gate_w = L.gate_up + (size_t)e * 2 * I * H;
                 pair0 = (jb - s * per_slot) * kPairsPerTask;
-                act_out = p.act + ((size_t)li * p.S + s) * (size_t)T * I;
-                act_stride = I;
+                act_out = p.act + ((size_t)li * p.S + s) * (size_t)T * (I / 2);
+                act_stride = I / 2;
                 wrow = g < 2 ? gate_w : gate_w + (size_t)I * H;
             }
             out_index = pair0 + 2 * w + (g & 1);
@@ -280,29 +446,30 @@ __device__ __forceinline__ void rows_role(const DecodeParams* __restrict__ P, De
         RowShare<MBH> rs;
         if (work && wave_active && !fold) row_issue(rs, reinterpret_cast<const uint32_t*>(wrow), nbh, q);
         if (kind != kTaskGateUp && li > 0 &&
-            !wait_at_least(p.counters + (size_t)(li - 1) * kCountersPerLayer + kCntC, (uint32_t)p.n_c, p.error,
-                           p.limit_ticks, &sh.flag))
+            !wait_phase(phase_flags(p, li - 1, kCntC), epoch, p.error, p.limit_ticks, &sh.flag))
             return;
         FW_TRACE_STAMP(t1);
         if (work) {
-            stage_input<NT>(p, li, kind == kTaskGateUp && p.prenorm, sh);
-            FW_TRACE_MARK(slot_trace, 0);
-            if (kind == kTaskRouter && j == 0 && p.prenorm) {
-                // the layer's normalised input, for its B tasks
-                uint32_t* h2 = reinterpret_cast<uint32_t*>(p.h + (size_t)li * T * H);
-                for (int i = threadIdx.x; i < T * H / 2; i += kThreads)
-                    coherent_store(h2 + i, to_bf16(sh.xs[2 * i]) | (to_bf16(sh.xs[2 * i + 1]) << 16));
+            if (staged != li) {
+                if (loaded != li) {
+                    if (!load_input<NT>(p, li, epoch, sh)) return;
+                    loaded = li;
+                }
+                normalise_input<NT>(p, sh);
+                staged = li;
             }
+            FW_TRACE_MARK(slot_trace, 0);
             if (fold) {
                 // src/router.rs:228-240: one lane folds one row; lanes 0 and 2
                 // store the pairs of rows (r, r + 1).
-                uint32_t* logits = reinterpret_cast<uint32_t*>(p.logits + (size_t)li * T * p.ls);
+                uint64_t* lw = p.logits + (size_t)li * T * (p.ls / 2);
                 const int r = j * kRouterRowsPerTask + w * kRowsPerWave + lane;
                 const bool mine = lane < kRowsPerWave && r < E;
                 for (int tt = 0; tt < T; ++tt) {
                     uint32_t bits = mine ? to_bf16(fold_row(L.router + (size_t)r * H, sh.xs + tt * H, H)) : 0u;
                     uint32_t next = (uint32_t)__shfl_down((int)bits, 1, kWave);
-                    if (mine && (lane & 1) == 0) coherent_store(logits + (tt * p.ls + r) / 2, bits | (next << 16));
+                    if (mine && (lane & 1) == 0)
+                        coherent_store64(lw + (tt * p.ls + r) / 2, tagged(bits | (next << 16), epoch));
                 }
             } else if (wave_active) {
                 float acc[NT][2];
@@ -317,14 +484,14 @@ __device__ __forceinline__ void rows_role(const DecodeParams* __restrict__ P, De
                 if (kind == kTaskRouter) {
                     // groups 0 and 2 store the pairs (row, row + 1); the gate
                     // logit goes to its own slot with a zero beside it
-                    uint32_t* logits = reinterpret_cast<uint32_t*>(p.logits + (size_t)li * T * p.ls);
-                    const bool gate_task = j == p.n_router - 1;
+                    uint64_t* lw = p.logits + (size_t)li * T * (p.ls / 2);
                     const int at = gate_task ? p.gi : out_index;
 #pragma unroll
                     for (int tt = 0; tt < NT; ++tt) {
                         uint32_t next = (uint32_t)__shfl((int)bits[tt], (lane + kLanesPerRow) & 63, kWave);
                         if (gate_task) next = 0u;
-                        if (q == 0 && (g & 1) == 0 && valid) coherent_store(logits + (tt * p.ls + at) / 2, bits[tt] | (next << 16));
+                        if (q == 0 && (g & 1) == 0 && valid)
+                            coherent_store64(lw + (tt * p.ls + at) / 2, tagged(bits[tt] | (next << 16), epoch));
                     }
                 } else {
                     // gate (groups 0, 1) meets up (groups 2, 3): lane l takes lane l + 32;
@@ -335,113 +502,154 @@ __device__ __forceinline__ void rows_role(const DecodeParams* __restrict__ P, De
                         uint32_t a = swiglu_bf16(bits[tt], up, sh.exp2tab);
                         uint32_t b = (uint32_t)__shfl((int)a, (lane + kLanesPerRow) & 63, kWave);
                         if (g == 0 && q == 0 && (mask & (1u << tt)))
-                            coherent_store(reinterpret_cast<uint32_t*>(act_out + (size_t)tt * act_stride + out_index), a | (b << 16));
+                            coherent_store64(act_out + (size_t)tt * act_stride + out_index / 2, tagged(a | (b << 16), epoch));
                     }
                 }
             }
             FW_TRACE_MARK(slot_trace, 1);
         }
-        publish(cnt + (kind == kTaskRouter ? kCntRouter : (kind == kTaskShared ? kCntShared : kCntB)));
+        {
+            const int phase = kind == kTaskRouter ? kCntRouter : (kind == kTaskShared ? kCntShared : kCntB);
+            const int count = kind == kTaskRouter ? p.n_router : (kind == kTaskShared ? p.n_shared : p.n_b);
+            publish(cnt + phase, (uint32_t)count, phase_flags(p, li, phase), epoch);
+        }
         FW_TRACE_STAMP(t2);
         FW_TRACE_WRITE(slot_trace, kind, t0, t1, t2);
     }
 }
 
 // ---- combine role: C tasks -----------------------------------------------------------
+//
+// Matrix m of a task: m = 0 is the shared expert's down projection, m = 1 + s
+// the down projection of slot s. Wave w covers the task's 4 rows (16 lanes
+// each) of matrices w, w + 4, w + 8, w + 12 in its first batch, then the next
+// 16 matrices, and so on.
 
-template <int NT, int MBI>
-__device__ __forceinline__ void combine_role(const DecodeParams* __restrict__ P, DecodeShared<NT>& sh, int rank) {
+// One down row against its activation words (tagged): the chains of
+// src/expert.rs:514-552 over K = nblocks * 32 (so the tail sum is +0.0), for
+// each token in mask (wave-uniform). Returns false on timeout or error.
+template <int NT, int MAXB>
+__device__ __forceinline__ bool down_row(const RowShare<MAXB>& r, int nblocks, const uint64_t* actw, int words_per_token,
+                                         int q, uint32_t mask, uint32_t epoch, const DecodeParams& p,
+                                         uint32_t (&bits)[NT]) {
+    bool ok = true;
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
+        bits[t] = 0u;
+        if (!(mask & (1u << t))) continue;
+        const int nb = opaque(nblocks);
+        uint64_t xv[MAXB];
+        ok = load_tagged<MAXB, 16>(xv, actw + (size_t)t * words_per_token + q, nb, epoch, p.error, p.limit_ticks) && ok;
+        float c0 = 0.0f, c1 = 0.0f;
+#pragma unroll
+        for (int u = 0; u < MAXB; ++u) {
+            if (u < nb) {
+                const uint32_t a = (uint32_t)xv[u];
+                c0 = add_rn(c0, mul_rn(bf16_lo(r.w[u]), bf16_lo(a)));
+                c1 = add_rn(c1, mul_rn(bf16_hi(r.w[u]), bf16_hi(a)));
+            }
+        }
+        bits[t] = to_bf16(add_rn(tree32_reduce(c0, c1), 0.0f));
+    }
+    return ok;
+}
+
+template <int NT, int MBI, int TK>
+__device__ __forceinline__ void combine_role(const DecodeParams* __restrict__ P, uint32_t epoch, DecodeShared<NT>& sh,
+                                             int rank) {
     const DecodeParams& p = *P;
     const int lane = lane_id(), w = wave_id(), g = lane / kLanesPerRow, q = lane % kLanesPerRow;
     const int T = p.T, H = p.H, I = p.I, Is = p.Is, K = p.K;
     const uint32_t all_tokens = (1u << T) - 1u;
     const int total = p.nlayers * p.n_c;
+    int selected = -1;
     for (int t = rank; t < total; t += p.g_comb) {
         FW_TRACE_STAMP(t0);
         const int li = t / p.n_c;
         const int j = t - li * p.n_c;
-        const int slot_trace = li * (p.n_rows + 1 + p.n_c) + p.n_rows + 1 + j;
+        const int slot_trace = li * (p.n_rows + p.n_c) + p.n_rows + j;
         (void)slot_trace;
         const DecodeLayer& L = p.layers[li];
         uint32_t* cnt = p.counters + (size_t)li * kCountersPerLayer;
-        if (!wait_at_least(cnt + kCntIds, 1u, p.error, p.limit_ticks, &sh.flag)) return;
         const int r0 = j * kRowsPerCTask;
-        const int U = uniform(coherent_load(p.union_count + li));
-        const int32_t* slot_expert = p.slot_expert + (size_t)li * p.S;
-        const uint32_t* slot_tokens = p.slot_tokens + (size_t)li * p.S;
         const int row = r0 + g;
-        // Down rows of up to 4 matrices per wave and batch (slots m0, m0+4, ...;
-        // the shared expert is matrix U). The first batch is issued before
-        // waiting for the gate/up phase.
         RowShare<MBI> rs0, rs1, rs2, rs3;
-#define FW_ISSUE_DOWN(RS, M)                                                                     \
-    do {                                                                                         \
-        const int m_ = (M);                                                                      \
-        if (m_ <= U) {                                                                           \
-            const bool shared_ = m_ == U;                                                        \
-            const int kd_ = shared_ ? Is : I;                                                    \
-            const uint16_t* wm_ =                                                                \
-                shared_ ? L.shared_down : L.down + (size_t)uniform(coherent_load(slot_expert + m_)) * (size_t)H * I; \
-            row_issue(RS, reinterpret_cast<const uint32_t*>(wm_ + (size_t)row * kd_), kd_ / 32, q); \
-        }                                                                                        \
+        // the shared expert's rows need no selection: issue them first
+        if (w == 0) row_issue(rs0, reinterpret_cast<const uint32_t*>(L.shared_down + (size_t)row * Is), Is / 32, q);
+        if (selected != li) {
+            if (!wait_phase(phase_flags(p, li, kCntRouter), epoch, p.error, p.limit_ticks, &sh.flag)) return;
+            if (!load_logits<NT>(p, li, epoch, sh)) return;
+            const bool host_outputs = j == 0;
+            select_experts<NT, TK>(p, sh, host_outputs && p.order == 0);
+            score_experts<NT>(p, li, sh, host_outputs);
+            selected = li;
+        }
+        const int U = uniform(sh.nunion);
+#define FW_ISSUE_DOWN(RS, M)                                                                              \
+    do {                                                                                                  \
+        const int m_ = (M);                                                                               \
+        if (m_ >= 1 && m_ <= U) {                                                                         \
+            const uint16_t* wm_ = L.down + (size_t)uniform(sh.sorted[m_ - 1]) * (size_t)H * I;            \
+            row_issue(RS, reinterpret_cast<const uint32_t*>(wm_ + (size_t)row * I), I / 32, q);            \
+        } else if (m_ == 0) {                                                                             \
+            row_issue(RS, reinterpret_cast<const uint32_t*>(L.shared_down + (size_t)row * Is), Is / 32, q); \
+        }                                                                                                 \
     } while (0)
-#define FW_ISSUE_BATCH(M0)             \
-    do {                               \
-        FW_ISSUE_DOWN(rs0, (M0));      \
-        FW_ISSUE_DOWN(rs1, (M0) + 4);  \
-        FW_ISSUE_DOWN(rs2, (M0) + 8);  \
-        FW_ISSUE_DOWN(rs3, (M0) + 12); \
+#define FW_DOWN_DOT(RS, M)                                                                                \
+    do {                                                                                                  \
+        const int m_ = (M);                                                                               \
+        if (m_ <= U) {                                                                                    \
+            const bool shared_ = m_ == 0;                                                                 \
+            const int kd_ = shared_ ? Is : I;                                                             \
+            const uint32_t mask_ = shared_ ? all_tokens : (uint32_t)uniform((int)sh.slot_tokens[m_ - 1]); \
+            const uint64_t* actw_ = shared_ ? p.shared_act + (size_t)li * T * (Is / 2)                    \
+                                            : p.act + ((size_t)li * p.S + m_ - 1) * (size_t)T * (I / 2);  \
+            uint32_t bits_[NT];                                                                           \
+            ok = down_row<NT, MBI>(RS, kd_ / 32, actw_, kd_ / 2, q, mask_, epoch, p, bits_) && ok;         \
+            _Pragma("unroll") for (int t_ = 0; t_ < NT; ++t_) {                                           \
+                if (q == 0 && (mask_ & (1u << t_))) sh.res[(m_ * NT + t_) * kRowsPerCTask + g] = bits_[t_]; \
+            }                                                                                             \
+        }                                                                                                 \
     } while (0)
-#define FW_DOWN_DOT(RS, M)                                                                       \
-    do {                                                                                         \
-        const int m_ = (M);                                                                      \
-        if (m_ <= U) {                                                                           \
-            const bool shared_ = m_ == U;                                                        \
-            const int kd_ = shared_ ? Is : I;                                                    \
-            const uint32_t mask_ = shared_ ? all_tokens : (uint32_t)uniform((int)coherent_load(slot_tokens + m_)); \
-            const uint16_t* actv_ = shared_ ? p.shared_act + (size_t)li * T * Is                 \
-                                            : p.act + ((size_t)li * p.S + m_) * (size_t)T * I;   \
-            float acc_[NT][2];                                                                   \
-            row_chains_gx<NT, MBI>(RS, kd_ / 32, actv_, kd_, q, mask_, acc_);                    \
-            _Pragma("unroll") for (int t_ = 0; t_ < NT; ++t_) {                                  \
-                /* K % 32 == 0 here: the tail sum is +0.0 */                                     \
-                float d_ = add_rn(tree32_reduce(acc_[t_][0], acc_[t_][1]), 0.0f);                \
-                if (q == 0 && (mask_ & (1u << t_)))                                              \
-                    sh.res[(m_ * kMaxTokens + t_) * kRowsPerCTask + g] = to_bf16(d_);            \
-            }                                                                                    \
-        }                                                                                        \
-    } while (0)
-        FW_ISSUE_BATCH(w);
-        if (!(wait_at_least(cnt + kCntB, (uint32_t)p.n_b, p.error, p.limit_ticks, &sh.flag) &&
-              wait_at_least(cnt + kCntShared, (uint32_t)p.n_shared, p.error, p.limit_ticks, &sh.flag) &&
-              wait_at_least(cnt + kCntScores, 1u, p.error, p.limit_ticks, &sh.flag)))
+        if (w != 0) FW_ISSUE_DOWN(rs0, w);
+        FW_ISSUE_DOWN(rs1, w + 4);
+        FW_ISSUE_DOWN(rs2, w + 8);
+        FW_ISSUE_DOWN(rs3, w + 12);
+        if (!(wait_phase(phase_flags(p, li, kCntB), epoch, p.error, p.limit_ticks, &sh.flag) &&
+              wait_phase(phase_flags(p, li, kCntShared), epoch, p.error, p.limit_ticks, &sh.flag)))
             return;
         FW_TRACE_STAMP(t1);
-        // Per-token slot order, weights and shared gate into LDS (one round trip).
-        const int tid = threadIdx.x;
-        if (tid < T * K) {
-            sh.tslot[tid] = coherent_load(p.token_slots + (size_t)li * T * K + tid);
-            sh.tweight[tid] = (uint16_t)coherent_load(p.token_weights + (size_t)li * T * K + tid);
-        }
-        if (tid < T) sh.sig[tid] = (uint16_t)coherent_load(p.sig + (size_t)li * T + tid);
+        bool ok = true;
         for (int m0 = w; m0 <= U; m0 += 16) {
-            if (m0 != w) FW_ISSUE_BATCH(m0);
+            if (m0 != w) {
+                FW_ISSUE_DOWN(rs0, m0);
+                FW_ISSUE_DOWN(rs1, m0 + 4);
+                FW_ISSUE_DOWN(rs2, m0 + 8);
+                FW_ISSUE_DOWN(rs3, m0 + 12);
+            }
             FW_DOWN_DOT(rs0, m0);
             FW_DOWN_DOT(rs1, m0 + 4);
             FW_DOWN_DOT(rs2, m0 + 8);
             FW_DOWN_DOT(rs3, m0 + 12);
         }
 #undef FW_DOWN_DOT
-#undef FW_ISSUE_BATCH
 #undef FW_ISSUE_DOWN
         FW_TRACE_MARK(slot_trace, 0);
-        __syncthreads();
+        if (!__syncthreads_and(ok)) return;
+        const int tid = threadIdx.x;
         if (tid < T * kRowsPerCTask / 2) {
             // one thread per token and pair of hidden rows
             const int tt = tid / (kRowsPerCTask / 2);
             const int g0 = 2 * (tid % (kRowsPerCTask / 2));
             const size_t at = ((size_t)tt * H + r0 + g0) / 2;
-            const uint32_t rin = coherent_load(reinterpret_cast<const uint32_t*>(layer_input(p, li)) + at);
+            uint32_t rin;
+            if (li == 0) {
+                rin = reinterpret_cast<const uint32_t*>(p.x_in)[at];
+            } else {
+                uint64_t v[1];
+                ok = load_tagged<1, 1>(v, p.xw + (size_t)li * T * H / 2 + at, 1, epoch, p.error, p.limit_ticks);
+                rin = (uint32_t)v[0];
+            }
             uint32_t o2 = 0, x2 = 0;
             for (int half = 0; half < 2; ++half) {
                 const int gg = g0 + half;
@@ -449,12 +657,12 @@ __device__ __forceinline__ void combine_role(const DecodeParams* __restrict__ P,
                 // in ascending expert order from bf16 zero, rounding after each add.
                 uint32_t mix = to_bf16(0.0f);
                 for (int k = 0; k < K; ++k) {
-                    uint32_t d = sh.res[(sh.tslot[tt * K + k] * kMaxTokens + tt) * kRowsPerCTask + gg];
+                    uint32_t d = sh.res[((1 + sh.tslot[tt * K + k]) * NT + tt) * kRowsPerCTask + gg];
                     uint32_t weighted = to_bf16(mul_rn(from_bf16(d), from_bf16(sh.tweight[tt * K + k])));
                     mix = add_bf16(mix, weighted);
                 }
                 // src/decoder_layer.rs:563-575: gated = bf16(shared_down * sigmoid).
-                uint32_t sd = sh.res[(U * kMaxTokens + tt) * kRowsPerCTask + gg];
+                uint32_t sd = sh.res[(0 * NT + tt) * kRowsPerCTask + gg];
                 uint32_t gated = to_bf16(mul_rn(from_bf16(sd), from_bf16(sh.sig[tt])));
                 uint32_t o = add_bf16(mix, gated);
                 uint32_t xn = add_bf16((rin >> (16 * half)) & 0xffffu, o);
@@ -462,157 +670,31 @@ __device__ __forceinline__ void combine_role(const DecodeParams* __restrict__ P,
                 x2 |= xn << (16 * half);
             }
             reinterpret_cast<uint32_t*>(p.out + (size_t)li * T * H)[at] = o2;
-            coherent_store(reinterpret_cast<uint32_t*>(p.x + (size_t)(li + 1) * T * H) + at, x2);
+            coherent_store64(p.xw + (size_t)(li + 1) * T * H / 2 + at, tagged(x2, epoch));
             if (li + 1 == p.nlayers && p.x_final != nullptr) reinterpret_cast<uint32_t*>(p.x_final)[at] = x2;
         }
+        if (!__syncthreads_and(ok)) return;
         FW_TRACE_MARK(slot_trace, 1);
-        publish(cnt + kCntC);
+        publish(cnt + kCntC, (uint32_t)p.n_c, phase_flags(p, li, kCntC), epoch);
         FW_TRACE_STAMP(t2);
         FW_TRACE_WRITE(slot_trace, kTaskDown, t0, t1, t2);
     }
 }
 
-// ---- top-k role: one workgroup, every layer ------------------------------------------
-
-template <int NT>
-__device__ __forceinline__ void topk_role(const DecodeParams* __restrict__ P, DecodeShared<NT>& sh) {
-    const DecodeParams& p = *P;
-    const int lane = lane_id(), w = wave_id(), tid = threadIdx.x;
-    const int T = p.T, E = p.E, K = p.K, S = p.S;
-    const int LS = p.ls;
-    uint16_t* lg = reinterpret_cast<uint16_t*>(sh.xs);  // [T][LS]
-    float* ex = sh.xs + T * LS / 2;                     // [T][E]
-    for (int li = 0; li < p.nlayers; ++li) {
-        FW_TRACE_STAMP(t0);
-        const int slot_trace = li * (p.n_rows + 1 + p.n_c) + p.n_rows;
-        (void)slot_trace;
-        uint32_t* cnt = p.counters + (size_t)li * kCountersPerLayer;
-        if (!wait_at_least(cnt + kCntRouter, (uint32_t)p.n_router, p.error, p.limit_ticks, &sh.flag)) return;
-        FW_TRACE_STAMP(t1);
-        const uint32_t* logits = reinterpret_cast<const uint32_t*>(p.logits + (size_t)li * T * LS);
-        for (int i = tid; i < T * LS / 2; i += kThreads) reinterpret_cast<uint32_t*>(lg)[i] = coherent_load(logits + i);
-        __syncthreads();
-        if (w < T) {
-            const uint16_t* lt = lg + w * LS;
-            if (p.order == 0) {
-                // src/decoder_layer.rs:279-281: NaN logits are rejected.
-                int nan = 0;
-                for (int e = lane; e < E; e += kWave) nan |= ((lt[e] & 0x7fffu) > 0x7f80u);
-                if (__any(nan) && lane == 0) atomicCAS(p.error, 0, 2);
-            }
-            if (E <= 512) {
-                wave_topk<8>(lt, E, K, sh.ids + w * kMaxTopK);
-            } else {
-                wave_topk<16>(lt, E, K, sh.ids + w * kMaxTopK);
-            }
-        }
-        __syncthreads();
-        FW_TRACE_MARK(slot_trace, 0);
-        // Union of the selections in ascending expert id (the execution order,
-        // src/decoder_layer.rs:422-424): entry i = (token i / K, rank i % K).
-        const int n_sel = T * K;
-        int my_id = -1;
-        if (tid < n_sel) {
-            my_id = sh.ids[(tid / K) * kMaxTopK + tid % K];
-            int first = 1;
-            for (int i = 0; i < tid; ++i) first &= (sh.ids[(i / K) * kMaxTopK + i % K] != my_id);
-            sh.first[tid] = first;
-        }
-        __syncthreads();
-        if (tid < n_sel) {
-            int slot = 0;
-            for (int i = 0; i < n_sel; ++i)
-                slot += (sh.first[i] && sh.ids[(i / K) * kMaxTopK + i % K] < my_id) ? 1 : 0;
-            sh.slot_of[tid] = slot;
-            if (sh.first[tid]) sh.sorted[slot] = my_id;
-            // position of this expert among the token's own ids, ascending
-            const int tt = tid / K;
-            int k = 0;
-            for (int r = 0; r < K; ++r) k += (sh.ids[tt * kMaxTopK + r] < my_id) ? 1 : 0;
-            sh.tslot[tt * K + k] = slot;
-        }
-        if (tid == 0) {
-            int n = 0;
-            for (int i = 0; i < n_sel; ++i) n += sh.first[i];
-            sh.nunion = n;
-        }
-        __syncthreads();
-        const int n = sh.nunion;
-        if (tid < n_sel) {
-            p.ids[(size_t)li * T * K + tid] = my_id;
-            coherent_store(p.token_slots + (size_t)li * T * K + tid, sh.tslot[tid]);
-        }
-        if (tid < S) {
-            uint32_t mask = 0;
-            if (tid < n) {
-                for (int i = 0; i < n_sel; ++i) mask |= (sh.slot_of[i] == tid) ? (1u << (i / K)) : 0u;
-            }
-            coherent_store(p.slot_expert + (size_t)li * S + tid, tid < n ? sh.sorted[tid] : -1);
-            coherent_store(p.slot_tokens + (size_t)li * S + tid, mask);
-        }
-        if (tid == 0) coherent_store(p.union_count + li, n);
-        FW_TRACE_MARK(slot_trace, 1);
-        publish(cnt + kCntIds);
-        FW_TRACE_MARK(slot_trace, 2);
-        // Scores: src/router.rs:248-262 / src/decoder_layer.rs:290-306.
-        if (w < T) {
-            const uint16_t* lt = lg + w * LS;
-            float* ew = ex + w * E;
-            float mx = -__builtin_inff();
-            for (int e = lane; e < E; e += kWave) mx = fmaxf(mx, from_bf16(lt[e]));
-#pragma unroll
-            for (int off = 32; off >= 1; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off, kWave));
-            for (int e = lane; e < E; e += kWave) ew[e] = expf_glibc(add_rn(from_bf16(lt[e]), -mx), sh.exp2tab);
-            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
-            __builtin_amdgcn_wave_barrier();
-            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
-            if (lane == 0) {
-                // one sequential f32 sum in index order, 32 values read per batch
-                float den = -0.0f;
-                int e = 0;
-                for (; e + 32 <= E; e += 32) {
-                    float v[32];
-#pragma unroll
-                    for (int i = 0; i < 32; ++i) v[i] = ew[e + i];
-#pragma unroll
-                    for (int i = 0; i < 32; ++i) den = add_rn(den, v[i]);
-                }
-                for (; e < E; ++e) den = add_rn(den, ew[e]);
-                const int32_t* tid_ids = sh.ids + w * kMaxTopK;
-                float sel = -0.0f;
-                for (int r = 0; r < K; ++r) sel = add_rn(sel, ew[tid_ids[r]] / den);
-                for (int r = 0; r < K; ++r) {
-                    uint16_t score = to_bf16((ew[tid_ids[r]] / den) / sel);
-                    p.scores[(size_t)li * T * K + (size_t)w * K + r] = score;
-                    // this expert's place in the token's ascending-id order
-                    int k = 0;
-                    for (int r2 = 0; r2 < K; ++r2) k += (tid_ids[r2] < tid_ids[r]) ? 1 : 0;
-                    coherent_store(p.token_weights + (size_t)li * T * K + (size_t)w * K + k, score);
-                }
-                coherent_store(p.sig + (size_t)li * T + w, sigmoid_bf16(lt[p.gi], sh.exp2tab));
-            }
-        }
-        FW_TRACE_MARK(slot_trace, 3);
-        publish(cnt + kCntScores);
-        FW_TRACE_STAMP(t2);
-        FW_TRACE_WRITE(slot_trace, kTaskTopk, t0, t1, t2);
-    }
-}
-
-template <int NT, int MBH, int MBI>
+// NT tokens; MBH, MBI: 32-column blocks held per hidden row / down row; TK:
+// logits per lane in the top-k.
+template <int NT, int MBH, int MBI, int TK>
 __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4)))
-k_moe_decode(const DecodeParams* __restrict__ P) {
+k_moe_decode(const DecodeParams* __restrict__ P, uint32_t epoch) {
     __shared__ DecodeShared<NT> sh;
     if (threadIdx.x < 32) sh.exp2tab[threadIdx.x] = c_exp2_table[threadIdx.x];
     __syncthreads();
     const int b = (int)blockIdx.x;
     const int G = (int)gridDim.x;
     if (b < P->g_rows) {
-        rows_role<NT, MBH>(P, sh, b);
+        rows_role<NT, MBH, TK>(P, epoch, sh, b);
     } else if (b < P->g_rows + P->g_comb) {
-        combine_role<NT, MBI>(P, sh, b - P->g_rows);
-    } else {
-        topk_role<NT>(P, sh);
+        combine_role<NT, MBI, TK>(P, epoch, sh, b - P->g_rows);
     }
     // The last workgroup out zeroes every counter for the next launch.
     __syncthreads();
@@ -628,5 +710,22 @@ k_moe_decode(const DecodeParams* __restrict__ P) {
         }
     }
 }
+
+// Every variant the host dispatches on; instantiated in fw_decode_kernels.hip
+// (one translation unit per token count, compiled in parallel).
+#define FW_DECODE_VARIANTS_FOR(X, NT) \
+    X(NT, 64, 16, 8)                  \
+    X(NT, 64, 32, 8)                  \
+    X(NT, 80, 16, 8)                  \
+    X(NT, 80, 32, 8)                  \
+    X(NT, 64, 16, 16)                 \
+    X(NT, 64, 32, 16)                 \
+    X(NT, 80, 16, 16)                 \
+    X(NT, 80, 32, 16)
+#define FW_DECODE_VARIANTS(X)     \
+    FW_DECODE_VARIANTS_FOR(X, 1)  \
+    FW_DECODE_VARIANTS_FOR(X, 2)  \
+    FW_DECODE_VARIANTS_FOR(X, 3)  \
+    FW_DECODE_VARIANTS_FOR(X, 4)
 
 }  // namespace fw

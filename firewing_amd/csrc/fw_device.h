@@ -106,6 +106,21 @@ __device__ __forceinline__ void coherent_store(int32_t* p, int32_t v) {
     __hip_atomic_store(as_global_rw(p), v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
+__device__ __forceinline__ uint64_t coherent_load64(const uint64_t* p) {
+    return __hip_atomic_load(as_global(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void coherent_store64(uint64_t* p, uint64_t v) {
+    __hip_atomic_store(as_global_rw(p), v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Tagged words: a 32-bit payload and the launch's epoch in one 64-bit store,
+// so a reader that sees the epoch also sees the payload. Words from earlier
+// launches carry older epochs.
+__device__ __forceinline__ uint64_t tagged(uint32_t payload, uint32_t epoch) {
+    return ((uint64_t)epoch << 32) | payload;
+}
+__device__ __forceinline__ bool has_tag(uint64_t word, uint32_t epoch) { return (uint32_t)(word >> 32) == epoch; }
+
 // Wave-uniform value as a scalar (lets the compiler branch on it without
 // exec masks).
 __device__ __forceinline__ int uniform(int v) { return __builtin_amdgcn_readfirstlane(v); }
@@ -287,39 +302,51 @@ __device__ __forceinline__ void wave_topk(const uint16_t* __restrict__ logits, i
 
 // ---- inter-workgroup synchronisation for the persistent kernel ----------------------
 //
-// Everything one workgroup writes for another (activations, logits, expert
-// lists, the residual stream) and the counters that announce it are accessed
-// only with agent-scope relaxed atomics: 32-bit stores that write through to
-// the device's coherence point and loads that read from it, past the per-XCD
-// L2 caches, which are not coherent with each other. A task publishes by
-// waiting until its own stores are acknowledged (so they are visible at the
-// coherence point), then raising the counter; a waiter reads the data only
-// after it has seen the count. No cache write-back or invalidation is needed:
-// such a fence costs one L2-wide operation, and hundreds of workgroups issuing
-// them at once on one XCD serialise behind each other.
+// The per-XCD L2 caches are not coherent with each other, and no cache is
+// written back or invalidated here (such a fence is one L2-wide operation, and
+// hundreds of workgroups issuing them at once on one XCD serialise behind each
+// other). Instead:
+//
+// * Data one workgroup writes for another (logits, activations, the residual
+//   stream) travels as tagged 64-bit words, payload and launch epoch in one
+//   agent-scope store that writes through to the coherence point. Readers
+//   load through the caches first, so the hundreds of workgroups that read
+//   the same small vector mostly hit their XCD's L2 instead of queueing on
+//   the few memory channels that hold it, and re-read with agent-scope loads
+//   (past the caches) only the words whose tag is not the current epoch.
+// * Each phase of each layer has a counter that every task of the phase
+//   increments once, right after issuing its stores (no wait for their
+//   acknowledgement: readers check the tags). The task that completes the
+//   count writes the epoch into kFlagCopies flag words; a waiter polls the
+//   copy for its workgroup, so no single word is polled by more than a few
+//   dozen workgroups.
 
-// Wait until this wave's outstanding memory operations have completed (stores
-// acknowledged by the coherence point). The asm is opaque to the compiler, so
-// no memory access moves across it.
-__device__ __forceinline__ void wait_own_stores() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+constexpr int kFlagCopies = 64;
 
-__device__ __forceinline__ void publish(uint32_t* counter) {
-    wait_own_stores();
+// Announce a finished task of a phase of `target` tasks. Every wave has issued
+// its tagged stores (program order up to the barrier).
+__device__ __forceinline__ void publish(uint32_t* counter, uint32_t target, uint32_t* flags, uint32_t epoch) {
     __syncthreads();
-    if (threadIdx.x == 0) __hip_atomic_fetch_add(as_global_rw(counter), 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (threadIdx.x == 0) {
+        const uint32_t before =
+            __hip_atomic_fetch_add(as_global_rw(counter), 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (before + 1u == target) {
+            for (int i = 0; i < kFlagCopies; ++i) coherent_store(flags + i, epoch);
+        }
+    }
 }
 
-// Thread 0 spins until *counter >= target, bounded by a wall-clock limit and
-// by the shared error word; the verdict is broadcast to the workgroup.
-// Returns false if the kernel must stop.
-__device__ __forceinline__ bool wait_at_least(const uint32_t* counter, uint32_t target,
-                                              int32_t* error, uint64_t limit_ticks,
-                                              int32_t* lds_flag) {
+// Thread 0 polls this workgroup's copy of a phase flag until it holds the
+// epoch, bounded by a wall-clock limit and by the shared error word; the
+// verdict is broadcast to the workgroup. Returns false if the kernel must stop.
+__device__ __forceinline__ bool wait_phase(const uint32_t* flags, uint32_t epoch, int32_t* error,
+                                           uint64_t limit_ticks, int32_t* lds_flag) {
     if (threadIdx.x == 0) {
+        const uint32_t* f = flags + (blockIdx.x % kFlagCopies);
         int32_t ok = 1;
-        if (coherent_load(counter) < target) {
+        if (coherent_load(f) != epoch) {
             uint64_t start = wall_clock64();
-            while (coherent_load(counter) < target) {
+            while (coherent_load(f) != epoch) {
                 if (coherent_load(error) != 0) {
                     ok = 0;
                     break;
@@ -331,7 +358,7 @@ __device__ __forceinline__ bool wait_at_least(const uint32_t* counter, uint32_t 
                     ok = 0;
                     break;
                 }
-                __builtin_amdgcn_s_sleep(1);
+                __builtin_amdgcn_s_sleep(2);
             }
         }
         *lds_flag = ok;
@@ -340,6 +367,45 @@ __device__ __forceinline__ bool wait_at_least(const uint32_t* counter, uint32_t 
     int32_t ok = *lds_flag;
     __syncthreads();
     return ok != 0;
+}
+
+// Tagged words v[k] = base[k * STRIDE] for k < n (slots k >= n are left
+// alone). The first read goes through the caches; words that do not carry
+// `epoch` (a stale cached line, or a store still in flight) are read again past
+// the caches until they do, bounded by the wall-clock limit and the shared
+// error word. Per lane; false on timeout or error.
+template <int N, int STRIDE>
+__device__ __forceinline__ bool load_tagged(uint64_t (&v)[N], const uint64_t* base, int n, uint32_t epoch,
+                                            int32_t* error, uint64_t limit_ticks) {
+    const auto* g = as_global(base);
+#pragma unroll
+    for (int k = 0; k < N; ++k) {
+        if (k < n) v[k] = __hip_atomic_load(g + k * STRIDE, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    }
+    bool ok = true;
+#pragma unroll
+    for (int k = 0; k < N; ++k) ok = ok && (k >= n || has_tag(v[k], epoch));
+    if (ok) return true;
+    const uint64_t start = wall_clock64();
+    while (true) {
+#pragma unroll
+        for (int k = 0; k < N; ++k) {
+            if (k < n && !has_tag(v[k], epoch))
+                v[k] = __hip_atomic_load(g + k * STRIDE, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+        ok = true;
+#pragma unroll
+        for (int k = 0; k < N; ++k) ok = ok && (k >= n || has_tag(v[k], epoch));
+        if (ok) return true;
+        if (coherent_load(error) != 0) return false;
+        if (wall_clock64() - start > limit_ticks) {
+            int32_t expected = 0;
+            __hip_atomic_compare_exchange_strong(error, &expected, 1, __ATOMIC_RELAXED, __ATOMIC_RELAXED,
+                                                 __HIP_MEMORY_SCOPE_AGENT);
+            return false;
+        }
+        __builtin_amdgcn_s_sleep(2);
+    }
 }
 
 }  // namespace fw

@@ -23,6 +23,14 @@
 
 using namespace fw;
 
+// The decode kernels are instantiated in fw_decode_kernels.hip.
+namespace fw {
+#define FW_EXTERN(NT, MBH, MBI, TK) \
+    extern template __global__ void k_moe_decode<NT, MBH, MBI, TK>(const DecodeParams*, uint32_t);
+FW_DECODE_VARIANTS(FW_EXTERN)
+#undef FW_EXTERN
+}  // namespace fw
+
 // ---- error reporting ------------------------------------------------------------------
 
 namespace {
@@ -297,12 +305,15 @@ struct firewing_hip_context {
     DecodeLayer* d_layers = nullptr;  // [L]
     uint16_t* d_weight_table = nullptr;
     // decode scratch sized for L layers and T <= 4
-    uint16_t *x = nullptr, *out = nullptr, *logits = nullptr, *scores = nullptr;
-    uint16_t *shared_act = nullptr, *act = nullptr, *h = nullptr;
-    uint32_t *token_weights = nullptr, *sig = nullptr;
-    int32_t *ids = nullptr, *slot_expert = nullptr, *union_count = nullptr, *token_slots = nullptr;
-    uint32_t *slot_tokens = nullptr, *counters = nullptr;
+    uint16_t* xin = nullptr;     // [T][H] host input staged for the launch
+    uint16_t* xfinal = nullptr;  // [T][H] residual after the last layer
+    uint16_t *out = nullptr, *scores = nullptr, *sig = nullptr;
+    int32_t* ids = nullptr;
+    uint64_t *xw = nullptr, *logits = nullptr, *shared_act = nullptr, *act = nullptr;  // tagged words
+    uint32_t* counters = nullptr;
+    uint32_t* flags = nullptr;  // phase flags (epoch of the completed phase)
     int32_t* error = nullptr;
+    uint32_t epoch = 0;  // tag of the last launch
     int grid[kMaxTokens + 1] = {0};
     uint64_t* trace = nullptr;  // profiling builds: per-task timestamps of the next launch
     DecodeParams* d_params = nullptr;  // device copy of the last launch's parameters
@@ -319,10 +330,6 @@ T* dalloc(size_t count) {
     check(hipMalloc(&p, std::max<size_t>(count, 1) * sizeof(T)), "hipMalloc");
     return static_cast<T*>(p);
 }
-
-// Row stride of the logit scratch: the E router logits, padded to an even
-// count, then the shared_expert_gate logit and a zero (32-bit aligned pairs).
-size_t logit_stride(size_t E) { return ((E + 1) & ~(size_t)1) + 2; }
 
 bool validate_shape(const firewing_hip_shape& s, std::string* why) {
     auto bad = [&](const char* m) {
@@ -342,23 +349,28 @@ bool validate_shape(const firewing_hip_shape& s, std::string* why) {
     return true;
 }
 
-// Kernel variant for T tokens and the context's block counts: hidden rows of
-// up to 64 blocks (H <= 2048) or 80 (H <= 2560); down rows of up to 16 blocks
-// (I, Is <= 512) or 32 (<= 1024).
+// Kernel variant for T tokens and the context's shape: hidden rows of up to
+// 64 blocks (H <= 2048) or 80 (H <= 2560); down rows of up to 16 blocks
+// (I, Is <= 512) or 32 (<= 1024); top-k over up to 512 experts or 1024.
 const void* decode_kernel(const firewing_hip_context* c, int T) {
     const bool wide_h = c->shape.hidden > 2048;
     const bool wide_i = std::max(c->shape.intermediate, c->shape.shared_intermediate) > 512;
-#define FW_DECODE_VARIANT(NT)                                                                  \
-    if (T == NT) {                                                                             \
-        if (!wide_h && !wide_i) return reinterpret_cast<const void*>(&k_moe_decode<NT, 64, 16>); \
-        if (!wide_h && wide_i) return reinterpret_cast<const void*>(&k_moe_decode<NT, 64, 32>);  \
-        if (wide_h && !wide_i) return reinterpret_cast<const void*>(&k_moe_decode<NT, 80, 16>);  \
-        return reinterpret_cast<const void*>(&k_moe_decode<NT, 80, 32>);                         \
+    const bool wide_e = c->shape.experts > 512;
+#define FW_DECODE_VARIANT(NT, TK)                                                                      \
+    if (T == NT && wide_e == (TK == 16)) {                                                             \
+        if (!wide_h && !wide_i) return reinterpret_cast<const void*>(&k_moe_decode<NT, 64, 16, TK>); \
+        if (!wide_h && wide_i) return reinterpret_cast<const void*>(&k_moe_decode<NT, 64, 32, TK>);  \
+        if (wide_h && !wide_i) return reinterpret_cast<const void*>(&k_moe_decode<NT, 80, 16, TK>);  \
+        return reinterpret_cast<const void*>(&k_moe_decode<NT, 80, 32, TK>);                         \
     }
-    FW_DECODE_VARIANT(1)
-    FW_DECODE_VARIANT(2)
-    FW_DECODE_VARIANT(3)
-    FW_DECODE_VARIANT(4)
+    FW_DECODE_VARIANT(1, 8)
+    FW_DECODE_VARIANT(2, 8)
+    FW_DECODE_VARIANT(3, 8)
+    FW_DECODE_VARIANT(4, 8)
+    FW_DECODE_VARIANT(1, 16)
+    FW_DECODE_VARIANT(2, 16)
+    FW_DECODE_VARIANT(3, 16)
+    FW_DECODE_VARIANT(4, 16)
 #undef FW_DECODE_VARIANT
     throw HipError{"no decode kernel for this token count"};
 }
@@ -372,7 +384,7 @@ int decode_grid(const firewing_hip_context* c, int T) {
 }
 
 // Launch the persistent kernel over layers [first, first + n) for T tokens.
-// x[0] of the scratch must already hold the input.
+// x_in holds the input of the first layer ([T][H] bf16, 4-byte aligned).
 void launch_decode(firewing_hip_context* c, size_t first, size_t n, int T, int order,
                    bool prenorm, bool bias_feature, const uint16_t* x_in, uint16_t* x_final,
                    hipStream_t s) {
@@ -393,24 +405,19 @@ void launch_decode(firewing_hip_context* c, size_t first, size_t n, int T, int o
     const size_t L = n, Tn = (size_t)T, H = sh.hidden, E = sh.experts, K = sh.top_k;
     const size_t S = (size_t)p.S, I = sh.intermediate, Is = sh.shared_intermediate;
     p.x_in = x_in;
-    p.x = c->x;
-    p.x_final = x_final;
-    p.h = c->h;
-    p.out = c->out;
+    p.xw = c->xw;
     p.logits = c->logits;
-    p.ls = (int)logit_stride(E);
+    p.ls = logit_stride((int)E);
     p.gi = p.ls - 2;
-    p.ids = c->ids;
-    p.scores = c->scores;
-    p.slot_expert = c->slot_expert;
-    p.slot_tokens = c->slot_tokens;
-    p.union_count = c->union_count;
-    p.token_slots = c->token_slots;
-    p.token_weights = c->token_weights;
-    p.sig = c->sig;
     p.shared_act = c->shared_act;
     p.act = c->act;
+    p.x_final = x_final;
+    p.out = c->out;
+    p.ids = c->ids;
+    p.scores = c->scores;
+    p.sig = c->sig;
     p.counters = c->counters;
+    p.flags = c->flags;
     p.error = c->error;
     p.limit_ticks = (uint64_t)(c->timeout_seconds * (double)c->wall_clock_hz);
     p.n_router = (int)((E + kRouterRowsPerTask - 1) / kRouterRowsPerTask) + 1;
@@ -421,12 +428,12 @@ void launch_decode(firewing_hip_context* c, size_t first, size_t n, int T, int o
     (void)L;
     (void)Tn;
     (void)K;
-    // Roles: one workgroup selects experts; the combine role gets one
-    // workgroup per C task of a layer where the grid allows (so every task's
-    // down rows are in flight before the gate/up phase ends), at most half.
+    // Roles: the combine role gets one workgroup per C task of a layer where
+    // the grid allows (so every task's down rows are in flight before the
+    // gate/up phase ends), at most half of the grid.
     const int grid = c->grid[T];
-    p.g_comb = std::min(p.n_c, (grid - 1) / 2);
-    p.g_rows = grid - 1 - p.g_comb;
+    p.g_comb = std::min(p.n_c, grid / 2);
+    p.g_rows = grid - p.g_comb;
     if (p.g_comb < 1 || p.g_rows < 1) throw HipError{"decode grid too small for its roles"};
     p.trace = c->trace;
     // The kernel reads its parameters from a device copy; upload only on change
@@ -437,7 +444,10 @@ void launch_decode(firewing_hip_context* c, size_t first, size_t n, int T, int o
         c->params_valid = true;
     }
     const DecodeParams* dp = c->d_params;
-    void* args[] = {&dp};
+    // a fresh tag for this launch's exchanged words (0 is never used)
+    c->epoch = c->epoch + 1 == 0 ? 1 : c->epoch + 1;
+    uint32_t epoch = c->epoch;
+    void* args[] = {&dp, &epoch};
     const void* fn = decode_kernel(c, T);
     check(hipLaunchCooperativeKernel(fn, dim3(grid), dim3(256), args, 0, s),
           "hipLaunchCooperativeKernel(k_moe_decode)");
@@ -703,24 +713,27 @@ bool firewing_hip_create(const firewing_hip_shape* shape, firewing_hip_context**
         check(hipMemcpy(c->d_layers, layers.data(), L * sizeof(DecodeLayer), hipMemcpyHostToDevice),
               "hipMemcpy layers");
         const size_t T = kMaxTokens, S = K * T;
-        c->x = dalloc<uint16_t>((L + 1) * T * H);
+        c->xin = dalloc<uint16_t>(T * H);
+        c->xfinal = dalloc<uint16_t>(T * H);
         c->out = dalloc<uint16_t>(L * T * H);
-        c->logits = dalloc<uint16_t>(L * T * logit_stride(E));
         c->ids = dalloc<int32_t>(L * T * K);
         c->scores = dalloc<uint16_t>(L * T * K);
-        c->slot_expert = dalloc<int32_t>(L * S);
-        c->slot_tokens = dalloc<uint32_t>(L * S);
-        c->union_count = dalloc<int32_t>(L);
-        c->token_slots = dalloc<int32_t>(L * T * K);
-        c->token_weights = dalloc<uint32_t>(L * T * K);
-        c->sig = dalloc<uint32_t>(L * T);
-        c->shared_act = dalloc<uint16_t>(L * T * Is);
-        c->h = dalloc<uint16_t>(L * T * H);
-        c->act = dalloc<uint16_t>(L * S * T * I);
+        c->sig = dalloc<uint16_t>(L * T);
+        c->xw = dalloc<uint64_t>((L + 1) * T * H / 2);
+        c->logits = dalloc<uint64_t>(L * T * logit_stride((int)E) / 2);
+        c->shared_act = dalloc<uint64_t>(L * T * Is / 2);
+        c->act = dalloc<uint64_t>(L * S * T * I / 2);
+        // tags start at zero: no launch uses epoch 0
+        check(hipMemset(c->xw, 0, (L + 1) * T * H / 2 * 8), "hipMemset");
+        check(hipMemset(c->logits, 0, L * T * logit_stride((int)E) / 2 * 8), "hipMemset");
+        check(hipMemset(c->shared_act, 0, L * T * Is / 2 * 8), "hipMemset");
+        check(hipMemset(c->act, 0, L * S * T * I / 2 * 8), "hipMemset");
         c->counters = dalloc<uint32_t>(L * kCountersPerLayer + 1);
         c->error = dalloc<int32_t>(1);
         c->d_params = dalloc<DecodeParams>(1);
         check(hipMemset(c->counters, 0, (L * kCountersPerLayer + 1) * 4), "hipMemset counters");
+        c->flags = dalloc<uint32_t>(L * kCountersPerLayer * kFlagCopies);
+        check(hipMemset(c->flags, 0, L * kCountersPerLayer * kFlagCopies * 4), "hipMemset flags");
         check(hipMemset(c->error, 0, 4), "hipMemset error");
         for (int t = 1; t <= kMaxTokens; ++t) c->grid[t] = decode_grid(c, t);
         // zero the banks so uninstalled layers are defined
@@ -753,10 +766,9 @@ void firewing_hip_destroy(firewing_hip_context* c) {
     freev(c->shared_gate);
     freev(c->shared_up);
     freev(c->shared_down);
-    void* bufs[] = {c->d_layers, c->d_weight_table, c->x, c->out, c->logits, c->ids, c->scores,
-                    c->slot_expert, c->slot_tokens, c->union_count, c->token_slots,
-                    c->token_weights, c->sig, c->shared_act, c->act, c->counters, c->error,
-                    c->d_params, c->h};
+    void* bufs[] = {c->d_layers, c->d_weight_table, c->xin, c->xfinal, c->out, c->ids, c->scores,
+                    c->sig, c->xw, c->logits, c->shared_act, c->act, c->counters, c->flags, c->error,
+                    c->d_params};
     for (void* b : bufs)
         if (b) (void)hipFree(b);
     if (c->stream) (void)hipStreamDestroy(c->stream);
@@ -998,14 +1010,23 @@ bool firewing_hip_sparse_moe_block(firewing_hip_context* c, size_t layer,
         if (layer >= c->shape.layers) return fail("sparse_moe_block: layer out of range");
         hipStream_t s = c->stream;
         const size_t H = c->shape.hidden, E = c->shape.experts, K = c->shape.top_k;
-        upload(c->x, hidden, tokens * H * 2, s);
-        launch_decode(c, layer, 1, (int)tokens, order, false, false, c->x, nullptr, s);
+        upload(c->xin, hidden, tokens * H * 2, s);
+        launch_decode(c, layer, 1, (int)tokens, order, false, false, c->xin, nullptr, s);
         if (!check_device_error(c, s)) return false;
         download(out, c->out, tokens * H * 2, s);
         if (cap) {
             if (cap->router_logits) {
-                for (size_t t = 0; t < tokens; ++t)
-                    download(cap->router_logits + t * E, c->logits + t * logit_stride(E), E * 2, s);
+                // tagged words: two logits in the low half of each
+                const size_t words = tokens * logit_stride((int)E) / 2;
+                std::vector<uint64_t> lw(words);
+                download(lw.data(), c->logits, words * 8, s);
+                check(hipStreamSynchronize(s), "hipStreamSynchronize");
+                for (size_t t = 0; t < tokens; ++t) {
+                    for (size_t e = 0; e < E; ++e) {
+                        const uint64_t wd = lw[(t * logit_stride((int)E) + e) / 2];
+                        cap->router_logits[t * E + e] = (uint16_t)(wd >> (16 * (e & 1)));
+                    }
+                }
             }
             if (cap->selected_experts) {
                 std::vector<int32_t> ids(tokens * K);
@@ -1014,12 +1035,7 @@ bool firewing_hip_sparse_moe_block(firewing_hip_context* c, size_t layer,
                 for (size_t i = 0; i < ids.size(); ++i) cap->selected_experts[i] = (size_t)ids[i];
             }
             if (cap->selected_scores) download(cap->selected_scores, c->scores, tokens * K * 2, s);
-            if (cap->shared_gate_sigmoid) {
-                uint32_t sig[kMaxTokens];
-                download(sig, c->sig, tokens * 4, s);
-                check(hipStreamSynchronize(s), "hipStreamSynchronize");
-                for (size_t t = 0; t < tokens; ++t) cap->shared_gate_sigmoid[t] = (uint16_t)sig[t];
-            }
+            if (cap->shared_gate_sigmoid) download(cap->shared_gate_sigmoid, c->sig, tokens * 2, s);
             if (cap->routed_mixture) return fail("sparse_moe_block: routed_mixture capture is not kept by the fused kernel");
         }
         check(hipStreamSynchronize(s), "hipStreamSynchronize");
@@ -1061,10 +1077,10 @@ bool firewing_hip_moe_step(firewing_hip_context* c, const uint16_t* hidden, size
         if (!hidden || !residual) return fail("moe_step: null pointer");
         hipStream_t s = c->stream;
         const size_t L = c->shape.layers, H = c->shape.hidden, K = c->shape.top_k;
-        upload(c->x, hidden, tokens * H * 2, s);
-        launch_decode(c, 0, L, (int)tokens, order, true, bias_feature, c->x, nullptr, s);
+        upload(c->xin, hidden, tokens * H * 2, s);
+        launch_decode(c, 0, L, (int)tokens, order, true, bias_feature, c->xin, c->xfinal, s);
         if (!check_device_error(c, s)) return false;
-        download(residual, c->x + L * tokens * H, tokens * H * 2, s);
+        download(residual, c->xfinal, tokens * H * 2, s);
         if (block_out) download(block_out, c->out, L * tokens * H * 2, s);
         if (ids) download(ids, c->ids, L * tokens * K * 4, s);
         if (scores) download(scores, c->scores, L * tokens * K * 2, s);
@@ -1083,13 +1099,13 @@ extern "C" bool firewing_hip_debug_traced_step(firewing_hip_context* c, const ui
         const size_t L = c->shape.layers, H = c->shape.hidden;
         const size_t E = c->shape.experts, K = c->shape.top_k, I = c->shape.intermediate;
         const size_t Is = c->shape.shared_intermediate;
-        size_t per_layer = (E + 15) / 16 + 1 + (Is + 7) / 8 + 1 + K * tokens * (I / 8) + H / 4;
+        size_t per_layer = (E + 15) / 16 + 1 + (Is + 7) / 8 + K * tokens * (I / 8) + H / 4;
         size_t n = L * per_layer;
         if (cap < n * kTraceWords) return fail("trace buffer too small");
         c->trace = dalloc<uint64_t>(n * kTraceWords);
         check(hipMemset(c->trace, 0, n * kTraceWords * 8), "hipMemset trace");
-        upload(c->x, hidden, tokens * H * 2, c->stream);
-        launch_decode(c, 0, L, (int)tokens, 0, true, true, c->x, nullptr, c->stream);
+        upload(c->xin, hidden, tokens * H * 2, c->stream);
+        launch_decode(c, 0, L, (int)tokens, 0, true, true, c->xin, nullptr, c->stream);
         bool ok = check_device_error(c, c->stream);
         download(out, c->trace, n * kTraceWords * 8, c->stream);
         check(hipStreamSynchronize(c->stream), "hipStreamSynchronize");
