@@ -47,10 +47,9 @@ struct DecodeLayer {
 
 enum DecodeCounter : int {
     kCntRouter = 0,
-    kCntShared = 1,
-    kCntB = 2,
-    kCntC = 3,
-    kCountersPerLayer = 4
+    kCntGateUp = 1,  // S and B tasks
+    kCntC = 2,
+    kCountersPerLayer = 3
 };
 
 enum DecodeTaskKind : int { kTaskRouter = 0, kTaskShared = 1, kTaskGateUp = 3, kTaskDown = 4 };
@@ -91,7 +90,7 @@ struct DecodeParams {
     uint16_t* scores;   // [nlayers][T][K]
     uint16_t* sig;      // [nlayers][T] sigmoid of the shared_expert_gate logit
     uint32_t* counters;  // [nlayers][kCountersPerLayer] then 1 done counter
-    uint32_t* flags;     // [nlayers][kCountersPerLayer][kFlagCopies] epoch of the completed phase
+    uint32_t* flags;     // [nlayers][kCountersPerLayer][kFlagCopies * kFlagStride] epoch of the completed phase
     int32_t* error;      // 0 ok, 1 timeout, 2 NaN router logit
     uint64_t limit_ticks;
     int n_router, n_shared, n_b, n_c, S;
@@ -158,7 +157,7 @@ struct DecodeShared {
 };
 
 __device__ __forceinline__ uint32_t* phase_flags(const DecodeParams& p, int li, int phase) {
-    return p.flags + ((size_t)li * kCountersPerLayer + phase) * kFlagCopies;
+    return p.flags + ((size_t)li * kCountersPerLayer + phase) * kFlagCopies * kFlagStride;
 }
 
 // ---- block input ---------------------------------------------------------------------
@@ -214,7 +213,16 @@ __device__ __forceinline__ void normalise_input(const DecodeParams& p, DecodeSha
         const float* r = xs + w * n;
         float c = 0.0f;
         if (lane < 32) {
-            for (int b = 0; b < n / 32; ++b) {
+            // one chain per lane, blocks in order; LDS reads batched ahead of the adds
+            int b = 0;
+            for (; b + 16 <= n / 32; b += 16) {
+                float e[16];
+#pragma unroll
+                for (int i = 0; i < 16; ++i) e[i] = r[32 * (b + i) + lane];
+#pragma unroll
+                for (int i = 0; i < 16; ++i) c = add_rn(c, mul_rn(e[i], e[i]));
+            }
+            for (; b < n / 32; ++b) {
                 float e = r[32 * b + lane];
                 c = add_rn(c, mul_rn(e, e));
             }
@@ -419,15 +427,20 @@ __device__ __forceinline__ void rows_role(const DecodeParams* __restrict__ P, ui
             } else {
                 const int jb = j - p.n_router - p.n_shared;
                 const int s = jb / per_slot;
+                if (staged != li) {
+                    // the block input is ready with the previous layer: stage it
+                    // while the router runs
+                    if (li > 0 && !wait_phase(phase_flags(p, li - 1, kCntC), epoch, p.error, p.limit_ticks, &sh.flag))
+                        return;
+                    if (!load_input<NT>(p, li, epoch, sh)) return;
+                    normalise_input<NT>(p, sh);
+                    loaded = staged = li;
+                }
                 if (selected != li) {
-                    // the router tasks of this layer are done: logits and the
-                    // residual are both in memory
                     if (!wait_phase(phase_flags(p, li, kCntRouter), epoch, p.error, p.limit_ticks, &sh.flag)) return;
+                    FW_TRACE_MARK(slot_trace, 2);
                     if (!load_logits<NT>(p, li, epoch, sh)) return;
-                    if (loaded != li) {
-                        if (!load_input<NT>(p, li, epoch, sh)) return;
-                        loaded = li;
-                    }
+                    FW_TRACE_MARK(slot_trace, 3);
                     select_experts<NT, TK>(p, sh, false);
                     selected = li;
                 }
@@ -509,8 +522,8 @@ __device__ __forceinline__ void rows_role(const DecodeParams* __restrict__ P, ui
             FW_TRACE_MARK(slot_trace, 1);
         }
         {
-            const int phase = kind == kTaskRouter ? kCntRouter : (kind == kTaskShared ? kCntShared : kCntB);
-            const int count = kind == kTaskRouter ? p.n_router : (kind == kTaskShared ? p.n_shared : p.n_b);
+            const int phase = kind == kTaskRouter ? kCntRouter : kCntGateUp;
+            const int count = kind == kTaskRouter ? p.n_router : p.n_shared + p.n_b;
             publish(cnt + phase, (uint32_t)count, phase_flags(p, li, phase), epoch);
         }
         FW_TRACE_STAMP(t2);
@@ -615,11 +628,27 @@ __device__ __forceinline__ void combine_role(const DecodeParams* __restrict__ P,
         FW_ISSUE_DOWN(rs1, w + 4);
         FW_ISSUE_DOWN(rs2, w + 8);
         FW_ISSUE_DOWN(rs3, w + 12);
-        if (!(wait_phase(phase_flags(p, li, kCntB), epoch, p.error, p.limit_ticks, &sh.flag) &&
-              wait_phase(phase_flags(p, li, kCntShared), epoch, p.error, p.limit_ticks, &sh.flag)))
-            return;
-        FW_TRACE_STAMP(t1);
+        // The residual words this task updates (ready since the router ran),
+        // read while the gate/up phase runs: one thread per token and pair of
+        // hidden rows.
+        const int tid = threadIdx.x;
+        const bool mixer = tid < T * kRowsPerCTask / 2;
+        const int mt = tid / (kRowsPerCTask / 2);
+        const int g0 = 2 * (tid % (kRowsPerCTask / 2));
+        const size_t at = ((size_t)mt * H + r0 + g0) / 2;
         bool ok = true;
+        uint32_t rin = 0;
+        if (mixer) {
+            if (li == 0) {
+                rin = reinterpret_cast<const uint32_t*>(p.x_in)[at];
+            } else {
+                uint64_t v[1];
+                ok = load_tagged<1, 1>(v, p.xw + (size_t)li * T * H / 2 + at, 1, epoch, p.error, p.limit_ticks);
+                rin = (uint32_t)v[0];
+            }
+        }
+        if (!wait_phase(phase_flags(p, li, kCntGateUp), epoch, p.error, p.limit_ticks, &sh.flag)) return;
+        FW_TRACE_STAMP(t1);
         for (int m0 = w; m0 <= U; m0 += 16) {
             if (m0 != w) {
                 FW_ISSUE_DOWN(rs0, m0);
@@ -636,20 +665,8 @@ __device__ __forceinline__ void combine_role(const DecodeParams* __restrict__ P,
 #undef FW_ISSUE_DOWN
         FW_TRACE_MARK(slot_trace, 0);
         if (!__syncthreads_and(ok)) return;
-        const int tid = threadIdx.x;
-        if (tid < T * kRowsPerCTask / 2) {
-            // one thread per token and pair of hidden rows
-            const int tt = tid / (kRowsPerCTask / 2);
-            const int g0 = 2 * (tid % (kRowsPerCTask / 2));
-            const size_t at = ((size_t)tt * H + r0 + g0) / 2;
-            uint32_t rin;
-            if (li == 0) {
-                rin = reinterpret_cast<const uint32_t*>(p.x_in)[at];
-            } else {
-                uint64_t v[1];
-                ok = load_tagged<1, 1>(v, p.xw + (size_t)li * T * H / 2 + at, 1, epoch, p.error, p.limit_ticks);
-                rin = (uint32_t)v[0];
-            }
+        if (mixer) {
+            const int tt = mt;
             uint32_t o2 = 0, x2 = 0;
             for (int half = 0; half < 2; ++half) {
                 const int gg = g0 + half;

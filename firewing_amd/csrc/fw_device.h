@@ -322,6 +322,7 @@ __device__ __forceinline__ void wave_topk(const uint16_t* __restrict__ logits, i
 //   dozen workgroups.
 
 constexpr int kFlagCopies = 64;
+constexpr int kFlagStride = 64;  // words between copies (256 bytes: different memory channels)
 
 // Announce a finished task of a phase of `target` tasks. Every wave has issued
 // its tagged stores (program order up to the barrier).
@@ -331,7 +332,7 @@ __device__ __forceinline__ void publish(uint32_t* counter, uint32_t target, uint
         const uint32_t before =
             __hip_atomic_fetch_add(as_global_rw(counter), 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         if (before + 1u == target) {
-            for (int i = 0; i < kFlagCopies; ++i) coherent_store(flags + i, epoch);
+            for (int i = 0; i < kFlagCopies; ++i) coherent_store(flags + i * kFlagStride, epoch);
         }
     }
 }
@@ -342,7 +343,7 @@ __device__ __forceinline__ void publish(uint32_t* counter, uint32_t target, uint
 __device__ __forceinline__ bool wait_phase(const uint32_t* flags, uint32_t epoch, int32_t* error,
                                            uint64_t limit_ticks, int32_t* lds_flag) {
     if (threadIdx.x == 0) {
-        const uint32_t* f = flags + (blockIdx.x % kFlagCopies);
+        const uint32_t* f = flags + (blockIdx.x % kFlagCopies) * kFlagStride;
         int32_t ok = 1;
         if (coherent_load(f) != epoch) {
             uint64_t start = wall_clock64();

@@ -732,8 +732,8 @@ bool firewing_hip_create(const firewing_hip_shape* shape, firewing_hip_context**
         c->error = dalloc<int32_t>(1);
         c->d_params = dalloc<DecodeParams>(1);
         check(hipMemset(c->counters, 0, (L * kCountersPerLayer + 1) * 4), "hipMemset counters");
-        c->flags = dalloc<uint32_t>(L * kCountersPerLayer * kFlagCopies);
-        check(hipMemset(c->flags, 0, L * kCountersPerLayer * kFlagCopies * 4), "hipMemset flags");
+        c->flags = dalloc<uint32_t>(L * kCountersPerLayer * kFlagCopies * kFlagStride);
+        check(hipMemset(c->flags, 0, L * kCountersPerLayer * kFlagCopies * kFlagStride * 4), "hipMemset flags");
         check(hipMemset(c->error, 0, 4), "hipMemset error");
         for (int t = 1; t <= kMaxTokens; ++t) c->grid[t] = decode_grid(c, t);
         // zero the banks so uninstalled layers are defined
