@@ -3,7 +3,8 @@
 // mixture -> combine, chained through the residual stream).
 //
 // The co-resident workgroups (cooperative launch) are split into two roles,
-// each walking its own task list in (layer, phase) order:
+// each walking its own task list in (layer, phase) order (B tasks beyond one
+// per rows workgroup run on the combine role, ahead of its C tasks):
 //
 //   rows     R  router rows, 16 per task (rows [0, E)), plus one task for the
 //               shared_expert_gate row                  -> logits
@@ -93,25 +94,24 @@ struct DecodeParams {
     uint32_t* flags;     // [nlayers][kCountersPerLayer][kFlagCopies * kFlagStride] epoch of the completed phase
     int32_t* error;      // 0 ok, 1 timeout, 2 NaN router logit
     uint64_t limit_ticks;
-    int n_router, n_shared, n_b, n_c, S;
-    int n_rows;          // R + S + B tasks per layer
-    int g_rows, g_comb;  // workgroups of the rows and combine roles
+    int n_router, n_shared, n_b, n_c, S;  // tasks per layer; slots
+    int nb_rows;                          // B tasks per layer on the rows role (the rest on combine)
+    int g_rows, g_comb;                   // workgroups of the rows and combine roles
     uint64_t* trace;     // profiling builds only
 };
 
-// Task timing (wall clock) for profiling builds only. Trace slot of a task:
-// layer * (n_rows + n_c) + [R, S, B | C] index.
+// Task timing (wall clock) for profiling builds only (slots: trace_slot).
 #ifdef FW_DECODE_TRACE
-constexpr int kTraceWords = 8;  // start, dependency met, end, wg << 8 | kind, 4 stage marks
+constexpr int kTraceWords = 12;  // start, dependency met, end, wg << 8 | kind, 8 stage marks
 #define FW_TRACE_STAMP(var) const uint64_t var = wall_clock64()
 #define FW_TRACE_MARK(slot_, k)                                                    \
     do {                                                                           \
-        if (threadIdx.x == 0 && p.trace != nullptr)                                \
+        if (threadIdx.x == 0 && p.trace != nullptr && (slot_) >= 0)                \
             p.trace[(size_t)(slot_) * kTraceWords + 4 + (k)] = wall_clock64();     \
     } while (0)
 #define FW_TRACE_WRITE(slot_, kind, a, b, c)                                       \
     do {                                                                           \
-        if (threadIdx.x == 0 && p.trace != nullptr) {                              \
+        if (threadIdx.x == 0 && p.trace != nullptr && (slot_) >= 0) {              \
             uint64_t* tr = p.trace + (size_t)(slot_) * kTraceWords;                \
             tr[0] = (a);                                                           \
             tr[1] = (b);                                                           \
@@ -146,8 +146,6 @@ struct DecodeShared {
     int32_t ids[NT * kMaxTopK];                               // rank order per token
     int32_t sorted[kMaxTopK * NT];                            // union, ascending id
     uint32_t slot_tokens[kMaxTopK * NT];
-    int32_t slot_of[NT * kMaxTopK];
-    int32_t first[NT * kMaxTopK];
     int32_t tslot[NT * kMaxTopK];     // [t][k]: slot of the token's k-th expert in ascending id
     uint16_t tweight[NT * kMaxTopK];  // [t][k]: its bf16 score
     uint16_t sig[NT];
@@ -271,9 +269,11 @@ __device__ __forceinline__ bool load_logits(const DecodeParams& p, int li, uint3
 // error word is set; the launch then completes and reports it). TK: logits per
 // lane in the top-k (E <= 64 * TK).
 template <int NT, int TK>
-__device__ __forceinline__ void select_experts(const DecodeParams& p, DecodeShared<NT>& sh, bool reject_nan) {
+__device__ __forceinline__ void select_experts(const DecodeParams& p, DecodeShared<NT>& sh, bool reject_nan,
+                                               int slot_trace = -1) {
+    (void)slot_trace;
     const int T = p.T, E = p.E, K = p.K, S = p.S, LS = p.ls;
-    const int lane = lane_id(), w = wave_id(), tid = threadIdx.x;
+    const int lane = lane_id(), w = wave_id();
     if (w < T) {
         const uint16_t* lt = sh.lg + w * LS;
         if (reject_nan) {
@@ -283,39 +283,80 @@ __device__ __forceinline__ void select_experts(const DecodeParams& p, DecodeShar
         }
         wave_topk<TK>(lt, E, K, sh.ids + w * kMaxTopK);
     }
+    FW_TRACE_MARK(slot_trace, 4);
     __syncthreads();
-    // entry i = (token i / K, rank i % K)
-    const int n_sel = T * K;
-    int my_id = -1;
-    if (tid < n_sel) {
-        my_id = sh.ids[(tid / K) * kMaxTopK + tid % K];
-        int first = 1;
-        for (int i = 0; i < tid; ++i) first &= (sh.ids[(i / K) * kMaxTopK + i % K] != my_id);
-        sh.first[tid] = first;
+    FW_TRACE_MARK(slot_trace, 5);
+    // The union, by wave 0 in registers: lane l holds entries l and l + 64 of
+    // the T * K selections (entry i = token i / K, rank i % K); every loop
+    // runs over the entries in order with the entry's values read from its
+    // lane. One token selects distinct experts: its slots are the ranks of its
+    // ids.
+    if (w == 0 && T == 1) {
+        const int id = lane < K ? sh.ids[lane] : 0x7fffffff;
+        int rank = 0;
+        for (int j = 0; j < K; ++j) rank += (__builtin_amdgcn_readlane(id, j) < id) ? 1 : 0;
+        if (lane < K) {
+            sh.sorted[rank] = id;
+            sh.slot_tokens[rank] = 1u;
+            sh.tslot[rank] = rank;
+        }
+        for (int s2 = K + lane; s2 < S; s2 += kWave) sh.slot_tokens[s2] = 0u;
+        if (lane == 0) sh.nunion = K;
+    } else if (w == 0) {
+        const int n_sel = T * K;
+        int id[2], tok[2], slot[2] = {0, 0}, rank_in_token[2] = {0, 0};
+        bool first[2];
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            const int e = lane + kWave * h;
+            tok[h] = e / K;
+            id[h] = e < n_sel ? sh.ids[tok[h] * kMaxTopK + (e - tok[h] * K)] : 0x7fffffff;
+            first[h] = e < n_sel;
+        }
+        // first occurrence: no earlier entry selects the same expert
+        for (int j = 0; j < n_sel; ++j) {
+            const int idj = j < kWave ? __builtin_amdgcn_readlane(id[0], j) : __builtin_amdgcn_readlane(id[1], j - kWave);
+#pragma unroll
+            for (int h = 0; h < 2; ++h) first[h] = first[h] && !(j < lane + kWave * h && idj == id[h]);
+        }
+        const uint64_t f0 = __ballot(first[0]), f1 = __ballot(first[1]);
+        // slot = distinct experts with a smaller id; position among the token's own ids
+        for (int t = 0, j = 0; t < T; ++t) {
+            for (int r = 0; r < K; ++r, ++j) {
+                const int idj =
+                    j < kWave ? __builtin_amdgcn_readlane(id[0], j) : __builtin_amdgcn_readlane(id[1], j - kWave);
+                const bool fj = ((j < kWave ? f0 >> j : f1 >> (j - kWave)) & 1ull) != 0;
+#pragma unroll
+                for (int h = 0; h < 2; ++h) {
+                    slot[h] += (fj && idj < id[h]) ? 1 : 0;
+                    rank_in_token[h] += (t == tok[h] && idj < id[h]) ? 1 : 0;
+                }
+            }
+        }
+        // tokens of each slot
+        uint32_t mask[2] = {0u, 0u};
+        for (int t = 0, j = 0; t < T; ++t) {
+            for (int r = 0; r < K; ++r, ++j) {
+                const int sj = j < kWave ? __builtin_amdgcn_readlane(slot[0], j) : __builtin_amdgcn_readlane(slot[1], j - kWave);
+#pragma unroll
+                for (int h = 0; h < 2; ++h) mask[h] |= (sj == slot[h]) ? (1u << t) : 0u;
+            }
+        }
+        const int nunion = __popcll(f0) + __popcll(f1);
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            if (lane + kWave * h < n_sel) {
+                if (first[h]) {
+                    sh.sorted[slot[h]] = id[h];
+                    sh.slot_tokens[slot[h]] = mask[h];
+                }
+                sh.tslot[tok[h] * K + rank_in_token[h]] = slot[h];
+            }
+        }
+        for (int s2 = nunion + lane; s2 < S; s2 += kWave) sh.slot_tokens[s2] = 0u;
+        if (lane == 0) sh.nunion = nunion;
     }
-    __syncthreads();
-    if (tid < n_sel) {
-        int slot = 0;
-        for (int i = 0; i < n_sel; ++i) slot += (sh.first[i] && sh.ids[(i / K) * kMaxTopK + i % K] < my_id) ? 1 : 0;
-        sh.slot_of[tid] = slot;
-        if (sh.first[tid]) sh.sorted[slot] = my_id;
-        // position of this expert among the token's own ids, ascending
-        const int tt = tid / K;
-        int k = 0;
-        for (int r = 0; r < K; ++r) k += (sh.ids[tt * kMaxTopK + r] < my_id) ? 1 : 0;
-        sh.tslot[tt * K + k] = slot;
-    }
-    if (tid == 0) {
-        int n = 0;
-        for (int i = 0; i < n_sel; ++i) n += sh.first[i];
-        sh.nunion = n;
-    }
-    __syncthreads();
-    if (tid < S) {
-        uint32_t mask = 0;
-        for (int i = 0; i < n_sel; ++i) mask |= (sh.slot_of[i] == tid) ? (1u << (i / K)) : 0u;
-        sh.slot_tokens[tid] = tid < sh.nunion ? mask : 0u;
-    }
+    FW_TRACE_MARK(slot_trace, 6);
     __syncthreads();
 }
 
@@ -371,180 +412,203 @@ __device__ __forceinline__ void score_experts(const DecodeParams& p, int li, Dec
     __syncthreads();
 }
 
-// ---- rows role: R, S and B tasks ------------------------------------------------------
+// ---- tasks ----------------------------------------------------------------------------
 //
 // A wave covers 4 rows (16 lanes each). R task: 16 router rows; the last R
 // task of a layer is the shared_expert_gate row alone. S and B tasks: 8
 // gate/up pairs, wave w taking pairs 2w and 2w+1 with its lane groups 0, 1 on
 // the gate rows and 2, 3 on the up rows, so SwiGLU joins lane l and l + 32.
 // R and S issue their weight loads before waiting for the previous layer; B
-// waits for the router, selects, then issues its expert's rows and
-// normalises the input while they arrive.
+// stages and normalises the input once the previous layer is done, waits for
+// the router, selects, then issues its expert's rows.
 
-template <int NT, int MBH, int TK>
-__device__ __forceinline__ void rows_role(const DecodeParams* __restrict__ P, uint32_t epoch, DecodeShared<NT>& sh,
-                                          int rank) {
-    const DecodeParams& p = *P;
-    const int lane = lane_id(), w = wave_id(), g = lane / kLanesPerRow, q = lane % kLanesPerRow;
-    const int T = p.T, H = p.H, I = p.I, E = p.E, Is = p.Is;
-    const int nbh = H / 32;
-    const int per_slot = I / kPairsPerTask;
-    const int total = p.nlayers * p.n_rows;
-    int loaded = -1, staged = -1, selected = -1;  // layer whose raw input / block input / selection LDS holds
-    for (int t = rank; t < total; t += p.g_rows) {
-        FW_TRACE_STAMP(t0);
-        const int li = t / p.n_rows;
-        const int j = t - li * p.n_rows;
-        const int slot_trace = li * (p.n_rows + p.n_c) + j;
-        (void)slot_trace;
-        const DecodeLayer& L = p.layers[li];
-        uint32_t* cnt = p.counters + (size_t)li * kCountersPerLayer;
-        const int kind = j < p.n_router ? kTaskRouter : (j < p.n_router + p.n_shared ? kTaskShared : kTaskGateUp);
-        const bool gate_task = kind == kTaskRouter && j == p.n_router - 1;
-        // rows of this lane group
-        const uint16_t* wrow;
-        int out_index;
-        bool valid = true, wave_active = true, fold = false, work = true;
-        uint32_t mask = (1u << T) - 1u;
-        uint64_t* act_out = nullptr;
-        int act_stride = 0;  // words per token
-        if (kind == kTaskRouter) {
-            const int row0 = gate_task ? E : j * kRouterRowsPerTask;
-            const int rows = gate_task ? 1 : min(kRouterRowsPerTask, E - row0);
-            const int rin = w * kRowsPerWave + g;
-            wave_active = w * kRowsPerWave < rows;
-            valid = rin < rows;
-            fold = p.order == 1 && !gate_task;
-            out_index = row0 + (valid ? rin : 0);
-            wrow = L.router + (size_t)out_index * H;
-        } else {
-            int pair0;
-            if (kind == kTaskShared) {
-                pair0 = (j - p.n_router) * kPairsPerTask;
-                act_out = p.shared_act + (size_t)li * T * (Is / 2);
-                act_stride = Is / 2;
-                wrow = g < 2 ? L.shared_gate : L.shared_up;
-            } else {
-                const int jb = j - p.n_router - p.n_shared;
-                const int s = jb / per_slot;
-                if (staged != li) {
-                    // the block input is ready with the previous layer: stage it
-                    // while the router runs
-                    if (li > 0 && !wait_phase(phase_flags(p, li - 1, kCntC), epoch, p.error, p.limit_ticks, &sh.flag))
-                        return;
-                    if (!load_input<NT>(p, li, epoch, sh)) return;
-                    normalise_input<NT>(p, sh);
-                    loaded = staged = li;
-                }
-                if (selected != li) {
-                    if (!wait_phase(phase_flags(p, li, kCntRouter), epoch, p.error, p.limit_ticks, &sh.flag)) return;
-                    FW_TRACE_MARK(slot_trace, 2);
-                    if (!load_logits<NT>(p, li, epoch, sh)) return;
-                    FW_TRACE_MARK(slot_trace, 3);
-                    select_experts<NT, TK>(p, sh, false);
-                    selected = li;
-                }
-                work = s < uniform(sh.nunion);
-                const int e = work ? uniform(sh.sorted[s]) : 0;
-                mask = work ? (uint32_t)uniform((int)sh.slot_tokens[s]) : 0u;
-                const uint16_t* gate_w = L.gate_up + (size_t)e * 2 * I * H;
-                pair0 = (jb - s * per_slot) * kPairsPerTask;
-                act_out = p.act + ((size_t)li * p.S + s) * (size_t)T * (I / 2);
-                act_stride = I / 2;
-                wrow = g < 2 ? gate_w : gate_w + (size_t)I * H;
-            }
-            out_index = pair0 + 2 * w + (g & 1);
-            wrow += (size_t)out_index * H;
-        }
-        RowShare<MBH> rs;
-        if (work && wave_active && !fold) row_issue(rs, reinterpret_cast<const uint32_t*>(wrow), nbh, q);
-        if (kind != kTaskGateUp && li > 0 &&
-            !wait_phase(phase_flags(p, li - 1, kCntC), epoch, p.error, p.limit_ticks, &sh.flag))
-            return;
-        FW_TRACE_STAMP(t1);
-        if (work) {
-            if (staged != li) {
-                if (loaded != li) {
-                    if (!load_input<NT>(p, li, epoch, sh)) return;
-                    loaded = li;
-                }
-                normalise_input<NT>(p, sh);
-                staged = li;
-            }
-            FW_TRACE_MARK(slot_trace, 0);
-            if (fold) {
-                // src/router.rs:228-240: one lane folds one row; lanes 0 and 2
-                // store the pairs of rows (r, r + 1).
-                uint64_t* lw = p.logits + (size_t)li * T * (p.ls / 2);
-                const int r = j * kRouterRowsPerTask + w * kRowsPerWave + lane;
-                const bool mine = lane < kRowsPerWave && r < E;
-                for (int tt = 0; tt < T; ++tt) {
-                    uint32_t bits = mine ? to_bf16(fold_row(L.router + (size_t)r * H, sh.xs + tt * H, H)) : 0u;
-                    uint32_t next = (uint32_t)__shfl_down((int)bits, 1, kWave);
-                    if (mine && (lane & 1) == 0)
-                        coherent_store64(lw + (tt * p.ls + r) / 2, tagged(bits | (next << 16), epoch));
-                }
-            } else if (wave_active) {
-                float acc[NT][2];
-                row_chains<NT, MBH>(rs, nbh, sh.xs, H, q, acc);
-                uint32_t bits[NT];
-#pragma unroll
-                for (int tt = 0; tt < NT; ++tt) {
-                    float d = tree32_reduce(acc[tt][0], acc[tt][1]);
-                    if (q == 0) d = tree32_finish(d, wrow, sh.xs + tt * H, H);
-                    bits[tt] = to_bf16(d);
-                }
-                if (kind == kTaskRouter) {
-                    // groups 0 and 2 store the pairs (row, row + 1); the gate
-                    // logit goes to its own slot with a zero beside it
-                    uint64_t* lw = p.logits + (size_t)li * T * (p.ls / 2);
-                    const int at = gate_task ? p.gi : out_index;
-#pragma unroll
-                    for (int tt = 0; tt < NT; ++tt) {
-                        uint32_t next = (uint32_t)__shfl((int)bits[tt], (lane + kLanesPerRow) & 63, kWave);
-                        if (gate_task) next = 0u;
-                        if (q == 0 && (g & 1) == 0 && valid)
-                            coherent_store64(lw + (tt * p.ls + at) / 2, tagged(bits[tt] | (next << 16), epoch));
-                    }
-                } else {
-                    // gate (groups 0, 1) meets up (groups 2, 3): lane l takes lane l + 32;
-                    // group 0 stores the pair (pair, pair + 1) with group 1's result
-#pragma unroll
-                    for (int tt = 0; tt < NT; ++tt) {
-                        uint32_t up = (uint32_t)__shfl((int)bits[tt], (lane + 32) & 63, kWave);
-                        uint32_t a = swiglu_bf16(bits[tt], up, sh.exp2tab);
-                        uint32_t b = (uint32_t)__shfl((int)a, (lane + kLanesPerRow) & 63, kWave);
-                        if (g == 0 && q == 0 && (mask & (1u << tt)))
-                            coherent_store64(act_out + (size_t)tt * act_stride + out_index / 2, tagged(a | (b << 16), epoch));
-                    }
-                }
-            }
-            FW_TRACE_MARK(slot_trace, 1);
-        }
-        {
-            const int phase = kind == kTaskRouter ? kCntRouter : kCntGateUp;
-            const int count = kind == kTaskRouter ? p.n_router : p.n_shared + p.n_b;
-            publish(cnt + phase, (uint32_t)count, phase_flags(p, li, phase), epoch);
-        }
-        FW_TRACE_STAMP(t2);
-        FW_TRACE_WRITE(slot_trace, kind, t0, t1, t2);
-    }
+// What this workgroup's LDS holds: the layer whose raw input / normalised
+// input / selection / scores are there (-1: none).
+struct LdsState {
+    int loaded = -1, staged = -1, selected = -1, scored = -1;
+};
+
+// Trace slot of a task: layer * (R + S + B + C tasks) + its index in that order.
+__device__ __forceinline__ int trace_slot(const DecodeParams& p, int li, int index) {
+    return li * (p.n_router + p.n_shared + p.n_b + p.n_c) + index;
 }
 
-// ---- combine role: C tasks -----------------------------------------------------------
-//
-// Matrix m of a task: m = 0 is the shared expert's down projection, m = 1 + s
-// the down projection of slot s. Wave w covers the task's 4 rows (16 lanes
-// each) of matrices w, w + 4, w + 8, w + 12 in its first batch, then the next
-// 16 matrices, and so on.
+// Block input of layer li in LDS, normalised.
+template <int NT>
+__device__ __forceinline__ bool stage_layer_input(const DecodeParams& p, uint32_t epoch, DecodeShared<NT>& sh,
+                                                  LdsState& st, int li) {
+    if (st.staged == li) return true;
+    if (st.loaded != li) {
+        if (!load_input<NT>(p, li, epoch, sh)) return false;
+        st.loaded = li;
+    }
+    normalise_input<NT>(p, sh);
+    st.staged = li;
+    return true;
+}
+
+// Selection of layer li in LDS (waits for its router tasks).
+template <int NT, int TK>
+__device__ __forceinline__ bool select_layer(const DecodeParams& p, uint32_t epoch, DecodeShared<NT>& sh, LdsState& st,
+                                             int li, bool reject_nan, int slot) {
+    if (st.selected == li) return true;
+    if (!wait_phase(phase_flags(p, li, kCntRouter), epoch, p.error, p.limit_ticks, &sh.flag)) return false;
+    FW_TRACE_MARK(slot, 2);
+    if (!load_logits<NT>(p, li, epoch, sh)) return false;
+    FW_TRACE_MARK(slot, 3);
+    select_experts<NT, TK>(p, sh, reject_nan, slot);
+    st.selected = li;
+    return true;
+}
+
+// R task j of layer li: 16 router rows, or the shared_expert_gate row.
+template <int NT, int MBH>
+__device__ __forceinline__ bool router_task(const DecodeParams& p, uint32_t epoch, DecodeShared<NT>& sh, LdsState& st,
+                                            int li, int j) {
+    FW_TRACE_STAMP(t0);
+    const int slot = trace_slot(p, li, j);
+    (void)slot;
+    const int lane = lane_id(), w = wave_id(), g = lane / kLanesPerRow, q = lane % kLanesPerRow;
+    const int T = p.T, H = p.H, E = p.E;
+    const DecodeLayer& L = p.layers[li];
+    const bool gate_task = j == p.n_router - 1;
+    const int row0 = gate_task ? E : j * kRouterRowsPerTask;
+    const int rows = gate_task ? 1 : min(kRouterRowsPerTask, E - row0);
+    const int rin = w * kRowsPerWave + g;
+    const bool wave_active = w * kRowsPerWave < rows;
+    const bool valid = rin < rows;
+    const bool fold = p.order == 1 && !gate_task;
+    const int out_index = row0 + (valid ? rin : 0);
+    const uint16_t* wrow = L.router + (size_t)out_index * H;
+    LineShare<MBH> rs;
+    if (wave_active && !fold) line_issue(rs, wrow, H / 32, q);
+    if (li > 0 && !wait_phase(phase_flags(p, li - 1, kCntC), epoch, p.error, p.limit_ticks, &sh.flag)) return false;
+    FW_TRACE_STAMP(t1);
+    if (!stage_layer_input<NT>(p, epoch, sh, st, li)) return false;
+    FW_TRACE_MARK(slot, 0);
+    uint64_t* lw = p.logits + (size_t)li * T * (p.ls / 2);
+    if (fold) {
+        // src/router.rs:228-240: one lane folds one row; lanes 0 and 2 store
+        // the pairs of rows (r, r + 1).
+        const int r = j * kRouterRowsPerTask + w * kRowsPerWave + lane;
+        const bool mine = lane < kRowsPerWave && r < E;
+        for (int tt = 0; tt < T; ++tt) {
+            uint32_t bits = mine ? to_bf16(fold_row(L.router + (size_t)r * H, sh.xs + tt * H, H)) : 0u;
+            uint32_t next = (uint32_t)__shfl_down((int)bits, 1, kWave);
+            if (mine && (lane & 1) == 0) coherent_store64(lw + (tt * p.ls + r) / 2, tagged(bits | (next << 16), epoch));
+        }
+    } else if (wave_active) {
+        float acc[NT][2];
+        line_chains<NT, MBH>(rs, H / 32, sh.xs, H, q, acc);
+        // groups 0 and 2 store the pairs (row, row + 1); the gate logit goes to
+        // its own slot with a zero beside it
+        const int at = gate_task ? p.gi : out_index;
+#pragma unroll
+        for (int tt = 0; tt < NT; ++tt) {
+            float d = tree32_reduce_lines(acc[tt][0], acc[tt][1]);
+            if (q == 0) d = tree32_finish(d, wrow, sh.xs + tt * H, H);
+            const uint32_t bits = to_bf16(d);
+            uint32_t next = (uint32_t)__shfl((int)bits, (lane + kLanesPerRow) & 63, kWave);
+            if (gate_task) next = 0u;
+            if (q == 0 && (g & 1) == 0 && valid) coherent_store64(lw + (tt * p.ls + at) / 2, tagged(bits | (next << 16), epoch));
+        }
+    }
+    FW_TRACE_MARK(slot, 1);
+    publish(p.counters + (size_t)li * kCountersPerLayer + kCntRouter, (uint32_t)p.n_router,
+            phase_flags(p, li, kCntRouter), epoch);
+    FW_TRACE_STAMP(t2);
+    FW_TRACE_WRITE(slot, kTaskRouter, t0, t1, t2);
+    return true;
+}
+
+// S task (shared = true, index js < n_shared) or B task (index js < n_b) of
+// layer li: 8 gate/up pairs with fused SwiGLU.
+template <int NT, int MBH, int TK>
+__device__ __forceinline__ bool pairs_task(const DecodeParams& p, uint32_t epoch, DecodeShared<NT>& sh, LdsState& st,
+                                           int li, int js, bool shared) {
+    FW_TRACE_STAMP(t0);
+    const int slot = trace_slot(p, li, p.n_router + (shared ? js : p.n_shared + js));
+    (void)slot;
+    const int lane = lane_id(), w = wave_id(), g = lane / kLanesPerRow, q = lane % kLanesPerRow;
+    const int T = p.T, H = p.H, I = p.I, Is = p.Is;
+    const DecodeLayer& L = p.layers[li];
+    const uint16_t* wrow;
+    uint64_t* act_out;
+    int act_stride, pair0;  // words per token
+    bool work = true;
+    uint32_t mask = (1u << T) - 1u;
+    if (shared) {
+        pair0 = js * kPairsPerTask;
+        act_out = p.shared_act + (size_t)li * T * (Is / 2);
+        act_stride = Is / 2;
+        wrow = g < 2 ? L.shared_gate : L.shared_up;
+    } else {
+        const int per_slot = I / kPairsPerTask;
+        const int s = js / per_slot;
+        if (st.staged != li) {
+            // the block input is ready with the previous layer: stage it while
+            // the router runs
+            if (li > 0 && !wait_phase(phase_flags(p, li - 1, kCntC), epoch, p.error, p.limit_ticks, &sh.flag))
+                return false;
+            if (!stage_layer_input<NT>(p, epoch, sh, st, li)) return false;
+        }
+        if (!select_layer<NT, TK>(p, epoch, sh, st, li, false, slot)) return false;
+        FW_TRACE_MARK(slot, 0);
+        work = s < uniform(sh.nunion);
+        const int e = work ? uniform(sh.sorted[s]) : 0;
+        mask = work ? (uint32_t)uniform((int)sh.slot_tokens[s]) : 0u;
+        const uint16_t* gate_w = L.gate_up + (size_t)e * 2 * I * H;
+        pair0 = (js - s * per_slot) * kPairsPerTask;
+        act_out = p.act + ((size_t)li * p.S + s) * (size_t)T * (I / 2);
+        act_stride = I / 2;
+        wrow = g < 2 ? gate_w : gate_w + (size_t)I * H;
+    }
+    const int out_index = pair0 + 2 * w + (g & 1);
+    wrow += (size_t)out_index * H;
+    LineShare<MBH> rs;
+    if (work) line_issue(rs, wrow, H / 32, q);
+    if (shared && li > 0 && !wait_phase(phase_flags(p, li - 1, kCntC), epoch, p.error, p.limit_ticks, &sh.flag))
+        return false;
+    FW_TRACE_STAMP(t1);
+    if (work) {
+        if (shared) {
+            if (!stage_layer_input<NT>(p, epoch, sh, st, li)) return false;
+            FW_TRACE_MARK(slot, 0);
+        }
+        float acc[NT][2];
+        line_chains<NT, MBH>(rs, H / 32, sh.xs, H, q, acc);
+        // gate (groups 0, 1) meets up (groups 2, 3): lane l takes lane l + 32;
+        // group 0 stores the pair (pair, pair + 1) with group 1's result
+#pragma unroll
+        for (int tt = 0; tt < NT; ++tt) {
+            float d = tree32_reduce_lines(acc[tt][0], acc[tt][1]);
+            if (q == 0) d = tree32_finish(d, wrow, sh.xs + tt * H, H);
+            const uint32_t bits = to_bf16(d);
+            const uint32_t up = (uint32_t)__shfl((int)bits, (lane + 32) & 63, kWave);
+            const uint32_t a = swiglu_bf16(bits, up, sh.exp2tab);
+            const uint32_t b = (uint32_t)__shfl((int)a, (lane + kLanesPerRow) & 63, kWave);
+            if (g == 0 && q == 0 && (mask & (1u << tt)))
+                coherent_store64(act_out + (size_t)tt * act_stride + out_index / 2, tagged(a | (b << 16), epoch));
+        }
+        FW_TRACE_MARK(slot, 1);
+    }
+    publish(p.counters + (size_t)li * kCountersPerLayer + kCntGateUp, (uint32_t)(p.n_shared + p.n_b),
+            phase_flags(p, li, kCntGateUp), epoch);
+    FW_TRACE_STAMP(t2);
+    FW_TRACE_WRITE(slot, shared ? kTaskShared : kTaskGateUp, t0, t1, t2);
+    return true;
+}
 
 // One down row against its activation words (tagged): the chains of
 // src/expert.rs:514-552 over K = nblocks * 32 (so the tail sum is +0.0), for
-// each token in mask (wave-uniform). Returns false on timeout or error.
+// each token in mask (wave-uniform). This lane's chain pair of block b is
+// activation pair 16 b + line_column(q) / 2. Returns false on timeout or
+// error.
 template <int NT, int MAXB>
-__device__ __forceinline__ bool down_row(const RowShare<MAXB>& r, int nblocks, const uint64_t* actw, int words_per_token,
+__device__ __forceinline__ bool down_row(const LineShare<MAXB>& r, int nblocks, const uint64_t* actw, int words_per_token,
                                          int q, uint32_t mask, uint32_t epoch, const DecodeParams& p,
                                          uint32_t (&bits)[NT]) {
+    const int col2 = line_column(q) / 2;
     bool ok = true;
 #pragma unroll
     for (int t = 0; t < NT; ++t) {
@@ -552,61 +616,58 @@ __device__ __forceinline__ bool down_row(const RowShare<MAXB>& r, int nblocks, c
         if (!(mask & (1u << t))) continue;
         const int nb = opaque(nblocks);
         uint64_t xv[MAXB];
-        ok = load_tagged<MAXB, 16>(xv, actw + (size_t)t * words_per_token + q, nb, epoch, p.error, p.limit_ticks) && ok;
+        ok = load_tagged<MAXB, 16>(xv, actw + (size_t)t * words_per_token + col2, nb, epoch, p.error, p.limit_ticks) && ok;
         float c0 = 0.0f, c1 = 0.0f;
 #pragma unroll
-        for (int u = 0; u < MAXB; ++u) {
-            if (u < nb) {
-                const uint32_t a = (uint32_t)xv[u];
-                c0 = add_rn(c0, mul_rn(bf16_lo(r.w[u]), bf16_lo(a)));
-                c1 = add_rn(c1, mul_rn(bf16_hi(r.w[u]), bf16_hi(a)));
+        for (int v = 0; v < (MAXB + 1) / 2; ++v) {
+            uint32_t first, second;
+            line_pairs(r.w[v], q, first, second);
+#pragma unroll
+            for (int half = 0; half < 2; ++half) {
+                const int u = 2 * v + half;
+                if (u < MAXB && u < nb) {
+                    const uint32_t wv = half ? second : first;
+                    const uint32_t a = (uint32_t)xv[u];
+                    c0 = add_rn(c0, mul_rn(bf16_lo(wv), bf16_lo(a)));
+                    c1 = add_rn(c1, mul_rn(bf16_hi(wv), bf16_hi(a)));
+                }
             }
         }
-        bits[t] = to_bf16(add_rn(tree32_reduce(c0, c1), 0.0f));
+        bits[t] = to_bf16(add_rn(tree32_reduce_lines(c0, c1), 0.0f));
     }
     return ok;
 }
 
+// C task j of layer li: hidden rows 4j .. 4j + 3. Matrix m of the task: m = 0
+// is the shared expert's down projection, m = 1 + s the down projection of
+// slot s. Wave w covers the 4 rows (16 lanes each) of matrices w, w + 4,
+// w + 8, w + 12 in its first batch, then the next 16 matrices, and so on.
 template <int NT, int MBI, int TK>
-__device__ __forceinline__ void combine_role(const DecodeParams* __restrict__ P, uint32_t epoch, DecodeShared<NT>& sh,
-                                             int rank) {
-    const DecodeParams& p = *P;
+__device__ __forceinline__ bool combine_task(const DecodeParams& p, uint32_t epoch, DecodeShared<NT>& sh, LdsState& st,
+                                             int li, int j) {
+    FW_TRACE_STAMP(t0);
+    const int slot = trace_slot(p, li, p.n_router + p.n_shared + p.n_b + j);
+    (void)slot;
     const int lane = lane_id(), w = wave_id(), g = lane / kLanesPerRow, q = lane % kLanesPerRow;
     const int T = p.T, H = p.H, I = p.I, Is = p.Is, K = p.K;
     const uint32_t all_tokens = (1u << T) - 1u;
-    const int total = p.nlayers * p.n_c;
-    int selected = -1;
-    for (int t = rank; t < total; t += p.g_comb) {
-        FW_TRACE_STAMP(t0);
-        const int li = t / p.n_c;
-        const int j = t - li * p.n_c;
-        const int slot_trace = li * (p.n_rows + p.n_c) + p.n_rows + j;
-        (void)slot_trace;
-        const DecodeLayer& L = p.layers[li];
-        uint32_t* cnt = p.counters + (size_t)li * kCountersPerLayer;
-        const int r0 = j * kRowsPerCTask;
-        const int row = r0 + g;
-        RowShare<MBI> rs0, rs1, rs2, rs3;
-        // the shared expert's rows need no selection: issue them first
-        if (w == 0) row_issue(rs0, reinterpret_cast<const uint32_t*>(L.shared_down + (size_t)row * Is), Is / 32, q);
-        if (selected != li) {
-            if (!wait_phase(phase_flags(p, li, kCntRouter), epoch, p.error, p.limit_ticks, &sh.flag)) return;
-            if (!load_logits<NT>(p, li, epoch, sh)) return;
-            const bool host_outputs = j == 0;
-            select_experts<NT, TK>(p, sh, host_outputs && p.order == 0);
-            score_experts<NT>(p, li, sh, host_outputs);
-            selected = li;
-        }
-        const int U = uniform(sh.nunion);
-#define FW_ISSUE_DOWN(RS, M)                                                                              \
-    do {                                                                                                  \
-        const int m_ = (M);                                                                               \
-        if (m_ >= 1 && m_ <= U) {                                                                         \
-            const uint16_t* wm_ = L.down + (size_t)uniform(sh.sorted[m_ - 1]) * (size_t)H * I;            \
-            row_issue(RS, reinterpret_cast<const uint32_t*>(wm_ + (size_t)row * I), I / 32, q);            \
-        } else if (m_ == 0) {                                                                             \
-            row_issue(RS, reinterpret_cast<const uint32_t*>(L.shared_down + (size_t)row * Is), Is / 32, q); \
-        }                                                                                                 \
+    const DecodeLayer& L = p.layers[li];
+    const int r0 = j * kRowsPerCTask;
+    const int row = r0 + g;
+    LineShare<MBI> rs0, rs1, rs2, rs3;
+    // the shared expert's rows need no selection: issue them first
+    if (w == 0) line_issue(rs0, L.shared_down + (size_t)row * Is, Is / 32, q);
+    if (!select_layer<NT, TK>(p, epoch, sh, st, li, j == 0 && p.order == 0, -1)) return false;
+    const int U = uniform(sh.nunion);
+#define FW_ISSUE_DOWN(RS, M)                                                                  \
+    do {                                                                                      \
+        const int m_ = (M);                                                                   \
+        if (m_ >= 1 && m_ <= U) {                                                             \
+            const uint16_t* wm_ = L.down + (size_t)uniform(sh.sorted[m_ - 1]) * (size_t)H * I; \
+            line_issue(RS, wm_ + (size_t)row * I, I / 32, q);                                  \
+        } else if (m_ == 0) {                                                                 \
+            line_issue(RS, L.shared_down + (size_t)row * Is, Is / 32, q);                      \
+        }                                                                                     \
     } while (0)
 #define FW_DOWN_DOT(RS, M)                                                                                \
     do {                                                                                                  \
@@ -624,77 +685,128 @@ __device__ __forceinline__ void combine_role(const DecodeParams* __restrict__ P,
             }                                                                                             \
         }                                                                                                 \
     } while (0)
-        if (w != 0) FW_ISSUE_DOWN(rs0, w);
-        FW_ISSUE_DOWN(rs1, w + 4);
-        FW_ISSUE_DOWN(rs2, w + 8);
-        FW_ISSUE_DOWN(rs3, w + 12);
-        // The residual words this task updates (ready since the router ran),
-        // read while the gate/up phase runs: one thread per token and pair of
-        // hidden rows.
-        const int tid = threadIdx.x;
-        const bool mixer = tid < T * kRowsPerCTask / 2;
-        const int mt = tid / (kRowsPerCTask / 2);
-        const int g0 = 2 * (tid % (kRowsPerCTask / 2));
-        const size_t at = ((size_t)mt * H + r0 + g0) / 2;
-        bool ok = true;
-        uint32_t rin = 0;
-        if (mixer) {
-            if (li == 0) {
-                rin = reinterpret_cast<const uint32_t*>(p.x_in)[at];
-            } else {
-                uint64_t v[1];
-                ok = load_tagged<1, 1>(v, p.xw + (size_t)li * T * H / 2 + at, 1, epoch, p.error, p.limit_ticks);
-                rin = (uint32_t)v[0];
-            }
+    if (w != 0) FW_ISSUE_DOWN(rs0, w);
+    FW_ISSUE_DOWN(rs1, w + 4);
+    FW_ISSUE_DOWN(rs2, w + 8);
+    FW_ISSUE_DOWN(rs3, w + 12);
+    // The residual words this task updates (ready since the router ran), read
+    // while the gate/up phase runs: one thread per token and pair of rows.
+    const int tid = threadIdx.x;
+    const bool mixer = tid < T * kRowsPerCTask / 2;
+    const int mt = tid / (kRowsPerCTask / 2);
+    const int g0 = 2 * (tid % (kRowsPerCTask / 2));
+    const size_t at = ((size_t)mt * H + r0 + g0) / 2;
+    bool ok = true;
+    uint32_t rin = 0;
+    if (mixer) {
+        if (li == 0) {
+            rin = reinterpret_cast<const uint32_t*>(p.x_in)[at];
+        } else {
+            uint64_t v[1];
+            ok = load_tagged<1, 1>(v, p.xw + (size_t)li * T * H / 2 + at, 1, epoch, p.error, p.limit_ticks);
+            rin = (uint32_t)v[0];
         }
-        if (!wait_phase(phase_flags(p, li, kCntGateUp), epoch, p.error, p.limit_ticks, &sh.flag)) return;
-        FW_TRACE_STAMP(t1);
-        for (int m0 = w; m0 <= U; m0 += 16) {
-            if (m0 != w) {
-                FW_ISSUE_DOWN(rs0, m0);
-                FW_ISSUE_DOWN(rs1, m0 + 4);
-                FW_ISSUE_DOWN(rs2, m0 + 8);
-                FW_ISSUE_DOWN(rs3, m0 + 12);
-            }
-            FW_DOWN_DOT(rs0, m0);
-            FW_DOWN_DOT(rs1, m0 + 4);
-            FW_DOWN_DOT(rs2, m0 + 8);
-            FW_DOWN_DOT(rs3, m0 + 12);
+    }
+    if (st.scored != li) {
+        // route weights are needed only after the gate/up phase; the
+        // exponentials overwrite the staged input
+        score_experts<NT>(p, li, sh, j == 0);
+        st.scored = li;
+        st.loaded = st.staged = -1;
+    }
+    if (!wait_phase(phase_flags(p, li, kCntGateUp), epoch, p.error, p.limit_ticks, &sh.flag)) return false;
+    FW_TRACE_STAMP(t1);
+    for (int m0 = w; m0 <= U; m0 += 16) {
+        if (m0 != w) {
+            FW_ISSUE_DOWN(rs0, m0);
+            FW_ISSUE_DOWN(rs1, m0 + 4);
+            FW_ISSUE_DOWN(rs2, m0 + 8);
+            FW_ISSUE_DOWN(rs3, m0 + 12);
         }
+        FW_DOWN_DOT(rs0, m0);
+        FW_DOWN_DOT(rs1, m0 + 4);
+        FW_DOWN_DOT(rs2, m0 + 8);
+        FW_DOWN_DOT(rs3, m0 + 12);
+    }
 #undef FW_DOWN_DOT
 #undef FW_ISSUE_DOWN
-        FW_TRACE_MARK(slot_trace, 0);
-        if (!__syncthreads_and(ok)) return;
-        if (mixer) {
-            const int tt = mt;
-            uint32_t o2 = 0, x2 = 0;
-            for (int half = 0; half < 2; ++half) {
-                const int gg = g0 + half;
-                // src/decoder_layer.rs:528-545: weighted = bf16(down * score), summed
-                // in ascending expert order from bf16 zero, rounding after each add.
-                uint32_t mix = to_bf16(0.0f);
-                for (int k = 0; k < K; ++k) {
-                    uint32_t d = sh.res[((1 + sh.tslot[tt * K + k]) * NT + tt) * kRowsPerCTask + gg];
-                    uint32_t weighted = to_bf16(mul_rn(from_bf16(d), from_bf16(sh.tweight[tt * K + k])));
-                    mix = add_bf16(mix, weighted);
-                }
-                // src/decoder_layer.rs:563-575: gated = bf16(shared_down * sigmoid).
-                uint32_t sd = sh.res[(0 * NT + tt) * kRowsPerCTask + gg];
-                uint32_t gated = to_bf16(mul_rn(from_bf16(sd), from_bf16(sh.sig[tt])));
-                uint32_t o = add_bf16(mix, gated);
-                uint32_t xn = add_bf16((rin >> (16 * half)) & 0xffffu, o);
-                o2 |= o << (16 * half);
-                x2 |= xn << (16 * half);
+    FW_TRACE_MARK(slot, 0);
+    if (!__syncthreads_and(ok)) return false;
+    if (mixer) {
+        const int tt = mt;
+        uint32_t o2 = 0, x2 = 0;
+        for (int half = 0; half < 2; ++half) {
+            const int gg = g0 + half;
+            // src/decoder_layer.rs:528-545: weighted = bf16(down * score), summed in
+            // ascending expert order from bf16 zero, rounding after each add.
+            uint32_t mix = to_bf16(0.0f);
+            for (int k = 0; k < K; ++k) {
+                uint32_t d = sh.res[((1 + sh.tslot[tt * K + k]) * NT + tt) * kRowsPerCTask + gg];
+                uint32_t weighted = to_bf16(mul_rn(from_bf16(d), from_bf16(sh.tweight[tt * K + k])));
+                mix = add_bf16(mix, weighted);
             }
-            reinterpret_cast<uint32_t*>(p.out + (size_t)li * T * H)[at] = o2;
-            coherent_store64(p.xw + (size_t)(li + 1) * T * H / 2 + at, tagged(x2, epoch));
-            if (li + 1 == p.nlayers && p.x_final != nullptr) reinterpret_cast<uint32_t*>(p.x_final)[at] = x2;
+            // src/decoder_layer.rs:563-575: gated = bf16(shared_down * sigmoid).
+            uint32_t sd = sh.res[(0 * NT + tt) * kRowsPerCTask + gg];
+            uint32_t gated = to_bf16(mul_rn(from_bf16(sd), from_bf16(sh.sig[tt])));
+            uint32_t o = add_bf16(mix, gated);
+            uint32_t xn = add_bf16((rin >> (16 * half)) & 0xffffu, o);
+            o2 |= o << (16 * half);
+            x2 |= xn << (16 * half);
         }
-        if (!__syncthreads_and(ok)) return;
-        FW_TRACE_MARK(slot_trace, 1);
-        publish(cnt + kCntC, (uint32_t)p.n_c, phase_flags(p, li, kCntC), epoch);
-        FW_TRACE_STAMP(t2);
-        FW_TRACE_WRITE(slot_trace, kTaskDown, t0, t1, t2);
+        reinterpret_cast<uint32_t*>(p.out + (size_t)li * T * H)[at] = o2;
+        coherent_store64(p.xw + (size_t)(li + 1) * T * H / 2 + at, tagged(x2, epoch));
+        if (li + 1 == p.nlayers && p.x_final != nullptr) reinterpret_cast<uint32_t*>(p.x_final)[at] = x2;
+    }
+    if (!__syncthreads_and(ok)) return false;
+    FW_TRACE_MARK(slot, 1);
+    publish(p.counters + (size_t)li * kCountersPerLayer + kCntC, (uint32_t)p.n_c, phase_flags(p, li, kCntC), epoch);
+    FW_TRACE_STAMP(t2);
+    FW_TRACE_WRITE(slot, kTaskDown, t0, t1, t2);
+    return true;
+}
+
+// ---- roles -----------------------------------------------------------------------------
+//
+// Per layer the rows role runs the R, S and the first nb_rows B tasks; the
+// combine role runs the remaining B tasks, then the C tasks. Both walk their
+// list in (layer, phase) order, task t on workgroup t mod (role size).
+
+template <int NT, int MBH, int TK>
+__device__ __forceinline__ void rows_role(const DecodeParams* __restrict__ P, uint32_t epoch, DecodeShared<NT>& sh,
+                                          int rank) {
+    const DecodeParams& p = *P;
+    const int per = p.n_router + p.n_shared + p.nb_rows;
+    const int total = p.nlayers * per;
+    LdsState st;
+    for (int t = rank; t < total; t += p.g_rows) {
+        const int li = t / per;
+        const int j = t - li * per;
+        bool ok;
+        if (j < p.n_router) {
+            ok = router_task<NT, MBH>(p, epoch, sh, st, li, j);
+        } else if (j < p.n_router + p.n_shared) {
+            ok = pairs_task<NT, MBH, TK>(p, epoch, sh, st, li, j - p.n_router, true);
+        } else {
+            ok = pairs_task<NT, MBH, TK>(p, epoch, sh, st, li, j - p.n_router - p.n_shared, false);
+        }
+        if (!ok) return;
+    }
+}
+
+template <int NT, int MBH, int MBI, int TK>
+__device__ __forceinline__ void combine_role(const DecodeParams* __restrict__ P, uint32_t epoch, DecodeShared<NT>& sh,
+                                             int rank) {
+    const DecodeParams& p = *P;
+    const int nb_comb = p.n_b - p.nb_rows;
+    const int per = nb_comb + p.n_c;
+    const int total = p.nlayers * per;
+    LdsState st;
+    for (int t = rank; t < total; t += p.g_comb) {
+        const int li = t / per;
+        const int j = t - li * per;
+        const bool ok = j < nb_comb ? pairs_task<NT, MBH, TK>(p, epoch, sh, st, li, p.nb_rows + j, false)
+                                    : combine_task<NT, MBI, TK>(p, epoch, sh, st, li, j - nb_comb);
+        if (!ok) return;
     }
 }
 
@@ -711,7 +823,7 @@ k_moe_decode(const DecodeParams* __restrict__ P, uint32_t epoch) {
     if (b < P->g_rows) {
         rows_role<NT, MBH, TK>(P, epoch, sh, b);
     } else if (b < P->g_rows + P->g_comb) {
-        combine_role<NT, MBI, TK>(P, epoch, sh, b - P->g_rows);
+        combine_role<NT, MBH, MBI, TK>(P, epoch, sh, b - P->g_rows);
     }
     // The last workgroup out zeroes every counter for the next launch.
     __syncthreads();

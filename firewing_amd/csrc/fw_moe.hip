@@ -424,16 +424,18 @@ void launch_decode(firewing_hip_context* c, size_t first, size_t n, int T, int o
     p.n_shared = (int)((Is + kPairsPerTask - 1) / kPairsPerTask);
     p.n_b = (int)(S * (I / kPairsPerTask));
     p.n_c = (int)(H / kRowsPerCTask);
-    p.n_rows = p.n_router + p.n_shared + p.n_b;
     (void)L;
     (void)Tn;
     (void)K;
     // Roles: the combine role gets one workgroup per C task of a layer where
     // the grid allows (so every task's down rows are in flight before the
-    // gate/up phase ends), at most half of the grid.
+    // gate/up phase ends), at most half of the grid. The rows role takes one
+    // B task per workgroup and layer; B tasks beyond that go to the combine
+    // role, ahead of its C tasks, instead of a second round on the rows role.
     const int grid = c->grid[T];
     p.g_comb = std::min(p.n_c, grid / 2);
     p.g_rows = grid - p.g_comb;
+    p.nb_rows = std::min(p.n_b, p.g_rows);
     if (p.g_comb < 1 || p.g_rows < 1) throw HipError{"decode grid too small for its roles"};
     p.trace = c->trace;
     // The kernel reads its parameters from a device copy; upload only on change
