@@ -48,12 +48,13 @@ struct DecodeLayer {
 
 enum DecodeCounter : int {
     kCntRouter = 0,
-    kCntGateUp = 1,  // S and B tasks
-    kCntC = 2,
-    kCountersPerLayer = 3
+    kCntSelect = 1,  // the layer's selection record
+    kCntGateUp = 2,  // S and B tasks
+    kCntC = 3,
+    kCountersPerLayer = 4
 };
 
-enum DecodeTaskKind : int { kTaskRouter = 0, kTaskShared = 1, kTaskGateUp = 3, kTaskDown = 4 };
+enum DecodeTaskKind : int { kTaskRouter = 0, kTaskShared = 1, kTaskSelect = 2, kTaskGateUp = 3, kTaskDown = 4 };
 
 constexpr int kRouterRowsPerTask = 16;
 constexpr int kPairsPerTask = 8;
@@ -84,6 +85,7 @@ struct DecodeParams {
     uint64_t* logits;      // [nlayers][T][ls / 2]
     uint64_t* shared_act;  // [nlayers][T][Is / 2]
     uint64_t* act;         // [nlayers][S][T][I / 2]
+    uint64_t* selrec;      // [nlayers][rec_words] selection records (record_words)
     // plain outputs, read after the launch
     uint16_t* x_final;  // [T][H] residual after the last layer, or null
     uint16_t* out;      // [nlayers][T][H] block outputs
@@ -102,8 +104,11 @@ struct DecodeParams {
 
 // Task timing (wall clock) for profiling builds only (slots: trace_slot).
 #ifdef FW_DECODE_TRACE
-constexpr int kTraceWords = 12;  // start, dependency met, end, wg << 8 | kind, 8 stage marks
-#define FW_TRACE_STAMP(var) const uint64_t var = wall_clock64()
+constexpr int kTraceWords = 14;  // start, dependency met, end, wg << 8 | kind, 8 stage marks, 2 cycle counts
+#define FW_TRACE_STAMP(var)                  \
+    const uint64_t var = wall_clock64();     \
+    const uint64_t var##_cycles = clock64(); \
+    (void)var##_cycles
 #define FW_TRACE_MARK(slot_, k)                                                    \
     do {                                                                           \
         if (threadIdx.x == 0 && p.trace != nullptr && (slot_) >= 0)                \
@@ -117,6 +122,8 @@ constexpr int kTraceWords = 12;  // start, dependency met, end, wg << 8 | kind, 
             tr[1] = (b);                                                           \
             tr[2] = (c);                                                           \
             tr[3] = ((uint64_t)blockIdx.x << 8) | (uint64_t)(kind);                \
+            tr[12] = a##_cycles;                                                   \
+            tr[13] = c##_cycles;                                                   \
         }                                                                          \
     } while (0)
 #else
@@ -137,9 +144,14 @@ static __device__ __constant__ uint64_t c_exp2_table[32] = {
     0x3fef5818dcfba487ULL, 0x3fef7c97337b9b5fULL, 0x3fefa4afa2a490daULL, 0x3fefd0765b6e4540ULL,
 };
 
-template <int NT>
+constexpr int kBatchMatrices = 16;  // C task: matrices per register batch (4 per wave)
+
+template <int NT, int MBI>
 struct DecodeShared {
-    float xs[NT * kMaxHidden];  // rows: block input as f32; combine: exponentials
+    // rows: block input as f32; combine: exponentials, then the activation
+    // vectors of one batch (16 matrices x NT tokens x MBI * 16 words)
+    alignas(16) float xs[NT * kMaxHidden > kBatchMatrices * NT * MBI * 16 ? NT * kMaxHidden
+                                                                           : kBatchMatrices * NT * MBI * 16];
     uint16_t lg[NT * logit_stride(kMaxExperts)];  // logits of the selected layer
     uint64_t exp2tab[32];
     uint16_t res[(kMaxTopK * NT + 1) * NT * kRowsPerCTask];  // down-row dots [matrix][token][row]
@@ -147,12 +159,25 @@ struct DecodeShared {
     int32_t sorted[kMaxTopK * NT];                            // union, ascending id
     uint32_t slot_tokens[kMaxTopK * NT];
     int32_t tslot[NT * kMaxTopK];     // [t][k]: slot of the token's k-th expert in ascending id
+    int32_t pos[NT * kMaxTopK];       // [t][r]: ascending-id position of the token's rank-r expert
     uint16_t tweight[NT * kMaxTopK];  // [t][k]: its bf16 score
     uint16_t sig[NT];
     float inv[NT];
+    int32_t vbase[kBatchMatrices];               // staged batch: first vector of its matrix i
+    uint32_t vsrc[kBatchMatrices * NT];          // staged vector v: word offset of its source
+    uint8_t vshared[kBatchMatrices * NT];        // staged vector v: from shared_act
+    int32_t nvec;
     int32_t nunion;
     int32_t flag;
 };
+
+// Selection record of a layer, tagged words: [0] union size U, then per slot
+// (S = T * K entries) the expert id and the token mask, then per token and
+// ascending-id position k the slot (words [0, 1 + 3S): the slot map, published
+// first), then per token and position the bf16 score and per token the bf16
+// shared-gate sigmoid (the weights, published when computed).
+__host__ __device__ constexpr int record_words(int T, int K) { return 1 + 4 * T * K + T; }
+__host__ __device__ constexpr int record_map_words(int T, int K) { return 1 + 3 * T * K; }
 
 __device__ __forceinline__ uint32_t* phase_flags(const DecodeParams& p, int li, int phase) {
     return p.flags + ((size_t)li * kCountersPerLayer + phase) * kFlagCopies * kFlagStride;
@@ -162,8 +187,8 @@ __device__ __forceinline__ uint32_t* phase_flags(const DecodeParams& p, int li, 
 
 // The residual of layer li ([T][H] bf16) into LDS as f32: the caller's input
 // for the first layer of the launch, else the tagged residual words.
-template <int NT>
-__device__ __forceinline__ bool load_input(const DecodeParams& p, int li, uint32_t epoch, DecodeShared<NT>& sh) {
+template <int NT, class SH>
+__device__ __forceinline__ bool load_input(const DecodeParams& p, int li, uint32_t epoch, SH& sh) {
     const int pairs = p.T * p.H / 2;
     float* xs = sh.xs;
     bool ok = true;
@@ -201,8 +226,8 @@ __device__ __forceinline__ bool load_input(const DecodeParams& p, int li, uint32
 // 1e-6)), mean(r^2) through the reference's dot order (32 chains, tree, +0.0)
 // divided by H; h[H-1] = 1.0 with the bias feature. Wave t normalises token t,
 // in place in LDS.
-template <int NT>
-__device__ __forceinline__ void normalise_input(const DecodeParams& p, DecodeShared<NT>& sh) {
+template <int NT, class SH>
+__device__ __forceinline__ void normalise_input(const DecodeParams& p, SH& sh) {
     if (!p.prenorm) return;
     const int T = p.T, n = p.H;
     float* xs = sh.xs;
@@ -245,8 +270,8 @@ __device__ __forceinline__ void normalise_input(const DecodeParams& p, DecodeSha
 
 // The layer's logits into LDS (after the router tasks): tagged words, T rows
 // of ls bf16.
-template <int NT>
-__device__ __forceinline__ bool load_logits(const DecodeParams& p, int li, uint32_t epoch, DecodeShared<NT>& sh) {
+template <int NT, class SH>
+__device__ __forceinline__ bool load_logits(const DecodeParams& p, int li, uint32_t epoch, SH& sh) {
     constexpr int kWords = (NT * logit_stride(kMaxExperts) / 2 + kThreads - 1) / kThreads;
     const int words = p.T * p.ls / 2;
     const int n = (words - (int)threadIdx.x + kThreads - 1) / kThreads;
@@ -268,8 +293,8 @@ __device__ __forceinline__ bool load_logits(const DecodeParams& p, int li, uint3
 // Requires the logits in LDS. reject_nan: src/decoder_layer.rs:279-281 (the
 // error word is set; the launch then completes and reports it). TK: logits per
 // lane in the top-k (E <= 64 * TK).
-template <int NT, int TK>
-__device__ __forceinline__ void select_experts(const DecodeParams& p, DecodeShared<NT>& sh, bool reject_nan,
+template <int NT, int TK, class SH>
+__device__ __forceinline__ void select_experts(const DecodeParams& p, SH& sh, bool reject_nan,
                                                int slot_trace = -1) {
     (void)slot_trace;
     const int T = p.T, E = p.E, K = p.K, S = p.S, LS = p.ls;
@@ -299,6 +324,7 @@ __device__ __forceinline__ void select_experts(const DecodeParams& p, DecodeShar
             sh.sorted[rank] = id;
             sh.slot_tokens[rank] = 1u;
             sh.tslot[rank] = rank;
+            sh.pos[lane] = rank;
         }
         for (int s2 = K + lane; s2 < S; s2 += kWave) sh.slot_tokens[s2] = 0u;
         if (lane == 0) sh.nunion = K;
@@ -351,6 +377,7 @@ __device__ __forceinline__ void select_experts(const DecodeParams& p, DecodeShar
                     sh.slot_tokens[slot[h]] = mask[h];
                 }
                 sh.tslot[tok[h] * K + rank_in_token[h]] = slot[h];
+                sh.pos[lane + kWave * h] = rank_in_token[h];
             }
         }
         for (int s2 = nunion + lane; s2 < S; s2 += kWave) sh.slot_tokens[s2] = 0u;
@@ -365,8 +392,8 @@ __device__ __forceinline__ void select_experts(const DecodeParams& p, DecodeShar
 // index order, renormalised over the selection), as tweight[t][k] in the
 // token's ascending-id order, and the shared-gate sigmoid. With host_outputs
 // also the rank-order ids and scores and the sigmoid for the caller.
-template <int NT>
-__device__ __forceinline__ void score_experts(const DecodeParams& p, int li, DecodeShared<NT>& sh, bool host_outputs) {
+template <int NT, class SH>
+__device__ __forceinline__ void score_experts(const DecodeParams& p, int li, SH& sh, bool host_outputs) {
     const int T = p.T, E = p.E, K = p.K, LS = p.ls;
     const int lane = lane_id(), w = wave_id();
     if (w < T) {
@@ -380,30 +407,44 @@ __device__ __forceinline__ void score_experts(const DecodeParams& p, int li, Dec
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
         __builtin_amdgcn_wave_barrier();
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+        // one sequential sum in index order (lane 0, reading four values at a
+        // time when the token's row is 16-byte aligned)
+        float den = -0.0f;
         if (lane == 0) {
-            float den = -0.0f;
             int e = 0;
-            for (; e + 32 <= E; e += 32) {
-                float v[32];
+            if (((E | (w * E)) & 3) == 0) {
+                const float4* e4 = reinterpret_cast<const float4*>(ew);
+                for (; e + 32 <= E; e += 32) {
+                    float4 v[8];
 #pragma unroll
-                for (int i = 0; i < 32; ++i) v[i] = ew[e + i];
+                    for (int i = 0; i < 8; ++i) v[i] = e4[e / 4 + i];
 #pragma unroll
-                for (int i = 0; i < 32; ++i) den = add_rn(den, v[i]);
-            }
-            for (; e < E; ++e) den = add_rn(den, ew[e]);
-            const int32_t* ids = sh.ids + w * kMaxTopK;
-            float sel = -0.0f;
-            for (int r = 0; r < K; ++r) sel = add_rn(sel, ew[ids[r]] / den);
-            for (int r = 0; r < K; ++r) {
-                const uint16_t score = to_bf16((ew[ids[r]] / den) / sel);
-                int k = 0;
-                for (int r2 = 0; r2 < K; ++r2) k += (ids[r2] < ids[r]) ? 1 : 0;
-                sh.tweight[w * K + k] = score;
-                if (host_outputs) {
-                    p.ids[((size_t)li * T + w) * K + r] = ids[r];
-                    p.scores[((size_t)li * T + w) * K + r] = score;
+                    for (int i = 0; i < 8; ++i) {
+                        den = add_rn(den, v[i].x);
+                        den = add_rn(den, v[i].y);
+                        den = add_rn(den, v[i].z);
+                        den = add_rn(den, v[i].w);
+                    }
                 }
             }
+            for (; e < E; ++e) den = add_rn(den, ew[e]);
+        }
+        den = __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, den)));
+        // lane r: the rank-r expert's probability; their sum in rank order
+        const int32_t* ids = sh.ids + w * kMaxTopK;
+        const float pr = lane < K ? ew[ids[lane]] / den : 0.0f;
+        float sel = -0.0f;
+        for (int r = 0; r < K; ++r)
+            sel = add_rn(sel, __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, pr), r)));
+        if (lane < K) {
+            const uint16_t score = to_bf16(pr / sel);
+            sh.tweight[w * K + sh.pos[w * K + lane]] = score;
+            if (host_outputs) {
+                p.ids[((size_t)li * T + w) * K + lane] = ids[lane];
+                p.scores[((size_t)li * T + w) * K + lane] = score;
+            }
+        }
+        if (lane == 0) {
             const uint16_t sg = sigmoid_bf16(lt[p.gi], sh.exp2tab);
             sh.sig[w] = sg;
             if (host_outputs) p.sig[(size_t)li * T + w] = sg;
@@ -425,17 +466,18 @@ __device__ __forceinline__ void score_experts(const DecodeParams& p, int li, Dec
 // What this workgroup's LDS holds: the layer whose raw input / normalised
 // input / selection / scores are there (-1: none).
 struct LdsState {
-    int loaded = -1, staged = -1, selected = -1, scored = -1;
+    int loaded = -1, staged = -1, selected = -1, scored = -1;  // scored: route weights and sigmoid
 };
 
-// Trace slot of a task: layer * (R + S + B + C tasks) + its index in that order.
+// Trace slot of a task: layer * (R + S + B + C tasks + 1) + its index in that
+// order, the selection task last.
 __device__ __forceinline__ int trace_slot(const DecodeParams& p, int li, int index) {
-    return li * (p.n_router + p.n_shared + p.n_b + p.n_c) + index;
+    return li * (p.n_router + p.n_shared + p.n_b + p.n_c + 1) + index;
 }
 
 // Block input of layer li in LDS, normalised.
-template <int NT>
-__device__ __forceinline__ bool stage_layer_input(const DecodeParams& p, uint32_t epoch, DecodeShared<NT>& sh,
+template <int NT, class SH>
+__device__ __forceinline__ bool stage_layer_input(const DecodeParams& p, uint32_t epoch, SH& sh,
                                                   LdsState& st, int li) {
     if (st.staged == li) return true;
     if (st.loaded != li) {
@@ -448,8 +490,8 @@ __device__ __forceinline__ bool stage_layer_input(const DecodeParams& p, uint32_
 }
 
 // Selection of layer li in LDS (waits for its router tasks).
-template <int NT, int TK>
-__device__ __forceinline__ bool select_layer(const DecodeParams& p, uint32_t epoch, DecodeShared<NT>& sh, LdsState& st,
+template <int NT, int TK, class SH>
+__device__ __forceinline__ bool select_layer(const DecodeParams& p, uint32_t epoch, SH& sh, LdsState& st,
                                              int li, bool reject_nan, int slot) {
     if (st.selected == li) return true;
     if (!wait_phase(phase_flags(p, li, kCntRouter), epoch, p.error, p.limit_ticks, &sh.flag)) return false;
@@ -462,8 +504,8 @@ __device__ __forceinline__ bool select_layer(const DecodeParams& p, uint32_t epo
 }
 
 // R task j of layer li: 16 router rows, or the shared_expert_gate row.
-template <int NT, int MBH>
-__device__ __forceinline__ bool router_task(const DecodeParams& p, uint32_t epoch, DecodeShared<NT>& sh, LdsState& st,
+template <int NT, int MBH, class SH>
+__device__ __forceinline__ bool router_task(const DecodeParams& p, uint32_t epoch, SH& sh, LdsState& st,
                                             int li, int j) {
     FW_TRACE_STAMP(t0);
     const int slot = trace_slot(p, li, j);
@@ -523,8 +565,8 @@ __device__ __forceinline__ bool router_task(const DecodeParams& p, uint32_t epoc
 
 // S task (shared = true, index js < n_shared) or B task (index js < n_b) of
 // layer li: 8 gate/up pairs with fused SwiGLU.
-template <int NT, int MBH, int TK>
-__device__ __forceinline__ bool pairs_task(const DecodeParams& p, uint32_t epoch, DecodeShared<NT>& sh, LdsState& st,
+template <int NT, int MBH, int TK, class SH>
+__device__ __forceinline__ bool pairs_task(const DecodeParams& p, uint32_t epoch, SH& sh, LdsState& st,
                                            int li, int js, bool shared) {
     FW_TRACE_STAMP(t0);
     const int slot = trace_slot(p, li, p.n_router + (shared ? js : p.n_shared + js));
@@ -592,58 +634,244 @@ __device__ __forceinline__ bool pairs_task(const DecodeParams& p, uint32_t epoch
         }
         FW_TRACE_MARK(slot, 1);
     }
-    publish(p.counters + (size_t)li * kCountersPerLayer + kCntGateUp, (uint32_t)(p.n_shared + p.n_b),
+    publish(p.counters + (size_t)li * kCountersPerLayer + kCntGateUp, (uint32_t)(p.n_shared + p.n_b + 1),
             phase_flags(p, li, kCntGateUp), epoch);
     FW_TRACE_STAMP(t2);
     FW_TRACE_WRITE(slot, shared ? kTaskShared : kTaskGateUp, t0, t1, t2);
     return true;
 }
 
-// One down row against its activation words (tagged): the chains of
-// src/expert.rs:514-552 over K = nblocks * 32 (so the tail sum is +0.0), for
-// each token in mask (wave-uniform). This lane's chain pair of block b is
-// activation pair 16 b + line_column(q) / 2. Returns false on timeout or
+// Z task of layer li: the layer's selection, scores and shared-gate sigmoid,
+// computed once (with the caller's ids, scores and sigmoid) and published as
+// the layer's selection record for the C tasks.
+template <int NT, int TK, class SH>
+__device__ __forceinline__ bool select_task(const DecodeParams& p, uint32_t epoch, SH& sh, LdsState& st,
+                                            int li) {
+    FW_TRACE_STAMP(t0);
+    const int slot = trace_slot(p, li, p.n_router + p.n_shared + p.n_b + p.n_c);
+    (void)slot;
+    if (!select_layer<NT, TK>(p, epoch, sh, st, li, p.order == 0, slot)) return false;
+    FW_TRACE_STAMP(t1);
+    const int T = p.T, K = p.K, S = T * K;
+    const int words = record_words(T, K), map_words = record_map_words(T, K);
+    uint64_t* rec = p.selrec + (size_t)li * words;
+    for (int i = threadIdx.x; i < map_words; i += kThreads) {
+        uint32_t v;
+        if (i == 0) {
+            v = (uint32_t)sh.nunion;
+        } else if (i < 1 + S) {
+            v = (uint32_t)sh.sorted[i - 1];
+        } else if (i < 1 + 2 * S) {
+            v = sh.slot_tokens[i - 1 - S];
+        } else {
+            v = (uint32_t)sh.tslot[i - 1 - 2 * S];
+        }
+        coherent_store64(rec + i, tagged(v, epoch));
+    }
+    publish(p.counters + (size_t)li * kCountersPerLayer + kCntSelect, 1u, phase_flags(p, li, kCntSelect), epoch);
+    FW_TRACE_MARK(slot, 0);
+    // the exponentials overwrite the staged input
+    score_experts<NT>(p, li, sh, true);
+    st.loaded = st.staged = -1;
+    st.scored = li;
+    for (int i = map_words + threadIdx.x; i < words; i += kThreads) {
+        const uint32_t v = i < 1 + 4 * S ? sh.tweight[i - 1 - 3 * S] : sh.sig[i - 1 - 4 * S];
+        coherent_store64(rec + i, tagged(v, epoch));
+    }
+    FW_TRACE_MARK(slot, 1);
+    // the weights complete with the gate/up phase
+    publish(p.counters + (size_t)li * kCountersPerLayer + kCntGateUp, (uint32_t)(p.n_shared + p.n_b + 1),
+            phase_flags(p, li, kCntGateUp), epoch);
+    FW_TRACE_STAMP(t2);
+    FW_TRACE_WRITE(slot, kTaskSelect, t0, t1, t2);
+    return true;
+}
+
+// Words [first, last) of the selection record of layer li into LDS.
+template <int NT, class SH>
+__device__ __forceinline__ bool load_record(const DecodeParams& p, int li, uint32_t epoch, SH& sh,
+                                            int first, int last) {
+    constexpr int kWords = (record_words(NT, kMaxTopK) + kThreads - 1) / kThreads;
+    const int T = p.T, K = p.K, S = T * K;
+    const int tid = threadIdx.x;
+    const int n = (last - first - tid + kThreads - 1) / kThreads;
+    uint64_t v[kWords];
+    const bool ok = load_tagged<kWords, kThreads>(v, p.selrec + (size_t)li * record_words(T, K) + first + tid, n,
+                                                  epoch, p.error, p.limit_ticks);
+#pragma unroll
+    for (int k = 0; k < kWords; ++k) {
+        if (k < n) {
+            const int i = first + tid + k * kThreads;
+            const uint32_t x = (uint32_t)v[k];
+            if (i == 0) {
+                sh.nunion = (int32_t)x;
+            } else if (i < 1 + S) {
+                sh.sorted[i - 1] = (int32_t)x;
+            } else if (i < 1 + 2 * S) {
+                sh.slot_tokens[i - 1 - S] = x;
+            } else if (i < 1 + 3 * S) {
+                sh.tslot[i - 1 - 2 * S] = (int32_t)x;
+            } else if (i < 1 + 4 * S) {
+                sh.tweight[i - 1 - 3 * S] = (uint16_t)x;
+            } else {
+                sh.sig[i - 1 - 4 * S] = (uint16_t)x;
+            }
+        }
+    }
+    return __syncthreads_and(ok) != 0;
+}
+
+// Stages into LDS the activation vectors of matrices [mb, me] of layer li (m
+// = 0 shared, 1 + s slot s): one vector per token in the matrix's mask, the
+// batch's i-th matrix from vector sh.vbase[i], vector v at sh.xs + v * stride
+// words (stride = max(I, Is) / 2 <= MBI * 16). Returns false on timeout or
 // error.
-template <int NT, int MAXB>
-__device__ __forceinline__ bool down_row(const LineShare<MAXB>& r, int nblocks, const uint64_t* actw, int words_per_token,
-                                         int q, uint32_t mask, uint32_t epoch, const DecodeParams& p,
-                                         uint32_t (&bits)[NT]) {
-    const int col2 = line_column(q) / 2;
-    bool ok = true;
-#pragma unroll
-    for (int t = 0; t < NT; ++t) {
-        bits[t] = 0u;
-        if (!(mask & (1u << t))) continue;
-        const int nb = opaque(nblocks);
-        uint64_t xv[MAXB];
-        ok = load_tagged<MAXB, 16>(xv, actw + (size_t)t * words_per_token + col2, nb, epoch, p.error, p.limit_ticks) && ok;
-        float c0 = 0.0f, c1 = 0.0f;
-#pragma unroll
-        for (int v = 0; v < (MAXB + 1) / 2; ++v) {
-            uint32_t first, second;
-            line_pairs(r.w[v], q, first, second);
-#pragma unroll
-            for (int half = 0; half < 2; ++half) {
-                const int u = 2 * v + half;
-                if (u < MAXB && u < nb) {
-                    const uint32_t wv = half ? second : first;
-                    const uint32_t a = (uint32_t)xv[u];
-                    c0 = add_rn(c0, mul_rn(bf16_lo(wv), bf16_lo(a)));
-                    c1 = add_rn(c1, mul_rn(bf16_hi(wv), bf16_hi(a)));
+template <int NT, int MBI, class SH>
+__device__ __forceinline__ bool stage_acts(const DecodeParams& p, int li, uint32_t epoch, SH& sh, int mb, int me,
+                                           int slot = -1) {
+    (void)slot;
+    constexpr int kChunks = (MBI * 16 + kThreads - 1) / kThreads;  // words of one vector per thread
+    constexpr int kRound = 12 / kChunks;                           // vectors per round
+    const int T = p.T, I = p.I, Is = p.Is;
+    const int stride = max(I, Is) / 2;
+    const int tid = threadIdx.x;
+    if (T == 1) {
+        // one token: vector i is matrix mb + i (every mask holds the token)
+        if (tid <= me - mb) {
+            const int m = mb + tid;
+            sh.vbase[tid] = tid;
+            sh.vshared[tid] = m == 0;
+            sh.vsrc[tid] = m == 0 ? (uint32_t)((size_t)li * (Is / 2)) : (uint32_t)(((size_t)li * p.S + m - 1) * (I / 2));
+        }
+        if (tid == 0) sh.nvec = me - mb + 1;
+    } else if (tid == 0) {
+        int n = 0;
+        for (int m = mb; m <= me; ++m) {
+            sh.vbase[m - mb] = n;
+            const uint32_t mask = m == 0 ? (1u << T) - 1u : sh.slot_tokens[m - 1];
+            for (int t = 0; t < T; ++t) {
+                if (mask & (1u << t)) {
+                    sh.vshared[n] = m == 0;
+                    sh.vsrc[n] = m == 0 ? (uint32_t)(((size_t)li * T + t) * (Is / 2))
+                                        : (uint32_t)((((size_t)li * p.S + m - 1) * T + t) * (I / 2));
+                    ++n;
                 }
             }
         }
-        bits[t] = to_bf16(add_rn(tree32_reduce_lines(c0, c1), 0.0f));
+        sh.nvec = n;
     }
-    return ok;
+    __syncthreads();
+    if (mb == 0) FW_TRACE_MARK(slot, 7);
+    const int nvec = uniform(sh.nvec);
+    uint32_t* dst = reinterpret_cast<uint32_t*>(sh.xs);
+    bool ok = true;
+    for (int v0 = 0; v0 < nvec; v0 += kRound) {
+        uint64_t x[kRound][kChunks];
+#pragma unroll
+        for (int r = 0; r < kRound; ++r) {
+            if (v0 + r < nvec) {
+                // one token: the source follows from the matrix index in scalar registers
+                const int m1 = mb + v0 + r;
+                const bool vs = T == 1 ? m1 == 0 : uniform(sh.vshared[v0 + r]) != 0;
+                const uint64_t* src =
+                    T == 1 ? (m1 == 0 ? p.shared_act + (size_t)li * (Is / 2) : p.act + ((size_t)li * p.S + m1 - 1) * (I / 2))
+                           : (vs ? p.shared_act : p.act) + (uint32_t)uniform((int)sh.vsrc[v0 + r]);
+                const int len = vs ? Is / 2 : I / 2;
+#pragma unroll
+                for (int c = 0; c < kChunks; ++c) {
+                    const int wd = tid + c * kThreads;
+                    if (wd < len)
+                        x[r][c] = __hip_atomic_load(as_global(src + wd), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+                }
+            }
+        }
+        // words not yet carrying the epoch (stale cached lines, stores in
+        // flight) are read again past the caches, all of them per pass
+        uint64_t start = 0;
+        for (int pass = 0;; ++pass) {
+            bool all = true;
+#ifdef FW_DECODE_TRACE
+            if (pass == 0) {
+                int stale = 0;
+                for (int r = 0; r < kRound; ++r)
+                    for (int c = 0; c < kChunks; ++c)
+                        stale += (v0 + r < nvec && tid + c * kThreads < I / 2 && !has_tag(x[r][c], epoch)) ? 1 : 0;
+                const int total = __syncthreads_count(stale);
+                if (tid == 0 && p.trace != nullptr && slot >= 0) p.trace[(size_t)slot * kTraceWords + 4 + 6] = total;
+            }
+#endif
+#pragma unroll
+            for (int r = 0; r < kRound; ++r) {
+                if (v0 + r < nvec) {
+#pragma unroll
+                    for (int c = 0; c < kChunks; ++c) {
+                        const int wd = tid + c * kThreads;
+                        const bool vs = sh.vshared[v0 + r] != 0;
+                        if (wd < (vs ? Is / 2 : I / 2) && !has_tag(x[r][c], epoch)) {
+                            all = false;
+                            x[r][c] = coherent_load64((vs ? p.shared_act : p.act) + sh.vsrc[v0 + r] + wd);
+                        }
+                    }
+                }
+            }
+            if (all) break;
+            if (pass == 0) start = wall_clock64();
+            if (coherent_load(p.error) != 0 || wall_clock64() - start > p.limit_ticks) {
+                int32_t expected = 0;
+                __hip_atomic_compare_exchange_strong(p.error, &expected, 1, __ATOMIC_RELAXED, __ATOMIC_RELAXED,
+                                                     __HIP_MEMORY_SCOPE_AGENT);
+                ok = false;
+                break;
+            }
+        }
+#pragma unroll
+        for (int r = 0; r < kRound; ++r) {
+            if (v0 + r < nvec) {
+                const int len = (T == 1 ? mb + v0 + r == 0 : sh.vshared[v0 + r] != 0) ? Is / 2 : I / 2;
+#pragma unroll
+                for (int c = 0; c < kChunks; ++c) {
+                    const int wd = tid + c * kThreads;
+                    if (wd < len) dst[(v0 + r) * stride + wd] = (uint32_t)x[r][c];
+                }
+            }
+        }
+    }
+    return __syncthreads_and(ok) != 0;
+}
+
+// One down row against an activation vector staged in LDS (av: its first
+// word): the chains of src/expert.rs:514-552 over K = nblocks * 32 (so the
+// tail sum is +0.0). This lane's chain pair of block b is activation pair
+// 16 b + line_column(q) / 2.
+template <int MAXB>
+__device__ __forceinline__ uint32_t down_row_lds(const LineShare<MAXB>& r, int nblocks, const uint32_t* av, int q) {
+    const uint32_t* a0 = av + line_column(q) / 2;
+    const int nb = opaque(nblocks);
+    float c0 = 0.0f, c1 = 0.0f;
+#pragma unroll
+    for (int v = 0; v < (MAXB + 1) / 2; ++v) {
+        uint32_t first, second;
+        line_pairs(r.w[v], q, first, second);
+#pragma unroll
+        for (int half = 0; half < 2; ++half) {
+            const int u = 2 * v + half;
+            if (u < MAXB && u < nb) {
+                const uint32_t wv = half ? second : first;
+                const uint32_t a = a0[16 * u];
+                c0 = add_rn(c0, mul_rn(bf16_lo(wv), bf16_lo(a)));
+                c1 = add_rn(c1, mul_rn(bf16_hi(wv), bf16_hi(a)));
+            }
+        }
+    }
+    return to_bf16(add_rn(tree32_reduce_lines(c0, c1), 0.0f));
 }
 
 // C task j of layer li: hidden rows 4j .. 4j + 3. Matrix m of the task: m = 0
 // is the shared expert's down projection, m = 1 + s the down projection of
 // slot s. Wave w covers the 4 rows (16 lanes each) of matrices w, w + 4,
 // w + 8, w + 12 in its first batch, then the next 16 matrices, and so on.
-template <int NT, int MBI, int TK>
-__device__ __forceinline__ bool combine_task(const DecodeParams& p, uint32_t epoch, DecodeShared<NT>& sh, LdsState& st,
+template <int NT, int MBI, int TK, class SH>
+__device__ __forceinline__ bool combine_task(const DecodeParams& p, uint32_t epoch, SH& sh, LdsState& st,
                                              int li, int j) {
     FW_TRACE_STAMP(t0);
     const int slot = trace_slot(p, li, p.n_router + p.n_shared + p.n_b + j);
@@ -657,7 +885,12 @@ __device__ __forceinline__ bool combine_task(const DecodeParams& p, uint32_t epo
     LineShare<MBI> rs0, rs1, rs2, rs3;
     // the shared expert's rows need no selection: issue them first
     if (w == 0) line_issue(rs0, L.shared_down + (size_t)row * Is, Is / 32, q);
-    if (!select_layer<NT, TK>(p, epoch, sh, st, li, j == 0 && p.order == 0, -1)) return false;
+    if (st.selected != li) {
+        if (!wait_phase(phase_flags(p, li, kCntSelect), epoch, p.error, p.limit_ticks, &sh.flag)) return false;
+        if (!load_record<NT>(p, li, epoch, sh, 0, record_map_words(T, K))) return false;
+        st.selected = li;
+    }
+    FW_TRACE_MARK(slot, 2);
     const int U = uniform(sh.nunion);
 #define FW_ISSUE_DOWN(RS, M)                                                                  \
     do {                                                                                      \
@@ -673,15 +906,15 @@ __device__ __forceinline__ bool combine_task(const DecodeParams& p, uint32_t epo
     do {                                                                                                  \
         const int m_ = (M);                                                                               \
         if (m_ <= U) {                                                                                    \
-            const bool shared_ = m_ == 0;                                                                 \
-            const int kd_ = shared_ ? Is : I;                                                             \
-            const uint32_t mask_ = shared_ ? all_tokens : (uint32_t)uniform((int)sh.slot_tokens[m_ - 1]); \
-            const uint64_t* actw_ = shared_ ? p.shared_act + (size_t)li * T * (Is / 2)                    \
-                                            : p.act + ((size_t)li * p.S + m_ - 1) * (size_t)T * (I / 2);  \
-            uint32_t bits_[NT];                                                                           \
-            ok = down_row<NT, MBI>(RS, kd_ / 32, actw_, kd_ / 2, q, mask_, epoch, p, bits_) && ok;         \
+            const int kd_ = m_ == 0 ? Is : I;                                                             \
+            const uint32_t mask_ = m_ == 0 ? all_tokens : (uint32_t)uniform((int)sh.slot_tokens[m_ - 1]); \
+            int v_ = uniform(sh.vbase[m_ - mb]);                                                          \
             _Pragma("unroll") for (int t_ = 0; t_ < NT; ++t_) {                                           \
-                if (q == 0 && (mask_ & (1u << t_))) sh.res[(m_ * NT + t_) * kRowsPerCTask + g] = bits_[t_]; \
+                if (mask_ & (1u << t_)) {                                                                 \
+                    const uint32_t bits_ = down_row_lds<MBI>(RS, kd_ / 32, act_lds + v_ * act_stride, q);  \
+                    if (q == 0) sh.res[(m_ * NT + t_) * kRowsPerCTask + g] = bits_;                       \
+                    ++v_;                                                                                 \
+                }                                                                                         \
             }                                                                                             \
         }                                                                                                 \
     } while (0)
@@ -690,12 +923,12 @@ __device__ __forceinline__ bool combine_task(const DecodeParams& p, uint32_t epo
     FW_ISSUE_DOWN(rs2, w + 8);
     FW_ISSUE_DOWN(rs3, w + 12);
     // The residual words this task updates (ready since the router ran), read
-    // while the gate/up phase runs: one thread per token and pair of rows.
+    // while the gate/up phase runs: one thread per token and row.
     const int tid = threadIdx.x;
-    const bool mixer = tid < T * kRowsPerCTask / 2;
-    const int mt = tid / (kRowsPerCTask / 2);
-    const int g0 = 2 * (tid % (kRowsPerCTask / 2));
-    const size_t at = ((size_t)mt * H + r0 + g0) / 2;
+    const bool mixer = tid < T * kRowsPerCTask;
+    const int mt = tid / kRowsPerCTask;
+    const int mg = tid % kRowsPerCTask;
+    const size_t at = ((size_t)mt * H + r0 + (mg & ~1)) / 2;
     bool ok = true;
     uint32_t rin = 0;
     if (mixer) {
@@ -707,55 +940,73 @@ __device__ __forceinline__ bool combine_task(const DecodeParams& p, uint32_t epo
             rin = (uint32_t)v[0];
         }
     }
-    if (st.scored != li) {
-        // route weights are needed only after the gate/up phase; the
-        // exponentials overwrite the staged input
-        score_experts<NT>(p, li, sh, j == 0);
-        st.scored = li;
-        st.loaded = st.staged = -1;
-    }
+    FW_TRACE_MARK(slot, 3);
     if (!wait_phase(phase_flags(p, li, kCntGateUp), epoch, p.error, p.limit_ticks, &sh.flag)) return false;
     FW_TRACE_STAMP(t1);
-    for (int m0 = w; m0 <= U; m0 += 16) {
-        if (m0 != w) {
-            FW_ISSUE_DOWN(rs0, m0);
-            FW_ISSUE_DOWN(rs1, m0 + 4);
-            FW_ISSUE_DOWN(rs2, m0 + 8);
-            FW_ISSUE_DOWN(rs3, m0 + 12);
+    if (st.scored != li) {
+        if (!load_record<NT>(p, li, epoch, sh, record_map_words(T, K), record_words(T, K))) return false;
+        st.scored = li;
+    }
+    FW_TRACE_MARK(slot, 5);
+    // Batches of 16 matrices (4 per wave): the batch's activation vectors
+    // are staged in LDS once for all waves, then each wave runs its rows.
+    const uint32_t* act_lds = reinterpret_cast<const uint32_t*>(sh.xs);
+    const int act_stride = max(I, Is) / 2;
+    st.loaded = st.staged = -1;
+    for (int mb = 0; mb <= U; mb += kBatchMatrices) {
+        if (mb > 0) {
+            FW_ISSUE_DOWN(rs0, mb + w);
+            FW_ISSUE_DOWN(rs1, mb + w + 4);
+            FW_ISSUE_DOWN(rs2, mb + w + 8);
+            FW_ISSUE_DOWN(rs3, mb + w + 12);
         }
-        FW_DOWN_DOT(rs0, m0);
-        FW_DOWN_DOT(rs1, m0 + 4);
-        FW_DOWN_DOT(rs2, m0 + 8);
-        FW_DOWN_DOT(rs3, m0 + 12);
+        if (!stage_acts<NT, MBI>(p, li, epoch, sh, mb, min(U, mb + kBatchMatrices - 1), slot)) return false;
+        FW_TRACE_MARK(slot, 4);
+        FW_DOWN_DOT(rs0, mb + w);
+        FW_DOWN_DOT(rs1, mb + w + 4);
+        FW_DOWN_DOT(rs2, mb + w + 8);
+        FW_DOWN_DOT(rs3, mb + w + 12);
+        // the next batch's staging overwrites these vectors
+        __syncthreads();
     }
 #undef FW_DOWN_DOT
 #undef FW_ISSUE_DOWN
     FW_TRACE_MARK(slot, 0);
     if (!__syncthreads_and(ok)) return false;
     if (mixer) {
-        const int tt = mt;
-        uint32_t o2 = 0, x2 = 0;
-        for (int half = 0; half < 2; ++half) {
-            const int gg = g0 + half;
-            // src/decoder_layer.rs:528-545: weighted = bf16(down * score), summed in
-            // ascending expert order from bf16 zero, rounding after each add.
-            uint32_t mix = to_bf16(0.0f);
-            for (int k = 0; k < K; ++k) {
-                uint32_t d = sh.res[((1 + sh.tslot[tt * K + k]) * NT + tt) * kRowsPerCTask + gg];
-                uint32_t weighted = to_bf16(mul_rn(from_bf16(d), from_bf16(sh.tweight[tt * K + k])));
-                mix = add_bf16(mix, weighted);
+        const int tt = mt, gg = mg;
+        // src/decoder_layer.rs:528-545: weighted = bf16(down * score), summed in
+        // ascending expert order from bf16 zero, rounding after each add (the
+        // operands of eight steps are read ahead of the chain).
+        uint32_t mix = to_bf16(0.0f);
+        for (int k0 = 0; k0 < K; k0 += 8) {
+            uint32_t d[8], wt[8];
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                if (k0 + i < K) {
+                    d[i] = sh.res[((1 + sh.tslot[tt * K + k0 + i]) * NT + tt) * kRowsPerCTask + gg];
+                    wt[i] = sh.tweight[tt * K + k0 + i];
+                }
             }
-            // src/decoder_layer.rs:563-575: gated = bf16(shared_down * sigmoid).
-            uint32_t sd = sh.res[(0 * NT + tt) * kRowsPerCTask + gg];
-            uint32_t gated = to_bf16(mul_rn(from_bf16(sd), from_bf16(sh.sig[tt])));
-            uint32_t o = add_bf16(mix, gated);
-            uint32_t xn = add_bf16((rin >> (16 * half)) & 0xffffu, o);
-            o2 |= o << (16 * half);
-            x2 |= xn << (16 * half);
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                if (k0 + i < K) mix = add_bf16(mix, to_bf16(mul_rn(from_bf16(d[i]), from_bf16(wt[i]))));
+            }
         }
-        reinterpret_cast<uint32_t*>(p.out + (size_t)li * T * H)[at] = o2;
-        coherent_store64(p.xw + (size_t)(li + 1) * T * H / 2 + at, tagged(x2, epoch));
-        if (li + 1 == p.nlayers && p.x_final != nullptr) reinterpret_cast<uint32_t*>(p.x_final)[at] = x2;
+        // src/decoder_layer.rs:563-575: gated = bf16(shared_down * sigmoid).
+        const uint32_t sd = sh.res[(0 * NT + tt) * kRowsPerCTask + gg];
+        const uint32_t gated = to_bf16(mul_rn(from_bf16(sd), from_bf16(sh.sig[tt])));
+        const uint32_t o = add_bf16(mix, gated);
+        const uint32_t xn = add_bf16((rin >> (16 * (gg & 1))) & 0xffffu, o);
+        // rows 2i and 2i + 1 share a word: the even thread stores both
+        const uint32_t o_odd = (uint32_t)__shfl_xor((int)o, 1, kWave);
+        const uint32_t x_odd = (uint32_t)__shfl_xor((int)xn, 1, kWave);
+        if ((gg & 1) == 0) {
+            const uint32_t o2 = o | (o_odd << 16), x2 = xn | (x_odd << 16);
+            reinterpret_cast<uint32_t*>(p.out + (size_t)li * T * H)[at] = o2;
+            coherent_store64(p.xw + (size_t)(li + 1) * T * H / 2 + at, tagged(x2, epoch));
+            if (li + 1 == p.nlayers && p.x_final != nullptr) reinterpret_cast<uint32_t*>(p.x_final)[at] = x2;
+        }
     }
     if (!__syncthreads_and(ok)) return false;
     FW_TRACE_MARK(slot, 1);
@@ -768,11 +1019,12 @@ __device__ __forceinline__ bool combine_task(const DecodeParams& p, uint32_t epo
 // ---- roles -----------------------------------------------------------------------------
 //
 // Per layer the rows role runs the R, S and the first nb_rows B tasks; the
-// combine role runs the remaining B tasks, then the C tasks. Both walk their
-// list in (layer, phase) order, task t on workgroup t mod (role size).
+// combine role runs the Z task, the remaining B tasks, then the C tasks. Both
+// walk their list in (layer, phase) order, task t on workgroup t mod (role
+// size).
 
-template <int NT, int MBH, int TK>
-__device__ __forceinline__ void rows_role(const DecodeParams* __restrict__ P, uint32_t epoch, DecodeShared<NT>& sh,
+template <int NT, int MBH, int TK, class SH>
+__device__ __forceinline__ void rows_role(const DecodeParams* __restrict__ P, uint32_t epoch, SH& sh,
                                           int rank) {
     const DecodeParams& p = *P;
     const int per = p.n_router + p.n_shared + p.nb_rows;
@@ -793,19 +1045,25 @@ __device__ __forceinline__ void rows_role(const DecodeParams* __restrict__ P, ui
     }
 }
 
-template <int NT, int MBH, int MBI, int TK>
-__device__ __forceinline__ void combine_role(const DecodeParams* __restrict__ P, uint32_t epoch, DecodeShared<NT>& sh,
+template <int NT, int MBH, int MBI, int TK, class SH>
+__device__ __forceinline__ void combine_role(const DecodeParams* __restrict__ P, uint32_t epoch, SH& sh,
                                              int rank) {
     const DecodeParams& p = *P;
     const int nb_comb = p.n_b - p.nb_rows;
-    const int per = nb_comb + p.n_c;
+    const int per = 1 + nb_comb + p.n_c;
     const int total = p.nlayers * per;
     LdsState st;
     for (int t = rank; t < total; t += p.g_comb) {
         const int li = t / per;
         const int j = t - li * per;
-        const bool ok = j < nb_comb ? pairs_task<NT, MBH, TK>(p, epoch, sh, st, li, p.nb_rows + j, false)
-                                    : combine_task<NT, MBI, TK>(p, epoch, sh, st, li, j - nb_comb);
+        bool ok;
+        if (j == 0) {
+            ok = select_task<NT, TK>(p, epoch, sh, st, li);
+        } else if (j <= nb_comb) {
+            ok = pairs_task<NT, MBH, TK>(p, epoch, sh, st, li, p.nb_rows + j - 1, false);
+        } else {
+            ok = combine_task<NT, MBI, TK>(p, epoch, sh, st, li, j - 1 - nb_comb);
+        }
         if (!ok) return;
     }
 }
@@ -815,7 +1073,7 @@ __device__ __forceinline__ void combine_role(const DecodeParams* __restrict__ P,
 template <int NT, int MBH, int MBI, int TK>
 __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4)))
 k_moe_decode(const DecodeParams* __restrict__ P, uint32_t epoch) {
-    __shared__ DecodeShared<NT> sh;
+    __shared__ DecodeShared<NT, MBI> sh;
     if (threadIdx.x < 32) sh.exp2tab[threadIdx.x] = c_exp2_table[threadIdx.x];
     __syncthreads();
     const int b = (int)blockIdx.x;

@@ -309,7 +309,7 @@ struct firewing_hip_context {
     uint16_t* xfinal = nullptr;  // [T][H] residual after the last layer
     uint16_t *out = nullptr, *scores = nullptr, *sig = nullptr;
     int32_t* ids = nullptr;
-    uint64_t *xw = nullptr, *logits = nullptr, *shared_act = nullptr, *act = nullptr;  // tagged words
+    uint64_t *xw = nullptr, *logits = nullptr, *shared_act = nullptr, *act = nullptr, *selrec = nullptr;  // tagged words
     uint32_t* counters = nullptr;
     uint32_t* flags = nullptr;  // phase flags (epoch of the completed phase)
     int32_t* error = nullptr;
@@ -411,6 +411,7 @@ void launch_decode(firewing_hip_context* c, size_t first, size_t n, int T, int o
     p.gi = p.ls - 2;
     p.shared_act = c->shared_act;
     p.act = c->act;
+    p.selrec = c->selrec;
     p.x_final = x_final;
     p.out = c->out;
     p.ids = c->ids;
@@ -730,6 +731,8 @@ bool firewing_hip_create(const firewing_hip_shape* shape, firewing_hip_context**
         check(hipMemset(c->logits, 0, L * T * logit_stride((int)E) / 2 * 8), "hipMemset");
         check(hipMemset(c->shared_act, 0, L * T * Is / 2 * 8), "hipMemset");
         check(hipMemset(c->act, 0, L * S * T * I / 2 * 8), "hipMemset");
+        c->selrec = dalloc<uint64_t>(L * record_words((int)T, (int)K));
+        check(hipMemset(c->selrec, 0, L * record_words((int)T, (int)K) * 8), "hipMemset");
         c->counters = dalloc<uint32_t>(L * kCountersPerLayer + 1);
         c->error = dalloc<int32_t>(1);
         c->d_params = dalloc<DecodeParams>(1);
@@ -769,8 +772,8 @@ void firewing_hip_destroy(firewing_hip_context* c) {
     freev(c->shared_up);
     freev(c->shared_down);
     void* bufs[] = {c->d_layers, c->d_weight_table, c->xin, c->xfinal, c->out, c->ids, c->scores,
-                    c->sig, c->xw, c->logits, c->shared_act, c->act, c->counters, c->flags, c->error,
-                    c->d_params};
+                    c->sig, c->xw, c->logits, c->shared_act, c->act, c->selrec, c->counters, c->flags,
+                    c->error, c->d_params};
     for (void* b : bufs)
         if (b) (void)hipFree(b);
     if (c->stream) (void)hipStreamDestroy(c->stream);
@@ -1101,7 +1104,7 @@ extern "C" bool firewing_hip_debug_traced_step(firewing_hip_context* c, const ui
         const size_t L = c->shape.layers, H = c->shape.hidden;
         const size_t E = c->shape.experts, K = c->shape.top_k, I = c->shape.intermediate;
         const size_t Is = c->shape.shared_intermediate;
-        size_t per_layer = (E + 15) / 16 + 1 + (Is + 7) / 8 + K * tokens * (I / 8) + H / 4;
+        size_t per_layer = (E + 15) / 16 + 1 + (Is + 7) / 8 + K * tokens * (I / 8) + H / 4 + 1;
         size_t n = L * per_layer;
         if (cap < n * kTraceWords) return fail("trace buffer too small");
         c->trace = dalloc<uint64_t>(n * kTraceWords);
