@@ -79,16 +79,40 @@ def union_sizes(ids: np.ndarray) -> list[int]:
     return [len(set(ids[l].ravel().tolist())) for l in range(ids.shape[0])]
 
 
-def read_traffic(kernel_avg_ns: float | None):
-    """HBM bytes per launch from the committed rocprofv3 PMC summary, if any."""
-    path = ROOT / "profiles" / "decode_step_48l_t1_pmc.json"
-    if not path.is_file():
+TRAFFIC_SUMMARY = ROOT / "profiles" / "k_moe_decode_48l_t1_hbm_traffic.md"
+
+
+def read_traffic():
+    """HBM bytes per launch of the decode kernel (FETCH_SIZE + WRITE_SIZE,
+    calibrated against a copy of known size) from the committed rocprofv3 PMC
+    summary, or None when there is none."""
+    if not TRAFFIC_SUMMARY.is_file():
         return None
-    try:
-        d = json.loads(path.read_text())
-        return int(d["hbm_bytes_per_launch"])
-    except Exception:
-        return None
+    for line in TRAFFIC_SUMMARY.read_text().splitlines():
+        if line.startswith("hbm_bytes_per_launch:"):
+            try:
+                return int(line.split(":", 1)[1].strip())
+            except ValueError:
+                return None
+    return None
+
+
+COPY_CALIBRATION_BYTES = 1 << 30
+
+
+def copy_calibration(rt, hm) -> None:
+    """Three launches of the plain copy kernel over 1 GiB, for the traffic
+    counters' scale (each reads and writes exactly 1 GiB)."""
+    src = rt.DeviceArray((COPY_CALIBRATION_BYTES // 2,), np.uint16)
+    dst = rt.DeviceArray((COPY_CALIBRATION_BYTES // 2,), np.uint16)
+    stream = rt.Stream()
+    for _ in range(3):
+        hm.copy_bytes(dst.ptr, src.ptr, COPY_CALIBRATION_BYTES, stream.handle)
+    stream.synchronize()
+    stream.destroy()
+    src.free()
+    dst.free()
+    log(f"copy calibration: 3 x {COPY_CALIBRATION_BYTES} bytes")
 
 
 def main() -> int:
@@ -100,6 +124,8 @@ def main() -> int:
     ap.add_argument("--seed", type=lambda s: int(s, 0), default=0x46495245)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-mtp", action="store_true")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="also run a 1 GiB plain copy kernel (traffic-counter calibration)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py runs on one GPU only (asked for --gpus {args.gpus}); the sparse-MoE "
@@ -169,12 +195,15 @@ def main() -> int:
             "peak": HBM_PEAK_GBPS,
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBPS, 4),
-            "traffic": read_traffic(avg_launch_ms * 1e6),
-            "kernel": "k_moe_decode<1>",
+            "traffic": read_traffic(),
+            "kernel": "fw::k_moe_decode<1, 64, 16, 8>",
             "algorithmic_bytes_per_launch": bytes_per_launch,
             "avg_launch_us": round(avg_launch_ms * 1000.0, 2),
         },
     }
+
+    if args.copy_calibration:
+        copy_calibration(rt, hm)
 
     if not args.no_mtp:
         mtp = {}

@@ -68,6 +68,10 @@ def build(verbose: bool = False) -> Path:
     _compile([hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", *[str(o) for _, _, o in units], "-o", str(tmp)],
              verbose)
     os.replace(tmp, LIB)
+    # stand-alone C++ driver of the decode step (for profilers), next to the library
+    drv = PKG / "fw_decode_bench"
+    _compile([hipcc(), "-O2", "-std=c++17", *include, str(CSRC / "fw_decode_bench.cpp"), "-o", str(drv),
+              "-L", str(PKG), "-lfirewing_hip_moe", f"-Wl,-rpath,{PKG}", "-Wl,-rpath,$ORIGIN"], verbose)
     return LIB
 
 

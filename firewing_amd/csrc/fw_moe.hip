@@ -169,6 +169,13 @@ __global__ void k_sigmoid(const uint16_t* in, size_t n, uint16_t* out) {
     if (i < n) out[i] = sigmoid_bf16(in[i], c_exp2_table);
 }
 
+// dst = src, 16 bytes per thread and iteration (a grid-stride streaming copy).
+__global__ void __launch_bounds__(256) k_copy_bytes(uint4* __restrict__ dst, const uint4* __restrict__ src,
+                                                    size_t n16) {
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n16; i += (size_t)gridDim.x * blockDim.x)
+        dst[i] = src[i];
+}
+
 __global__ void k_expf(const float* in, float* out, size_t n) {
     size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (i < n) out[i] = expf_glibc(in[i], c_exp2_table);
@@ -504,6 +511,20 @@ bool firewing_hip_expf_device(const float* in, float* out, size_t count) {
         }
         download(out, dout.ptr, count * 4, nullptr);
         check(hipStreamSynchronize(nullptr), "hipStreamSynchronize");
+        return true;
+    });
+}
+
+bool firewing_hip_copy_bytes(void* dst, const void* src, size_t bytes, void* stream) {
+    return guarded([&] {
+        if (!dst || !src) return fail("copy_bytes: null pointer");
+        if (bytes % 16) return fail("copy_bytes: bytes must be a multiple of 16");
+        if (bytes == 0) return true;
+        const size_t n16 = bytes / 16;
+        const unsigned grid = (unsigned)std::min<size_t>((n16 + 255) / 256, 4096);
+        hipLaunchKernelGGL(k_copy_bytes, dim3(grid), dim3(256), 0, static_cast<hipStream_t>(stream),
+                           static_cast<uint4*>(dst), static_cast<const uint4*>(src), n16);
+        check(hipGetLastError(), "k_copy_bytes launch");
         return true;
     });
 }

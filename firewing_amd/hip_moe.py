@@ -87,6 +87,7 @@ _SIGNATURES = {
                                          ctypes.c_uint32, _b, _u16p]),
     "firewing_hip_expf_host": (None, [ctypes.POINTER(ctypes.c_float), ctypes.POINTER(ctypes.c_float), _sz]),
     "firewing_hip_expf_device": (_b, [ctypes.POINTER(ctypes.c_float), ctypes.POINTER(ctypes.c_float), _sz]),
+    "firewing_hip_copy_bytes": (_b, [_vp, _vp, _sz, _vp]),
 }
 
 _lib = None
@@ -221,6 +222,13 @@ def expf_device(values) -> np.ndarray:
     out = np.empty_like(x)
     _call("firewing_hip_expf_device", _pf(x), _pf(out), x.size)
     return out
+
+
+def copy_bytes(dst_ptr: int, src_ptr: int, nbytes: int, stream: int = 0) -> None:
+    """Device-to-device copy of nbytes (multiple of 16) by a plain streaming
+    kernel, queued on `stream` (a traffic-counter calibration aid)."""
+    _call("firewing_hip_copy_bytes", ctypes.c_void_p(dst_ptr), ctypes.c_void_p(src_ptr), nbytes,
+          ctypes.c_void_p(stream))
 
 
 # ---- resident context ------------------------------------------------------------------

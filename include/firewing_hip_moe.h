@@ -197,6 +197,13 @@ void firewing_hip_expf_host(const float* in, float* out, size_t count);
 /* Device evaluation of the same expf, for verification (synchronous). */
 bool firewing_hip_expf_device(const float* in, float* out, size_t count);
 
+/* Plain device-to-device copy of `bytes` (a multiple of 16) with a streaming
+ * kernel (k_copy_bytes), queued on `stream` (0: the default stream). A
+ * measurement aid with no counterpart in the reference: the bytes it moves are
+ * known exactly, so hardware traffic counters read over it calibrate the
+ * decode kernel's counts. */
+bool firewing_hip_copy_bytes(void* dst, const void* src, size_t bytes, void* stream);
+
 #ifdef __cplusplus
 }
 #endif
