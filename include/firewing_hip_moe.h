@@ -155,7 +155,7 @@ bool firewing_hip_sparse_moe_block(firewing_hip_context* ctx, size_t layer,
                                    const uint16_t* hidden, size_t tokens, int order,
                                    uint16_t* out, firewing_hip_block_captures* captures);
 
-/* Device-pointer variant; hidden [T, H], out [T, H] in HBM. */
+/* Device-pointer variant; hidden [T, H] (4-byte aligned), out [T, H] in HBM. */
 bool firewing_hip_sparse_moe_block_dev(firewing_hip_context* ctx, size_t layer,
                                        const uint16_t* hidden, size_t tokens, int order,
                                        uint16_t* out, void* stream);
@@ -167,7 +167,8 @@ bool firewing_hip_sparse_moe_block_dev(firewing_hip_context* ctx, size_t layer,
  * bias_feature), r_{l+1} = add_bf16(r_l, block_l(h_l)), where rms_norm is
  * bf16(r / sqrt(dot(r, r) / H + 1e-6)) with the reference's dot order; this
  * glue stands in for the rest of the decoder layer, which is not built here.
- * Device pointers: hidden [T, H] in, residual r_L [T, H] out; block_out
+ * Device pointers (hidden and residual 4-byte aligned): hidden [T, H] in,
+ * residual r_L [T, H] out; block_out
  * [L, T, H], ids [L, T, K] (int32) and scores [L, T, K] may be NULL. */
 bool firewing_hip_moe_step_dev(firewing_hip_context* ctx, const uint16_t* hidden, size_t tokens,
                                int order, bool bias_feature, uint16_t* residual,
