@@ -146,12 +146,25 @@ static __device__ __constant__ uint64_t c_exp2_table[32] = {
 
 constexpr int kBatchMatrices = 16;  // C task: matrices per register batch (4 per wave)
 
+// Words of the LDS area that holds the block input (rows role) or the staged
+// activation vectors (combine role): the block input of NT tokens, and the
+// vectors of a whole batch for NT tokens where that fits 32 KiB.
+__host__ __device__ constexpr int stage_words(int NT, int MBI) {
+    return NT * kMaxHidden > (kBatchMatrices * NT * MBI * 16 < 8192 ? kBatchMatrices * NT * MBI * 16 : 8192)
+               ? NT * kMaxHidden
+               : (kBatchMatrices * NT * MBI * 16 < 8192 ? kBatchMatrices * NT * MBI * 16 : 8192);
+}
+// Matrices staged at once (a multiple of 4, so whole waves' matrices): as many
+// of a batch as the area holds for NT tokens each.
+__host__ __device__ constexpr int stage_matrices(int NT, int MBI) {
+    return stage_words(NT, MBI) / (NT * MBI * 16) >= 16 ? 16 : (stage_words(NT, MBI) / (NT * MBI * 16) >= 8 ? 8 : 4);
+}
+
 template <int NT, int MBI>
 struct DecodeShared {
-    // rows: block input as f32; combine: exponentials, then the activation
-    // vectors of one batch (16 matrices x NT tokens x MBI * 16 words)
-    alignas(16) float xs[NT * kMaxHidden > kBatchMatrices * NT * MBI * 16 ? NT * kMaxHidden
-                                                                           : kBatchMatrices * NT * MBI * 16];
+    // rows: block input as f32; combine: exponentials, then staged
+    // activation vectors
+    alignas(16) float xs[stage_words(NT, MBI)];
     uint16_t lg[NT * logit_stride(kMaxExperts)];  // logits of the selected layer
     uint64_t exp2tab[32];
     uint16_t res[(kMaxTopK * NT + 1) * NT * kRowsPerCTask];  // down-row dots [matrix][token][row]
@@ -908,7 +921,7 @@ __device__ __forceinline__ bool combine_task(const DecodeParams& p, uint32_t epo
         if (m_ <= U) {                                                                                    \
             const int kd_ = m_ == 0 ? Is : I;                                                             \
             const uint32_t mask_ = m_ == 0 ? all_tokens : (uint32_t)uniform((int)sh.slot_tokens[m_ - 1]); \
-            int v_ = uniform(sh.vbase[m_ - mb]);                                                          \
+            int v_ = uniform(sh.vbase[m_ - ms]);                                                          \
             _Pragma("unroll") for (int t_ = 0; t_ < NT; ++t_) {                                           \
                 if (mask_ & (1u << t_)) {                                                                 \
                     const uint32_t bits_ = down_row_lds<MBI>(RS, kd_ / 32, act_lds + v_ * act_stride, q);  \
@@ -953,6 +966,7 @@ __device__ __forceinline__ bool combine_task(const DecodeParams& p, uint32_t epo
     const uint32_t* act_lds = reinterpret_cast<const uint32_t*>(sh.xs);
     const int act_stride = max(I, Is) / 2;
     st.loaded = st.staged = -1;
+    constexpr int SB = stage_matrices(NT, MBI);
     for (int mb = 0; mb <= U; mb += kBatchMatrices) {
         if (mb > 0) {
             FW_ISSUE_DOWN(rs0, mb + w);
@@ -960,14 +974,18 @@ __device__ __forceinline__ bool combine_task(const DecodeParams& p, uint32_t epo
             FW_ISSUE_DOWN(rs2, mb + w + 8);
             FW_ISSUE_DOWN(rs3, mb + w + 12);
         }
-        if (!stage_acts<NT, MBI>(p, li, epoch, sh, mb, min(U, mb + kBatchMatrices - 1), slot)) return false;
-        FW_TRACE_MARK(slot, 4);
-        FW_DOWN_DOT(rs0, mb + w);
-        FW_DOWN_DOT(rs1, mb + w + 4);
-        FW_DOWN_DOT(rs2, mb + w + 8);
-        FW_DOWN_DOT(rs3, mb + w + 12);
-        // the next batch's staging overwrites these vectors
-        __syncthreads();
+        // matrices [ms, ms + SB) of the batch: register slots i with 4i in that range
+        for (int sb = 0; sb < kBatchMatrices && mb + sb <= U; sb += SB) {
+            const int ms = mb + sb;
+            if (!stage_acts<NT, MBI>(p, li, epoch, sh, ms, min(U, ms + SB - 1), slot)) return false;
+            FW_TRACE_MARK(slot, 4);
+            if (sb <= 0 && 0 < sb + SB) FW_DOWN_DOT(rs0, mb + w);
+            if (sb <= 4 && 4 < sb + SB) FW_DOWN_DOT(rs1, mb + w + 4);
+            if (sb <= 8 && 8 < sb + SB) FW_DOWN_DOT(rs2, mb + w + 8);
+            if (sb <= 12 && 12 < sb + SB) FW_DOWN_DOT(rs3, mb + w + 12);
+            // the next staging overwrites these vectors
+            __syncthreads();
+        }
     }
 #undef FW_DOWN_DOT
 #undef FW_ISSUE_DOWN
@@ -1071,7 +1089,7 @@ __device__ __forceinline__ void combine_role(const DecodeParams* __restrict__ P,
 // NT tokens; MBH, MBI: 32-column blocks held per hidden row / down row; TK:
 // logits per lane in the top-k.
 template <int NT, int MBH, int MBI, int TK>
-__global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4)))
+__global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(NT <= 2 ? 4 : 2)))
 k_moe_decode(const DecodeParams* __restrict__ P, uint32_t epoch) {
     __shared__ DecodeShared<NT, MBI> sh;
     if (threadIdx.x < 32) sh.exp2tab[threadIdx.x] = c_exp2_table[threadIdx.x];
