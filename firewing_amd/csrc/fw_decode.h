@@ -42,19 +42,18 @@ struct DecodeLayer {
     const uint16_t* gate_up;      // [E][2I][H]
     const uint16_t* down;         // [E][H][I]
     const uint16_t* shared_gate;  // [Is][H]
-    const uint16_t* shared_up;    // [Is][H]
+    const uint16_t* shared_up;    // [Is][H], = shared_gate + Is * H
     const uint16_t* shared_down;  // [H][Is]
 };
 
 enum DecodeCounter : int {
     kCntRouter = 0,
-    kCntSelect = 1,  // the layer's selection record
-    kCntGateUp = 2,  // S and B tasks
-    kCntC = 3,
-    kCountersPerLayer = 4
+    kCntGateUp = 1,  // S and B tasks
+    kCntC = 2,
+    kCountersPerLayer = 3
 };
 
-enum DecodeTaskKind : int { kTaskRouter = 0, kTaskShared = 1, kTaskSelect = 2, kTaskGateUp = 3, kTaskDown = 4 };
+enum DecodeTaskKind : int { kTaskRouter = 0, kTaskShared = 1, kTaskGateUp = 3, kTaskDown = 4 };
 
 constexpr int kRouterRowsPerTask = 16;
 constexpr int kPairsPerTask = 8;
@@ -85,26 +84,29 @@ struct DecodeParams {
     uint64_t* logits;      // [nlayers][T][ls / 2]
     uint64_t* shared_act;  // [nlayers][T][Is / 2]
     uint64_t* act;         // [nlayers][S][T][I / 2]
-    uint64_t* selrec;      // [nlayers][rec_words] selection records (record_words)
     // plain outputs, read after the launch
     uint16_t* x_final;  // [T][H] residual after the last layer, or null
     uint16_t* out;      // [nlayers][T][H] block outputs
     int32_t* ids;       // [nlayers][T][K] rank order
     uint16_t* scores;   // [nlayers][T][K]
     uint16_t* sig;      // [nlayers][T] sigmoid of the shared_expert_gate logit
-    uint32_t* counters;  // [nlayers][kCountersPerLayer] then 1 done counter
+    uint32_t* counters;  // [nlayers][kCountersPerLayer] counter groups, then the done group
     uint32_t* flags;     // [nlayers][kCountersPerLayer][kFlagCopies * kFlagStride] epoch of the completed phase
     int32_t* error;      // 0 ok, 1 timeout, 2 NaN router logit
     uint64_t limit_ticks;
     int n_router, n_shared, n_b, n_c, S;  // tasks per layer; slots
     int nb_rows;                          // B tasks per layer on the rows role (the rest on combine)
     int g_rows, g_comb;                   // workgroups of the rows and combine roles
+    int cpairs;                           // > 0: gate/up pairs past the rows role's B tasks, carried
+                                          // by wave 0 of each C task (one token); 0: B tasks on combine
+    int n_gu;                             // tasks counted in the gate/up phase
+    int cu_count;                         // compute units (workgroup b sits on the CU of b mod cu_count)
     uint64_t* trace;     // profiling builds only
 };
 
 // Task timing (wall clock) for profiling builds only (slots: trace_slot).
 #ifdef FW_DECODE_TRACE
-constexpr int kTraceWords = 14;  // start, dependency met, end, wg << 8 | kind, 8 stage marks, 2 cycle counts
+constexpr int kTraceWords = 18;  // start, dependency met, end, wg << 8 | kind, 12 stage marks, 2 cycle counts
 #define FW_TRACE_STAMP(var)                  \
     const uint64_t var = wall_clock64();     \
     const uint64_t var##_cycles = clock64(); \
@@ -114,6 +116,11 @@ constexpr int kTraceWords = 14;  // start, dependency met, end, wg << 8 | kind, 
         if (threadIdx.x == 0 && p.trace != nullptr && (slot_) >= 0)                \
             p.trace[(size_t)(slot_) * kTraceWords + 4 + (k)] = wall_clock64();     \
     } while (0)
+#define FW_TRACE_VALUE(slot_, k, v)                                                \
+    do {                                                                           \
+        if (threadIdx.x == 0 && p.trace != nullptr && (slot_) >= 0)                \
+            p.trace[(size_t)(slot_) * kTraceWords + 4 + (k)] = (uint64_t)(v);      \
+    } while (0)
 #define FW_TRACE_WRITE(slot_, kind, a, b, c)                                       \
     do {                                                                           \
         if (threadIdx.x == 0 && p.trace != nullptr && (slot_) >= 0) {              \
@@ -122,13 +129,14 @@ constexpr int kTraceWords = 14;  // start, dependency met, end, wg << 8 | kind, 
             tr[1] = (b);                                                           \
             tr[2] = (c);                                                           \
             tr[3] = ((uint64_t)blockIdx.x << 8) | (uint64_t)(kind);                \
-            tr[12] = a##_cycles;                                                   \
-            tr[13] = c##_cycles;                                                   \
+            tr[16] = a##_cycles;                                                   \
+            tr[17] = c##_cycles;                                                   \
         }                                                                          \
     } while (0)
 #else
 #define FW_TRACE_STAMP(var)
 #define FW_TRACE_MARK(slot_, k)
+#define FW_TRACE_VALUE(slot_, k, v)
 #define FW_TRACE_WRITE(slot_, kind, a, b, c)
 #endif
 
@@ -149,8 +157,16 @@ constexpr int kBatchMatrices = 16;  // C task: matrices per register batch (4 pe
 // Words of the LDS area that holds the block input (rows role) or the staged
 // activation vectors (combine role): the block input of NT tokens, and the
 // vectors of a whole batch for NT tokens where that fits 32 KiB.
+// One token with MBI <= 16 (the fused C task) also holds, above the block
+// input and the exponentials, the four gate/up rows of its pairs, and later
+// the tagged words of twelve activation vectors.
+constexpr int kDirectVectors = 12;
+constexpr int kBRowsAt = kMaxHidden + kMaxExperts;  // words
+constexpr int kFusedWords = kBRowsAt + 2 * kMaxHidden > kDirectVectors * 16 * 16 * 2 ? kBRowsAt + 2 * kMaxHidden
+                                                                                      : kDirectVectors * 16 * 16 * 2;
 __host__ __device__ constexpr int stage_words(int NT, int MBI) {
-    return NT * kMaxHidden > (kBatchMatrices * NT * MBI * 16 < 8192 ? kBatchMatrices * NT * MBI * 16 : 8192)
+    return (NT == 1 && MBI <= 16) ? kFusedWords
+           : NT * kMaxHidden > (kBatchMatrices * NT * MBI * 16 < 8192 ? kBatchMatrices * NT * MBI * 16 : 8192)
                ? NT * kMaxHidden
                : (kBatchMatrices * NT * MBI * 16 < 8192 ? kBatchMatrices * NT * MBI * 16 : 8192);
 }
@@ -182,16 +198,22 @@ struct DecodeShared {
     int32_t nvec;
     int32_t nunion;
     int32_t flag;
+    int32_t trace_stale;  // profiling builds: stale words of the last block-input read
 };
 
-// Selection record of a layer, tagged words: [0] union size U, then per slot
-// (S = T * K entries) the expert id and the token mask, then per token and
-// ascending-id position k the slot (words [0, 1 + 3S): the slot map, published
-// first), then per token and position the bf16 score and per token the bf16
-// shared-gate sigmoid (the weights, published when computed).
-__host__ __device__ constexpr int record_words(int T, int K) { return 1 + 4 * T * K + T; }
-__host__ __device__ constexpr int record_map_words(int T, int K) { return 1 + 3 * T * K; }
+// The workgroups on one CU (blocks b, b + cu_count, ...) place their waves on
+// the SIMDs identically, so a wave doing a workgroup's serial work (top-k,
+// scores, the norm, the mixture) would share one SIMD with the same wave of the
+// other workgroups there. That work goes to the wave whose index is rotated by
+// the workgroup's slot on its CU; rel_wave is a wave's index relative to it.
+__device__ __forceinline__ int rel_wave(const DecodeParams& p) {
+    const int lead = (int)(blockIdx.x / (unsigned)p.cu_count) & 3;
+    return (wave_id() - lead) & 3;
+}
 
+__device__ __forceinline__ uint32_t* phase_counters(const DecodeParams& p, int li, int phase) {
+    return p.counters + ((size_t)li * kCountersPerLayer + phase) * kCounterGroupWords;
+}
 __device__ __forceinline__ uint32_t* phase_flags(const DecodeParams& p, int li, int phase) {
     return p.flags + ((size_t)li * kCountersPerLayer + phase) * kFlagCopies * kFlagStride;
 }
@@ -222,8 +244,14 @@ __device__ __forceinline__ bool load_input(const DecodeParams& p, int li, uint32
         // this thread's words: tid, tid + 256, ... below pairs
         const int n = (pairs - (int)threadIdx.x + kThreads - 1) / kThreads;
         uint64_t v[NT * kXWords];
+        int stale = 0;
         ok = load_tagged<NT * kXWords, kThreads>(v, p.xw + (size_t)li * pairs + threadIdx.x, n, epoch, p.error,
-                                                 p.limit_ticks);
+                                                 p.limit_ticks, &stale);
+#ifdef FW_DECODE_TRACE
+        stale = __syncthreads_count(stale);
+        if (threadIdx.x == 0) sh.trace_stale = stale;
+#endif
+        (void)stale;
 #pragma unroll
         for (int k = 0; k < NT * kXWords; ++k) {
             const int i = (int)threadIdx.x + k * kThreads;
@@ -244,7 +272,7 @@ __device__ __forceinline__ void normalise_input(const DecodeParams& p, SH& sh) {
     if (!p.prenorm) return;
     const int T = p.T, n = p.H;
     float* xs = sh.xs;
-    const int w = wave_id(), lane = lane_id();
+    const int w = rel_wave(p), lane = lane_id();
     if (w < T) {
         const float* r = xs + w * n;
         float c = 0.0f;
@@ -271,10 +299,14 @@ __device__ __forceinline__ void normalise_input(const DecodeParams& p, SH& sh) {
         if (lane == 0) sh.inv[w] = 1.0f / sqrtf(add_rn(ss / (float)n, 1e-6f));
     }
     __syncthreads();
-    for (int i = threadIdx.x; i < T * n; i += kThreads) {
-        float hv = from_bf16(to_bf16(mul_rn(xs[i], sh.inv[i / n])));
-        if (p.bias_feature && i % n == n - 1) hv = 1.0f;
-        xs[i] = hv;
+    for (int t = 0; t < T; ++t) {
+        const float inv = sh.inv[t];
+        float* r = xs + t * n;
+        for (int i = threadIdx.x; i < n; i += kThreads) {
+            float hv = from_bf16(to_bf16(mul_rn(r[i], inv)));
+            if (p.bias_feature && i == n - 1) hv = 1.0f;
+            r[i] = hv;
+        }
     }
     __syncthreads();
 }
@@ -303,23 +335,14 @@ __device__ __forceinline__ bool load_logits(const DecodeParams& p, int li, uint3
 // the selections in ascending expert id, the execution order of
 // src/decoder_layer.rs:422-424: sorted[slot], slot_tokens[slot] (token mask),
 // tslot[t][k] (slot of the token's k-th expert in ascending id), nunion.
-// Requires the logits in LDS. reject_nan: src/decoder_layer.rs:279-281 (the
-// error word is set; the launch then completes and reports it). TK: logits per
-// lane in the top-k (E <= 64 * TK).
+// Requires the logits in LDS. TK: logits per lane in the top-k (E <= 64 * TK).
 template <int NT, int TK, class SH>
-__device__ __forceinline__ void select_experts(const DecodeParams& p, SH& sh, bool reject_nan,
-                                               int slot_trace = -1) {
+__device__ __forceinline__ void select_experts(const DecodeParams& p, SH& sh, int slot_trace = -1) {
     (void)slot_trace;
     const int T = p.T, E = p.E, K = p.K, S = p.S, LS = p.ls;
-    const int lane = lane_id(), w = wave_id();
+    const int lane = lane_id(), w = rel_wave(p);
     if (w < T) {
-        const uint16_t* lt = sh.lg + w * LS;
-        if (reject_nan) {
-            int nan = 0;
-            for (int e = lane; e < E; e += kWave) nan |= ((lt[e] & 0x7fffu) > 0x7f80u);
-            if (__any(nan) && lane == 0) atomicCAS(p.error, 0, 2);
-        }
-        wave_topk<TK>(lt, E, K, sh.ids + w * kMaxTopK);
+        wave_topk<TK>(sh.lg + w * LS, E, K, sh.ids + w * kMaxTopK);
     }
     FW_TRACE_MARK(slot_trace, 4);
     __syncthreads();
@@ -329,7 +352,7 @@ __device__ __forceinline__ void select_experts(const DecodeParams& p, SH& sh, bo
     // runs over the entries in order with the entry's values read from its
     // lane. One token selects distinct experts: its slots are the ranks of its
     // ids.
-    if (w == 0 && T == 1) {
+    if (w == 0 && (NT == 1 || T == 1)) {
         const int id = lane < K ? sh.ids[lane] : 0x7fffffff;
         int rank = 0;
         for (int j = 0; j < K; ++j) rank += (__builtin_amdgcn_readlane(id, j) < id) ? 1 : 0;
@@ -341,7 +364,7 @@ __device__ __forceinline__ void select_experts(const DecodeParams& p, SH& sh, bo
         }
         for (int s2 = K + lane; s2 < S; s2 += kWave) sh.slot_tokens[s2] = 0u;
         if (lane == 0) sh.nunion = K;
-    } else if (w == 0) {
+    } else if (NT > 1 && w == 0) {
         const int n_sel = T * K;
         int id[2], tok[2], slot[2] = {0, 0}, rank_in_token[2] = {0, 0};
         bool first[2];
@@ -400,18 +423,21 @@ __device__ __forceinline__ void select_experts(const DecodeParams& p, SH& sh, bo
     __syncthreads();
 }
 
-// Scores of the selected experts: src/router.rs:248-262 /
+// Scores of the selected experts (token t on the wave first_wave + t relative
+// to the lead wave; without `barrier` the caller synchronises before the
+// results are read): src/router.rs:248-262 /
 // src/decoder_layer.rs:290-306 (max, exp(v - max), one sequential f32 sum in
 // index order, renormalised over the selection), as tweight[t][k] in the
 // token's ascending-id order, and the shared-gate sigmoid. With host_outputs
 // also the rank-order ids and scores and the sigmoid for the caller.
 template <int NT, class SH>
-__device__ __forceinline__ void score_experts(const DecodeParams& p, int li, SH& sh, bool host_outputs) {
+__device__ __forceinline__ void score_experts(const DecodeParams& p, int li, SH& sh, bool host_outputs,
+                                              int exp_offset = 0, int first_wave = 0, bool barrier = true) {
     const int T = p.T, E = p.E, K = p.K, LS = p.ls;
-    const int lane = lane_id(), w = wave_id();
+    const int lane = lane_id(), w = (rel_wave(p) - first_wave) & 3;
     if (w < T) {
         const uint16_t* lt = sh.lg + w * LS;
-        float* ew = sh.xs + w * E;
+        float* ew = sh.xs + exp_offset + w * E;
         float mx = -__builtin_inff();
         for (int e = lane; e < E; e += kWave) mx = fmaxf(mx, from_bf16(lt[e]));
 #pragma unroll
@@ -463,7 +489,7 @@ __device__ __forceinline__ void score_experts(const DecodeParams& p, int li, SH&
             if (host_outputs) p.sig[(size_t)li * T + w] = sg;
         }
     }
-    __syncthreads();
+    if (barrier) __syncthreads();
 }
 
 // ---- tasks ----------------------------------------------------------------------------
@@ -482,20 +508,23 @@ struct LdsState {
     int loaded = -1, staged = -1, selected = -1, scored = -1;  // scored: route weights and sigmoid
 };
 
-// Trace slot of a task: layer * (R + S + B + C tasks + 1) + its index in that
-// order, the selection task last.
+// Trace slot of a task: layer * (R + S + B + C tasks) + its index in that
+// order.
 __device__ __forceinline__ int trace_slot(const DecodeParams& p, int li, int index) {
-    return li * (p.n_router + p.n_shared + p.n_b + p.n_c + 1) + index;
+    return li * (p.n_router + p.n_shared + p.n_b + p.n_c) + index;
 }
 
 // Block input of layer li in LDS, normalised.
 template <int NT, class SH>
 __device__ __forceinline__ bool stage_layer_input(const DecodeParams& p, uint32_t epoch, SH& sh,
-                                                  LdsState& st, int li) {
+                                                  LdsState& st, int li, int slot = -1) {
+    (void)slot;
     if (st.staged == li) return true;
     if (st.loaded != li) {
         if (!load_input<NT>(p, li, epoch, sh)) return false;
         st.loaded = li;
+        FW_TRACE_MARK(slot, 2);
+        FW_TRACE_VALUE(slot, 4, sh.trace_stale);
     }
     normalise_input<NT>(p, sh);
     st.staged = li;
@@ -505,13 +534,13 @@ __device__ __forceinline__ bool stage_layer_input(const DecodeParams& p, uint32_
 // Selection of layer li in LDS (waits for its router tasks).
 template <int NT, int TK, class SH>
 __device__ __forceinline__ bool select_layer(const DecodeParams& p, uint32_t epoch, SH& sh, LdsState& st,
-                                             int li, bool reject_nan, int slot) {
+                                             int li, int slot) {
     if (st.selected == li) return true;
     if (!wait_phase(phase_flags(p, li, kCntRouter), epoch, p.error, p.limit_ticks, &sh.flag)) return false;
     FW_TRACE_MARK(slot, 2);
     if (!load_logits<NT>(p, li, epoch, sh)) return false;
     FW_TRACE_MARK(slot, 3);
-    select_experts<NT, TK>(p, sh, reject_nan, slot);
+    select_experts<NT, TK>(p, sh, slot);
     st.selected = li;
     return true;
 }
@@ -536,10 +565,11 @@ __device__ __forceinline__ bool router_task(const DecodeParams& p, uint32_t epoc
     const int out_index = row0 + (valid ? rin : 0);
     const uint16_t* wrow = L.router + (size_t)out_index * H;
     LineShare<MBH> rs;
-    if (wave_active && !fold) line_issue(rs, wrow, H / 32, q);
+    if (wave_active && !fold)
+        line_issue(rs, L.router + (size_t)row0 * H, (uint32_t)(valid ? rin : 0) * (uint32_t)H * 2u, q);
     if (li > 0 && !wait_phase(phase_flags(p, li - 1, kCntC), epoch, p.error, p.limit_ticks, &sh.flag)) return false;
     FW_TRACE_STAMP(t1);
-    if (!stage_layer_input<NT>(p, epoch, sh, st, li)) return false;
+    if (!stage_layer_input<NT>(p, epoch, sh, st, li, slot)) return false;
     FW_TRACE_MARK(slot, 0);
     uint64_t* lw = p.logits + (size_t)li * T * (p.ls / 2);
     if (fold) {
@@ -565,12 +595,12 @@ __device__ __forceinline__ bool router_task(const DecodeParams& p, uint32_t epoc
             const uint32_t bits = to_bf16(d);
             uint32_t next = (uint32_t)__shfl((int)bits, (lane + kLanesPerRow) & 63, kWave);
             if (gate_task) next = 0u;
-            if (q == 0 && (g & 1) == 0 && valid) coherent_store64(lw + (tt * p.ls + at) / 2, tagged(bits | (next << 16), epoch));
+            if (tt < T && q == 0 && (g & 1) == 0 && valid)
+                coherent_store64(lw + (tt * p.ls + at) / 2, tagged(bits | (next << 16), epoch));
         }
     }
     FW_TRACE_MARK(slot, 1);
-    publish(p.counters + (size_t)li * kCountersPerLayer + kCntRouter, (uint32_t)p.n_router,
-            phase_flags(p, li, kCntRouter), epoch);
+    publish(phase_counters(p, li, kCntRouter), p.n_router, j, phase_flags(p, li, kCntRouter), epoch);
     FW_TRACE_STAMP(t2);
     FW_TRACE_WRITE(slot, kTaskRouter, t0, t1, t2);
     return true;
@@ -587,16 +617,17 @@ __device__ __forceinline__ bool pairs_task(const DecodeParams& p, uint32_t epoch
     const int lane = lane_id(), w = wave_id(), g = lane / kLanesPerRow, q = lane % kLanesPerRow;
     const int T = p.T, H = p.H, I = p.I, Is = p.Is;
     const DecodeLayer& L = p.layers[li];
-    const uint16_t* wrow;
+    const uint16_t* wbase;  // the task's first gate row; up rows follow `up` rows later
     uint64_t* act_out;
-    int act_stride, pair0;  // words per token
+    int act_stride, pair0, up;  // words per token
     bool work = true;
     uint32_t mask = (1u << T) - 1u;
     if (shared) {
         pair0 = js * kPairsPerTask;
         act_out = p.shared_act + (size_t)li * T * (Is / 2);
         act_stride = Is / 2;
-        wrow = g < 2 ? L.shared_gate : L.shared_up;
+        wbase = L.shared_gate;  // shared_up follows it
+        up = Is;
     } else {
         const int per_slot = I / kPairsPerTask;
         const int s = js / per_slot;
@@ -607,21 +638,23 @@ __device__ __forceinline__ bool pairs_task(const DecodeParams& p, uint32_t epoch
                 return false;
             if (!stage_layer_input<NT>(p, epoch, sh, st, li)) return false;
         }
-        if (!select_layer<NT, TK>(p, epoch, sh, st, li, false, slot)) return false;
+        if (!select_layer<NT, TK>(p, epoch, sh, st, li, slot)) return false;
         FW_TRACE_MARK(slot, 0);
         work = s < uniform(sh.nunion);
         const int e = work ? uniform(sh.sorted[s]) : 0;
         mask = work ? (uint32_t)uniform((int)sh.slot_tokens[s]) : 0u;
-        const uint16_t* gate_w = L.gate_up + (size_t)e * 2 * I * H;
+        wbase = L.gate_up + (size_t)e * 2 * I * H;
+        up = I;
         pair0 = (js - s * per_slot) * kPairsPerTask;
         act_out = p.act + ((size_t)li * p.S + s) * (size_t)T * (I / 2);
         act_stride = I / 2;
-        wrow = g < 2 ? gate_w : gate_w + (size_t)I * H;
     }
     const int out_index = pair0 + 2 * w + (g & 1);
-    wrow += (size_t)out_index * H;
+    const uint32_t row_rel = (uint32_t)((g < 2 ? 0 : up) + (g & 1));  // rows past the wave's first gate row
+    const uint16_t* wave_row = wbase + (size_t)(pair0 + 2 * w) * H;
+    const uint16_t* wrow = wave_row + (size_t)row_rel * H;
     LineShare<MBH> rs;
-    if (work) line_issue(rs, wrow, H / 32, q);
+    if (work) line_issue(rs, wave_row, row_rel * (uint32_t)H * 2u, q);
     if (shared && li > 0 && !wait_phase(phase_flags(p, li - 1, kCntC), epoch, p.error, p.limit_ticks, &sh.flag))
         return false;
     FW_TRACE_STAMP(t1);
@@ -647,91 +680,11 @@ __device__ __forceinline__ bool pairs_task(const DecodeParams& p, uint32_t epoch
         }
         FW_TRACE_MARK(slot, 1);
     }
-    publish(p.counters + (size_t)li * kCountersPerLayer + kCntGateUp, (uint32_t)(p.n_shared + p.n_b + 1),
+    publish(phase_counters(p, li, kCntGateUp), p.n_gu, shared ? js : p.n_shared + js,
             phase_flags(p, li, kCntGateUp), epoch);
     FW_TRACE_STAMP(t2);
     FW_TRACE_WRITE(slot, shared ? kTaskShared : kTaskGateUp, t0, t1, t2);
     return true;
-}
-
-// Z task of layer li: the layer's selection, scores and shared-gate sigmoid,
-// computed once (with the caller's ids, scores and sigmoid) and published as
-// the layer's selection record for the C tasks.
-template <int NT, int TK, class SH>
-__device__ __forceinline__ bool select_task(const DecodeParams& p, uint32_t epoch, SH& sh, LdsState& st,
-                                            int li) {
-    FW_TRACE_STAMP(t0);
-    const int slot = trace_slot(p, li, p.n_router + p.n_shared + p.n_b + p.n_c);
-    (void)slot;
-    if (!select_layer<NT, TK>(p, epoch, sh, st, li, p.order == 0, slot)) return false;
-    FW_TRACE_STAMP(t1);
-    const int T = p.T, K = p.K, S = T * K;
-    const int words = record_words(T, K), map_words = record_map_words(T, K);
-    uint64_t* rec = p.selrec + (size_t)li * words;
-    for (int i = threadIdx.x; i < map_words; i += kThreads) {
-        uint32_t v;
-        if (i == 0) {
-            v = (uint32_t)sh.nunion;
-        } else if (i < 1 + S) {
-            v = (uint32_t)sh.sorted[i - 1];
-        } else if (i < 1 + 2 * S) {
-            v = sh.slot_tokens[i - 1 - S];
-        } else {
-            v = (uint32_t)sh.tslot[i - 1 - 2 * S];
-        }
-        coherent_store64(rec + i, tagged(v, epoch));
-    }
-    publish(p.counters + (size_t)li * kCountersPerLayer + kCntSelect, 1u, phase_flags(p, li, kCntSelect), epoch);
-    FW_TRACE_MARK(slot, 0);
-    // the exponentials overwrite the staged input
-    score_experts<NT>(p, li, sh, true);
-    st.loaded = st.staged = -1;
-    st.scored = li;
-    for (int i = map_words + threadIdx.x; i < words; i += kThreads) {
-        const uint32_t v = i < 1 + 4 * S ? sh.tweight[i - 1 - 3 * S] : sh.sig[i - 1 - 4 * S];
-        coherent_store64(rec + i, tagged(v, epoch));
-    }
-    FW_TRACE_MARK(slot, 1);
-    // the weights complete with the gate/up phase
-    publish(p.counters + (size_t)li * kCountersPerLayer + kCntGateUp, (uint32_t)(p.n_shared + p.n_b + 1),
-            phase_flags(p, li, kCntGateUp), epoch);
-    FW_TRACE_STAMP(t2);
-    FW_TRACE_WRITE(slot, kTaskSelect, t0, t1, t2);
-    return true;
-}
-
-// Words [first, last) of the selection record of layer li into LDS.
-template <int NT, class SH>
-__device__ __forceinline__ bool load_record(const DecodeParams& p, int li, uint32_t epoch, SH& sh,
-                                            int first, int last) {
-    constexpr int kWords = (record_words(NT, kMaxTopK) + kThreads - 1) / kThreads;
-    const int T = p.T, K = p.K, S = T * K;
-    const int tid = threadIdx.x;
-    const int n = (last - first - tid + kThreads - 1) / kThreads;
-    uint64_t v[kWords];
-    const bool ok = load_tagged<kWords, kThreads>(v, p.selrec + (size_t)li * record_words(T, K) + first + tid, n,
-                                                  epoch, p.error, p.limit_ticks);
-#pragma unroll
-    for (int k = 0; k < kWords; ++k) {
-        if (k < n) {
-            const int i = first + tid + k * kThreads;
-            const uint32_t x = (uint32_t)v[k];
-            if (i == 0) {
-                sh.nunion = (int32_t)x;
-            } else if (i < 1 + S) {
-                sh.sorted[i - 1] = (int32_t)x;
-            } else if (i < 1 + 2 * S) {
-                sh.slot_tokens[i - 1 - S] = x;
-            } else if (i < 1 + 3 * S) {
-                sh.tslot[i - 1 - 2 * S] = (int32_t)x;
-            } else if (i < 1 + 4 * S) {
-                sh.tweight[i - 1 - 3 * S] = (uint16_t)x;
-            } else {
-                sh.sig[i - 1 - 4 * S] = (uint16_t)x;
-            }
-        }
-    }
-    return __syncthreads_and(ok) != 0;
 }
 
 // Stages into LDS the activation vectors of matrices [mb, me] of layer li (m
@@ -800,6 +753,7 @@ __device__ __forceinline__ bool stage_acts(const DecodeParams& p, int li, uint32
         }
         // words not yet carrying the epoch (stale cached lines, stores in
         // flight) are read again past the caches, all of them per pass
+        if (v0 == 0 && mb == 0) FW_TRACE_MARK(slot, 8);
         uint64_t start = 0;
         for (int pass = 0;; ++pass) {
             bool all = true;
@@ -852,31 +806,98 @@ __device__ __forceinline__ bool stage_acts(const DecodeParams& p, int li, uint32
     return __syncthreads_and(ok) != 0;
 }
 
+// The sweep of down_row_lds (STRIDE: words between activation pairs, 2 for
+// tagged words).
+template <int MAXB, int STRIDE = 1>
+__device__ __forceinline__ uint32_t down_row_sweep(const LineShare<MAXB>& r, int nb, const uint32_t* a0, int q) {
+    // the activation pairs of eight blocks at a time (one LDS wait each), then
+    // their chain steps
+    constexpr int kStep = 8;
+    float c0 = 0.0f, c1 = 0.0f;
+#pragma unroll
+    for (int u0 = 0; u0 < MAXB; u0 += kStep) {
+        uint32_t a[kStep];
+#pragma unroll
+        for (int i = 0; i < kStep; ++i) {
+            if (u0 + i < MAXB && u0 + i < nb) a[i] = a0[STRIDE * 16 * (u0 + i)];
+        }
+#pragma unroll
+        for (int i = 0; i < kStep; i += 2) {
+            const int v = (u0 + i) / 2;
+            if (v < (MAXB + 1) / 2) {
+                uint32_t first, second;
+                line_pairs(r.w[v], q, first, second);
+#pragma unroll
+                for (int half = 0; half < 2; ++half) {
+                    const int u = u0 + i + half;
+                    if (u < MAXB && u < nb) {
+                        const uint32_t wv = half ? second : first;
+                        c0 = add_rn(c0, mul_rn(bf16_lo(wv), bf16_lo(a[i + half])));
+                        c1 = add_rn(c1, mul_rn(bf16_hi(wv), bf16_hi(a[i + half])));
+                    }
+                }
+            }
+        }
+        __builtin_amdgcn_sched_barrier(0);
+    }
+    return to_bf16(add_rn(tree32_reduce_lines(c0, c1), 0.0f));
+}
+
 // One down row against an activation vector staged in LDS (av: its first
 // word): the chains of src/expert.rs:514-552 over K = nblocks * 32 (so the
 // tail sum is +0.0). This lane's chain pair of block b is activation pair
 // 16 b + line_column(q) / 2.
-template <int MAXB>
+template <int MAXB, int STRIDE = 1>
 __device__ __forceinline__ uint32_t down_row_lds(const LineShare<MAXB>& r, int nblocks, const uint32_t* av, int q) {
-    const uint32_t* a0 = av + line_column(q) / 2;
-    const int nb = opaque(nblocks);
-    float c0 = 0.0f, c1 = 0.0f;
-#pragma unroll
-    for (int v = 0; v < (MAXB + 1) / 2; ++v) {
-        uint32_t first, second;
-        line_pairs(r.w[v], q, first, second);
-#pragma unroll
-        for (int half = 0; half < 2; ++half) {
-            const int u = 2 * v + half;
-            if (u < MAXB && u < nb) {
-                const uint32_t wv = half ? second : first;
-                const uint32_t a = a0[16 * u];
-                c0 = add_rn(c0, mul_rn(bf16_lo(wv), bf16_lo(a)));
-                c1 = add_rn(c1, mul_rn(bf16_hi(wv), bf16_hi(a)));
-            }
+    const uint32_t* a0 = av + STRIDE * (line_column(q) / 2);
+    return down_row_sweep<MAXB, STRIDE>(r, opaque(nblocks), a0, q);
+}
+
+// One token, matrices 0..U (U < kDirectVectors): the tagged words of every
+// activation vector of the task go straight from global memory into LDS
+// (sixteen bytes per lane, no registers held while they travel), vector m at
+// word m * stride (stride = max(I, Is) / 2, a multiple of 128); then words
+// without the epoch are read again past the caches until they carry it.
+template <int MBI, class SH>
+__device__ __forceinline__ bool stage_acts_direct(const DecodeParams& p, int li, uint32_t epoch, SH& sh, int U) {
+    const int I = p.I, Is = p.Is;
+    const int stride = max(I, Is) / 2;
+    const int parts = stride / 128;  // 1 KB parts: 64 lanes x 16 bytes
+    uint64_t* raw = reinterpret_cast<uint64_t*>(sh.xs);
+    const int w = wave_id(), lane = lane_id();
+    auto source = [&](int m) -> const uint64_t* {
+        return m == 0 ? p.shared_act + (size_t)li * (Is / 2) : p.act + ((size_t)li * p.S + m - 1) * (I / 2);
+    };
+    for (int c = w; c < (U + 1) * parts; c += kThreads / kWave) {
+        const int m = c / parts, h = c - m * parts;
+        if (h * 128 < (m == 0 ? Is / 2 : I / 2)) {
+            __builtin_amdgcn_global_load_lds(
+                reinterpret_cast<const void*>(source(m) + h * 128 + 2 * lane),
+                (__attribute__((address_space(3))) void*)(raw + (size_t)m * stride + h * 128), 16, 0, 0);
         }
     }
-    return to_bf16(add_rn(tree32_reduce_lines(c0, c1), 0.0f));
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    bool ok = true;
+    for (int i = threadIdx.x; i < (U + 1) * stride; i += kThreads) {
+        const int m = i / stride, wd = i - m * stride;
+        if (wd < (m == 0 ? Is / 2 : I / 2) && !has_tag(raw[i], epoch)) {
+            const uint64_t* src = source(m) + wd;
+            const uint64_t start = wall_clock64();
+            uint64_t v;
+            while (!has_tag(v = coherent_load64(src), epoch)) {
+                if (coherent_load(p.error) != 0 || wall_clock64() - start > p.limit_ticks) {
+                    int32_t expected = 0;
+                    __hip_atomic_compare_exchange_strong(p.error, &expected, 1, __ATOMIC_RELAXED, __ATOMIC_RELAXED,
+                                                         __HIP_MEMORY_SCOPE_AGENT);
+                    ok = false;
+                    break;
+                }
+            }
+            raw[i] = v;
+        }
+    }
+    return __syncthreads_and(ok) != 0;
 }
 
 // C task j of layer li: hidden rows 4j .. 4j + 3. Matrix m of the task: m = 0
@@ -897,12 +918,8 @@ __device__ __forceinline__ bool combine_task(const DecodeParams& p, uint32_t epo
     const int row = r0 + g;
     LineShare<MBI> rs0, rs1, rs2, rs3;
     // the shared expert's rows need no selection: issue them first
-    if (w == 0) line_issue(rs0, L.shared_down + (size_t)row * Is, Is / 32, q);
-    if (st.selected != li) {
-        if (!wait_phase(phase_flags(p, li, kCntSelect), epoch, p.error, p.limit_ticks, &sh.flag)) return false;
-        if (!load_record<NT>(p, li, epoch, sh, 0, record_map_words(T, K))) return false;
-        st.selected = li;
-    }
+    if (w == 0) line_issue(rs0, L.shared_down + (size_t)r0 * Is, (uint32_t)(g * Is * 2), q);
+    if (!select_layer<NT, TK>(p, epoch, sh, st, li, slot)) return false;
     FW_TRACE_MARK(slot, 2);
     const int U = uniform(sh.nunion);
 #define FW_ISSUE_DOWN(RS, M)                                                                  \
@@ -910,9 +927,9 @@ __device__ __forceinline__ bool combine_task(const DecodeParams& p, uint32_t epo
         const int m_ = (M);                                                                   \
         if (m_ >= 1 && m_ <= U) {                                                             \
             const uint16_t* wm_ = L.down + (size_t)uniform(sh.sorted[m_ - 1]) * (size_t)H * I; \
-            line_issue(RS, wm_ + (size_t)row * I, I / 32, q);                                  \
+            line_issue(RS, wm_ + (size_t)r0 * I, (uint32_t)(g * I * 2), q);                    \
         } else if (m_ == 0) {                                                                 \
-            line_issue(RS, L.shared_down + (size_t)row * Is, Is / 32, q);                      \
+            line_issue(RS, L.shared_down + (size_t)r0 * Is, (uint32_t)(g * Is * 2), q); \
         }                                                                                     \
     } while (0)
 #define FW_DOWN_DOT(RS, M)                                                                                \
@@ -935,12 +952,28 @@ __device__ __forceinline__ bool combine_task(const DecodeParams& p, uint32_t epo
     FW_ISSUE_DOWN(rs1, w + 4);
     FW_ISSUE_DOWN(rs2, w + 8);
     FW_ISSUE_DOWN(rs3, w + 12);
-    // The residual words this task updates (ready since the router ran), read
-    // while the gate/up phase runs: one thread per token and row.
+    // Route weights and the shared-gate sigmoid while the gate/up phase runs
+    // (the exponentials overwrite the staged block input); task 0 also
+    // reports the layer's ids, scores and sigmoid and rejects a NaN logit
+    // (src/decoder_layer.rs:279-281).
     const int tid = threadIdx.x;
-    const bool mixer = tid < T * kRowsPerCTask;
-    const int mt = tid / kRowsPerCTask;
-    const int mg = tid % kRowsPerCTask;
+    if (j == 0 && p.order == 0) {
+        int nan = 0;
+        for (int e = tid; e < T * p.ls; e += kThreads) nan |= (e % p.ls < p.E) && ((sh.lg[e] & 0x7fffu) > 0x7f80u);
+        if (__syncthreads_or(nan) && tid == 0) atomicCAS(p.error, 0, 2);
+    }
+    if (st.scored != li || j == 0) {
+        score_experts<NT>(p, li, sh, j == 0);
+        st.loaded = st.staged = -1;
+        st.scored = li;
+    }
+    FW_TRACE_MARK(slot, 5);
+    // The residual words this task updates (ready since the router ran): one
+    // lane of the lead wave per token and row.
+    const int rt = rel_wave(p) * kWave + lane;
+    const bool mixer = rt < T * kRowsPerCTask;
+    const int mt = rt / kRowsPerCTask;
+    const int mg = rt % kRowsPerCTask;
     const size_t at = ((size_t)mt * H + r0 + (mg & ~1)) / 2;
     bool ok = true;
     uint32_t rin = 0;
@@ -956,11 +989,6 @@ __device__ __forceinline__ bool combine_task(const DecodeParams& p, uint32_t epo
     FW_TRACE_MARK(slot, 3);
     if (!wait_phase(phase_flags(p, li, kCntGateUp), epoch, p.error, p.limit_ticks, &sh.flag)) return false;
     FW_TRACE_STAMP(t1);
-    if (st.scored != li) {
-        if (!load_record<NT>(p, li, epoch, sh, record_map_words(T, K), record_words(T, K))) return false;
-        st.scored = li;
-    }
-    FW_TRACE_MARK(slot, 5);
     // Batches of 16 matrices (4 per wave): the batch's activation vectors
     // are staged in LDS once for all waves, then each wave runs its rows.
     const uint32_t* act_lds = reinterpret_cast<const uint32_t*>(sh.xs);
@@ -1028,7 +1056,186 @@ __device__ __forceinline__ bool combine_task(const DecodeParams& p, uint32_t epo
     }
     if (!__syncthreads_and(ok)) return false;
     FW_TRACE_MARK(slot, 1);
-    publish(p.counters + (size_t)li * kCountersPerLayer + kCntC, (uint32_t)p.n_c, phase_flags(p, li, kCntC), epoch);
+    publish(phase_counters(p, li, kCntC), p.n_c, j, phase_flags(p, li, kCntC), epoch);
+    FW_TRACE_STAMP(t2);
+    FW_TRACE_WRITE(slot, kTaskDown, t0, t1, t2);
+    return true;
+}
+
+// Whether a variant carries the fused C task (one token; three down-row slots
+// per wave).
+__host__ __device__ constexpr bool fused_combine(int NT, int MBH, int MBI) {
+    (void)MBH;
+    return NT == 1 && MBI <= 16;
+}
+
+// C task j of layer li for one token when the gate/up pairs past the rows
+// role's B tasks ride on the C tasks (p.cpairs = 2 pairs per task): the lead
+// wave computes pairs nb_rows * 8 + 2j and + 1 like a B task, from rows it
+// copies straight into LDS (gate rows for lane groups 0 and 2, up rows for 1
+// and 3); every wave holds down rows of three matrices (matrix m: the shared
+// expert for m = 0, slot m - 1 else; on wave m % 4, register slot m / 4). All
+// rows are requested as soon as the selection is known, so no C task waits
+// behind a B task of its workgroup.
+template <int NT, int MBH, int MBI, int TK, class SH>
+__device__ __forceinline__ bool combine_task_fused(const DecodeParams& p, uint32_t epoch, SH& sh, LdsState& st,
+                                                   int li, int j) {
+    static_assert(fused_combine(NT, MBH, MBI), "one token");
+    static_assert(stage_words(NT, MBI) >= kBRowsAt + 2 * kMaxHidden, "gate/up rows above the exponentials");
+    static_assert(stage_words(NT, MBI) >= kDirectVectors * MBI * 16 * 2, "tagged words of the staged vectors");
+    FW_TRACE_STAMP(t0);
+    const int slot = trace_slot(p, li, p.n_router + p.n_shared + p.n_b + j);
+    (void)slot;
+    // w: index relative to the lead wave
+    const int lane = lane_id(), w = rel_wave(p), g = lane / kLanesPerRow, q = lane % kLanesPerRow;
+    const int H = p.H, I = p.I, Is = p.Is, K = p.K;
+    const DecodeLayer& L = p.layers[li];
+    const int r0 = j * kRowsPerCTask;
+    LineShare<MBI> c[3];
+    // the shared expert's rows need no selection: issue them first
+    if (w == 0) line_issue(c[0], L.shared_down + (size_t)r0 * Is, (uint32_t)(g * Is * 2), q);
+    // this task's gate/up pairs need the block input (ready with the previous layer)
+    if (li > 0 && !wait_phase(phase_flags(p, li - 1, kCntC), epoch, p.error, p.limit_ticks, &sh.flag)) return false;
+    if (!stage_layer_input<NT>(p, epoch, sh, st, li)) return false;
+    if (!select_layer<NT, TK>(p, epoch, sh, st, li, slot)) return false;
+    FW_TRACE_MARK(slot, 2);
+    const int U = uniform(sh.nunion);
+    const int fp0 = p.nb_rows * kPairsPerTask + j * p.cpairs;  // flattened (slot, pair) index
+    const int bs = fp0 / I;                                      // both pairs are in this slot
+    const int pr = fp0 - bs * I + (g >> 1);
+    // row r (= lane group) of the pairs: gate of pair r / 2 for even r, up for odd
+    auto brel = [&](int r) { return ((r & 1) ? I : 0) + (r >> 1); };
+    const uint16_t* bbase = L.gate_up + ((size_t)uniform(sh.sorted[bs]) * 2 * I + (fp0 - bs * I)) * H;
+    uint64_t* brows = reinterpret_cast<uint64_t*>(sh.xs + kBRowsAt);  // [4][H / 4]
+    if (w == 0) {
+        // 1 KB per wave instruction (16 bytes per lane)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            for (int c0 = 0; c0 < H / 512; ++c0) {
+                __builtin_amdgcn_global_load_lds(
+                    reinterpret_cast<const void*>(bbase + (size_t)brel(r) * H + c0 * 512 + 8 * lane),
+                    (__attribute__((address_space(3))) void*)(brows + r * (H / 4) + c0 * 128), 16, 0, 0);
+            }
+        }
+    }
+#pragma unroll
+    for (int k = 0; k < 3; ++k) {
+        const int m = w + 4 * k;
+        if (m >= 1 && m <= U) {
+            const uint16_t* wm = L.down + (size_t)uniform(sh.sorted[m - 1]) * (size_t)H * I;
+            line_issue(c[k], wm + (size_t)r0 * I, (uint32_t)(g * I * 2), q);
+        }
+    }
+    // route weights and the shared-gate sigmoid (exponentials above the block
+    // input); task 0 also reports the layer's ids, scores and sigmoid and
+    // rejects a NaN logit (src/decoder_layer.rs:279-281)
+    const int tid = threadIdx.x;
+    if (j == 0 && p.order == 0) {
+        int nan = 0;
+        for (int e = tid; e < p.ls; e += kThreads) nan |= (e < p.E) && ((sh.lg[e] & 0x7fffu) > 0x7f80u);
+        if (__syncthreads_or(nan) && tid == 0) atomicCAS(p.error, 0, 2);
+    }
+#ifdef FW_DECODE_TRACE
+    if (w != 0) {
+        // profiling: when this wave's down rows have arrived
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        FW_TRACE_MARK(slot, 9);
+    }
+#endif
+    // wave 1 scores while the lead wave runs the pairs (the publish below
+    // synchronises both before anything reads the scores)
+    score_experts<NT>(p, li, sh, j == 0, kMaxHidden, 1, false);
+    st.scored = li;
+    // lead wave: the two pairs' dots and SwiGLU (src/expert.rs:514-571) once
+    // its copies into LDS have landed; lane 0 stores the word of both
+    // activations
+    if (w == 0) {
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        float acc[1][2];
+        line_chains_lds<MBH, 2>(brows + g * (H / 4), H / 32, sh.xs, q, acc);
+        float d = tree32_reduce_lines(acc[0][0], acc[0][1]);
+        if (q == 0) d = tree32_finish(d, bbase + (size_t)brel(g) * H, sh.xs, H);
+        const uint32_t bits = to_bf16(d);
+        const uint32_t up = (uint32_t)__shfl((int)bits, (lane + kLanesPerRow) & 63, kWave);
+        const uint32_t a = swiglu_bf16(bits, up, sh.exp2tab);
+        const uint32_t a1 = (uint32_t)__shfl((int)a, (lane + 2 * kLanesPerRow) & 63, kWave);
+        if (lane == 0)
+            coherent_store64(p.act + (size_t)(li * p.S + bs) * (I / 2) + pr / 2, tagged(a | (a1 << 16), epoch));
+    }
+    publish(phase_counters(p, li, kCntGateUp), p.n_gu, p.n_shared + p.nb_rows + j, phase_flags(p, li, kCntGateUp),
+            epoch);
+    FW_TRACE_MARK(slot, 5);
+    // the residual words this task updates: one lane of the lead wave per row
+    const int rt = w * kWave + lane;
+    const bool mixer = rt < kRowsPerCTask;
+    const size_t at = ((size_t)r0 + (rt & ~1)) / 2;
+    bool ok = true;
+    uint32_t rin = 0;
+    if (mixer) {
+        if (li == 0) {
+            rin = reinterpret_cast<const uint32_t*>(p.x_in)[at];
+        } else {
+            uint64_t v[1];
+            ok = load_tagged<1, 1>(v, p.xw + (size_t)li * H / 2 + at, 1, epoch, p.error, p.limit_ticks);
+            rin = (uint32_t)v[0];
+        }
+    }
+    FW_TRACE_MARK(slot, 3);
+    if (!wait_phase(phase_flags(p, li, kCntGateUp), epoch, p.error, p.limit_ticks, &sh.flag)) return false;
+    FW_TRACE_STAMP(t1);
+    // every activation vector of the task at once (matrices 0..U <= 11)
+    st.loaded = st.staged = -1;
+    if (!stage_acts_direct<MBI>(p, li, epoch, sh, U)) return false;
+    FW_TRACE_MARK(slot, 4);
+    // payloads: the low halves of the tagged words
+    const uint32_t* act_lds = reinterpret_cast<const uint32_t*>(sh.xs);
+    const int act_stride = 2 * (max(I, Is) / 2);
+#pragma unroll
+    for (int k = 0; k < 3; ++k) {
+        const int m = w + 4 * k;
+        if (m <= U) {
+            const uint32_t bits = down_row_lds<MBI, 2>(c[k], (m == 0 ? Is : I) / 32, act_lds + m * act_stride, q);
+            if (q == 0) sh.res[m * kRowsPerCTask + g] = bits;
+        }
+    }
+    FW_TRACE_MARK(slot, 0);
+    if (!__syncthreads_and(ok)) return false;
+    if (mixer) {
+        const int gg = rt;
+        // src/decoder_layer.rs:528-545: weighted = bf16(down * score), summed in
+        // ascending expert order from bf16 zero, rounding after each add
+        uint32_t mix = to_bf16(0.0f);
+        for (int k0 = 0; k0 < K; k0 += 8) {
+            uint32_t d[8], wt[8];
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                if (k0 + i < K) {
+                    d[i] = sh.res[(1 + sh.tslot[k0 + i]) * kRowsPerCTask + gg];
+                    wt[i] = sh.tweight[k0 + i];
+                }
+            }
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                if (k0 + i < K) mix = add_bf16(mix, to_bf16(mul_rn(from_bf16(d[i]), from_bf16(wt[i]))));
+            }
+        }
+        // src/decoder_layer.rs:563-575: gated = bf16(shared_down * sigmoid)
+        const uint32_t sd = sh.res[gg];
+        const uint32_t gated = to_bf16(mul_rn(from_bf16(sd), from_bf16(sh.sig[0])));
+        const uint32_t o = add_bf16(mix, gated);
+        const uint32_t xn = add_bf16((rin >> (16 * (gg & 1))) & 0xffffu, o);
+        const uint32_t o_odd = (uint32_t)__shfl_xor((int)o, 1, kWave);
+        const uint32_t x_odd = (uint32_t)__shfl_xor((int)xn, 1, kWave);
+        if ((gg & 1) == 0) {
+            const uint32_t o2 = o | (o_odd << 16), x2 = xn | (x_odd << 16);
+            reinterpret_cast<uint32_t*>(p.out + (size_t)li * H)[at] = o2;
+            coherent_store64(p.xw + (size_t)(li + 1) * H / 2 + at, tagged(x2, epoch));
+            if (li + 1 == p.nlayers && p.x_final != nullptr) reinterpret_cast<uint32_t*>(p.x_final)[at] = x2;
+        }
+    }
+    if (!__syncthreads_and(ok)) return false;
+    FW_TRACE_MARK(slot, 1);
+    publish(phase_counters(p, li, kCntC), p.n_c, j, phase_flags(p, li, kCntC), epoch);
     FW_TRACE_STAMP(t2);
     FW_TRACE_WRITE(slot, kTaskDown, t0, t1, t2);
     return true;
@@ -1037,7 +1244,7 @@ __device__ __forceinline__ bool combine_task(const DecodeParams& p, uint32_t epo
 // ---- roles -----------------------------------------------------------------------------
 //
 // Per layer the rows role runs the R, S and the first nb_rows B tasks; the
-// combine role runs the Z task, the remaining B tasks, then the C tasks. Both
+// combine role runs the remaining B tasks, then the C tasks. Both
 // walk their list in (layer, phase) order, task t on workgroup t mod (role
 // size).
 
@@ -1067,20 +1274,21 @@ template <int NT, int MBH, int MBI, int TK, class SH>
 __device__ __forceinline__ void combine_role(const DecodeParams* __restrict__ P, uint32_t epoch, SH& sh,
                                              int rank) {
     const DecodeParams& p = *P;
-    const int nb_comb = p.n_b - p.nb_rows;
-    const int per = 1 + nb_comb + p.n_c;
+    const int nb_comb = p.cpairs > 0 ? 0 : p.n_b - p.nb_rows;
+    const int per = nb_comb + p.n_c;
     const int total = p.nlayers * per;
     LdsState st;
     for (int t = rank; t < total; t += p.g_comb) {
         const int li = t / per;
         const int j = t - li * per;
         bool ok;
-        if (j == 0) {
-            ok = select_task<NT, TK>(p, epoch, sh, st, li);
-        } else if (j <= nb_comb) {
-            ok = pairs_task<NT, MBH, TK>(p, epoch, sh, st, li, p.nb_rows + j - 1, false);
+        if constexpr (fused_combine(NT, MBH, MBI)) {
+            // the host runs one-token steps it cannot fuse on the two-token kernel
+            ok = combine_task_fused<NT, MBH, MBI, TK>(p, epoch, sh, st, li, j);
+        } else if (j < nb_comb) {
+            ok = pairs_task<NT, MBH, TK>(p, epoch, sh, st, li, p.nb_rows + j, false);
         } else {
-            ok = combine_task<NT, MBI, TK>(p, epoch, sh, st, li, j - 1 - nb_comb);
+            ok = combine_task<NT, MBI, TK>(p, epoch, sh, st, li, j - nb_comb);
         }
         if (!ok) return;
     }
@@ -1101,17 +1309,14 @@ k_moe_decode(const DecodeParams* __restrict__ P, uint32_t epoch) {
     } else if (b < P->g_rows + P->g_comb) {
         combine_role<NT, MBH, MBI, TK>(P, epoch, sh, b - P->g_rows);
     }
-    // The last workgroup out zeroes every counter for the next launch.
+    // Completed counters zero themselves. After a failure some are left
+    // partly counted: the last workgroup out then zeroes them all.
     __syncthreads();
     if (threadIdx.x == 0) {
-        __threadfence();
-        uint32_t* done = P->counters + (size_t)P->nlayers * kCountersPerLayer;
-        uint32_t prev = __hip_atomic_fetch_add(done, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
-        if (prev == (uint32_t)G - 1u) {
-            for (int i = 0; i < P->nlayers * kCountersPerLayer; ++i) {
+        uint32_t* done = P->counters + (size_t)P->nlayers * kCountersPerLayer * kCounterGroupWords;
+        if (count_task(done, G, b) && coherent_load(P->error) != 0) {
+            for (int i = 0; i < P->nlayers * kCountersPerLayer * kCounterGroupWords; i += kCounterStride)
                 __hip_atomic_store(P->counters + i, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            }
-            __hip_atomic_store(done, 0u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
         }
     }
 }

@@ -25,8 +25,19 @@ constexpr int kWave = 64;
 constexpr int kLanesPerRow = 16;
 constexpr int kRowsPerWave = kWave / kLanesPerRow;  // 4
 
-__device__ __forceinline__ int lane_id() { return (int)(threadIdx.x & (kWave - 1)); }
-__device__ __forceinline__ int wave_id() { return __builtin_amdgcn_readfirstlane((int)(threadIdx.x / kWave)); }
+// Lane and wave indices, opaque to loop-invariant code motion: what a task
+// derives from them is recomputed in the task instead of being hoisted out of
+// the persistent task loop and held in registers for its whole length.
+__device__ __forceinline__ int lane_id() {
+    int t = (int)threadIdx.x;
+    asm volatile("" : "+v"(t));
+    return t & (kWave - 1);
+}
+__device__ __forceinline__ int wave_id() {
+    int w = __builtin_amdgcn_readfirstlane((int)(threadIdx.x / kWave));
+    asm volatile("" : "+s"(w));
+    return w;
+}
 
 // DPP controls (GFX9 encoding).
 constexpr int kDppRowShl1 = 0x101, kDppRowShl2 = 0x102, kDppRowShl4 = 0x104, kDppRowShl8 = 0x108;
@@ -244,21 +255,30 @@ struct LineShare {
     uint64_t w[(MAXB + 1) / 2];
 };
 
-// Issue the loads of a row's line share: nblocks <= MAXB blocks (nblocks may
-// be odd: the last line is then half a line, and lanes 8..15 read the first
-// half again instead of the bytes past the row). Slots past the row repeat the
-// last line; the sweep skips them.
+// A pointer that is the same in every lane, as a scalar pair.
+__device__ __forceinline__ const char* uniform_ptr(const void* p) {
+    const uint64_t v = reinterpret_cast<uint64_t>(p);
+    const uint32_t lo = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)v);
+    const uint32_t hi = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(v >> 32));
+    return reinterpret_cast<const char*>(((uint64_t)hi << 32) | lo);
+}
+
+// Issue the loads of a row's line share: all (MAXB + 1) / 2 lines from the
+// row start, whatever the row's length (the sweeps skip blocks past the row),
+// so the allocation must extend kLineSharePad bytes past any row start. The
+// row is given as a base shared by the wave plus this lane's byte offset to
+// its row (below 4 GiB): every load then addresses the scalar base, one 32-bit
+// offset register and an immediate.
+constexpr int kLineSharePad = 80 * 64;  // the widest variant's line share
 template <int MAXB>
-__device__ __forceinline__ void line_issue(LineShare<MAXB>& r, const uint16_t* row, int nblocks, int q) {
-    const auto* g = as_global(reinterpret_cast<const uint64_t*>(row)) + q;
-    const int last = opaque((nblocks - 1) / 2);
-    // lanes 8..15 of an odd row's last line step back to its first half
-    const int back = ((nblocks & 1) && q >= 8) ? 8 : 0;
+__device__ __forceinline__ void line_issue(LineShare<MAXB>& r, const uint16_t* base, uint32_t row_bytes, int q) {
+    static_assert((MAXB + 1) / 2 * 128 <= kLineSharePad, "allocation padding");
+    const auto* b = as_global(uniform_ptr(base));
+    const uint32_t off = row_bytes + 8u * (uint32_t)q;
 #pragma unroll
-    for (int v = 0; v < (MAXB + 1) / 2; ++v) {
-        const int line = v < last ? v : last;
-        r.w[v] = __builtin_nontemporal_load(g + line * 16 - (line == last ? back : 0));
-    }
+    for (int v = 0; v < (MAXB + 1) / 2; ++v)
+        r.w[v] = __builtin_nontemporal_load(
+            reinterpret_cast<const __attribute__((address_space(1))) uint64_t*>(b + off + 128 * v));
 }
 
 // The two blocks of line v as this lane's chain pairs (first: block 2v,
@@ -274,38 +294,149 @@ __device__ __forceinline__ void line_pairs(uint64_t word, int q, uint32_t& first
 // Column offset of this lane's chain pair within a block.
 __device__ __forceinline__ int line_column(int q) { return 4 * (q & 7) + 2 * (q >> 3); }
 
-// Chains of one row for NT tokens against f32 vectors in LDS (stride xstride);
-// nblocks is uniform. Every token is computed.
-template <int NT, int MAXB>
-__device__ __forceinline__ void line_chains(const LineShare<MAXB>& r, int nblocks, const float* __restrict__ xs,
-                                            int xstride, int q, float (&acc)[NT][2]) {
+// The pipelined sweep of line_chains (NT <= 2), G lines per group.
+template <int NT, int MAXB, int G>
+__device__ __forceinline__ void line_sweep(const LineShare<MAXB>& r, int nblocks, const float* __restrict__ xq,
+                                           int xstride, int q, float (&acc)[NT][2]) {
+    constexpr int NL = (MAXB + 1) / 2;  // lines
+    float2 xv[2][NT][2 * G];
 #pragma unroll
-    for (int t = 0; t < NT; ++t) acc[t][0] = acc[t][1] = 0.0f;
-    nblocks = opaque(nblocks);
-    const float* xq = xs + line_column(q);
+    for (int i = 0; i < G && i < NL; ++i) {
 #pragma unroll
-    for (int v0 = 0; v0 < (MAXB + 1) / 2; v0 += 4) {
+        for (int t = 0; t < NT; ++t) {
+            xv[0][t][2 * i] = *reinterpret_cast<const float2*>(xq + t * xstride + 64 * i);
+            xv[0][t][2 * i + 1] = *reinterpret_cast<const float2*>(xq + t * xstride + 64 * i + 32);
+        }
+    }
 #pragma unroll
-        for (int v = v0; v < v0 + 4 && v < (MAXB + 1) / 2; ++v) {
+    for (int v0 = 0, buf = 0; v0 < NL; v0 += G, buf ^= 1) {
+        if (v0 + G < NL) {
+#pragma unroll
+            for (int i = 0; i < G && v0 + G + i < NL; ++i) {
+#pragma unroll
+                for (int t = 0; t < NT; ++t) {
+                    const float* xa = xq + t * xstride + 64 * (v0 + G + i);
+                    xv[buf ^ 1][t][2 * i] = *reinterpret_cast<const float2*>(xa);
+                    xv[buf ^ 1][t][2 * i + 1] = *reinterpret_cast<const float2*>(xa + 32);
+                }
+            }
+        }
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int i = 0; i < G && v0 + i < NL; ++i) {
+            const int v = v0 + i;
             uint32_t first, second;
             line_pairs(r.w[v], q, first, second);
             if (2 * v < nblocks) {
                 const float w0 = bf16_lo(first), w1 = bf16_hi(first);
 #pragma unroll
                 for (int t = 0; t < NT; ++t) {
-                    const float2 xv = *reinterpret_cast<const float2*>(xq + t * xstride + 64 * v);
-                    acc[t][0] = add_rn(acc[t][0], mul_rn(w0, xv.x));
-                    acc[t][1] = add_rn(acc[t][1], mul_rn(w1, xv.y));
+                    acc[t][0] = add_rn(acc[t][0], mul_rn(w0, xv[buf][t][2 * i].x));
+                    acc[t][1] = add_rn(acc[t][1], mul_rn(w1, xv[buf][t][2 * i].y));
                 }
             }
             if (2 * v + 1 < nblocks) {
                 const float w0 = bf16_lo(second), w1 = bf16_hi(second);
 #pragma unroll
                 for (int t = 0; t < NT; ++t) {
-                    const float2 xv = *reinterpret_cast<const float2*>(xq + t * xstride + 64 * v + 32);
-                    acc[t][0] = add_rn(acc[t][0], mul_rn(w0, xv.x));
-                    acc[t][1] = add_rn(acc[t][1], mul_rn(w1, xv.y));
+                    acc[t][0] = add_rn(acc[t][0], mul_rn(w0, xv[buf][t][2 * i + 1].x));
+                    acc[t][1] = add_rn(acc[t][1], mul_rn(w1, xv[buf][t][2 * i + 1].y));
                 }
+            }
+        }
+        __builtin_amdgcn_sched_barrier(0);
+    }
+}
+
+// Chains of one row for NT tokens against f32 vectors in LDS (stride xstride);
+// nblocks is uniform. Every token is computed. The vector values of the next
+// group of G lines are read from LDS while the current group is computed (G
+// = 0: 4 lines for one token, 2 for two; fewer registers with a smaller G).
+template <int NT, int MAXB, int G = 0>
+__device__ __forceinline__ void line_chains(const LineShare<MAXB>& r, int nblocks, const float* __restrict__ xs,
+                                            int xstride, int q, float (&acc)[NT][2]) {
+    constexpr int NL = (MAXB + 1) / 2;  // lines
+#pragma unroll
+    for (int t = 0; t < NT; ++t) acc[t][0] = acc[t][1] = 0.0f;
+    nblocks = opaque(nblocks);
+    const float* xq = xs + line_column(q);
+    if constexpr (NT > 2) {
+        // no registers to spare for a second group: read as used
+#pragma unroll
+        for (int v0 = 0; v0 < NL; v0 += 4) {
+#pragma unroll
+            for (int v = v0; v < v0 + 4 && v < NL; ++v) {
+                uint32_t first, second;
+                line_pairs(r.w[v], q, first, second);
+                if (2 * v < nblocks) {
+                    const float w0 = bf16_lo(first), w1 = bf16_hi(first);
+#pragma unroll
+                    for (int t = 0; t < NT; ++t) {
+                        const float2 x2 = *reinterpret_cast<const float2*>(xq + t * xstride + 64 * v);
+                        acc[t][0] = add_rn(acc[t][0], mul_rn(w0, x2.x));
+                        acc[t][1] = add_rn(acc[t][1], mul_rn(w1, x2.y));
+                    }
+                }
+                if (2 * v + 1 < nblocks) {
+                    const float w0 = bf16_lo(second), w1 = bf16_hi(second);
+#pragma unroll
+                    for (int t = 0; t < NT; ++t) {
+                        const float2 x2 = *reinterpret_cast<const float2*>(xq + t * xstride + 64 * v + 32);
+                        acc[t][0] = add_rn(acc[t][0], mul_rn(w0, x2.x));
+                        acc[t][1] = add_rn(acc[t][1], mul_rn(w1, x2.y));
+                    }
+                }
+            }
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        return;
+    }
+    line_sweep<NT, MAXB, G != 0 ? G : (NT == 1 ? 4 : 2)>(r, nblocks, xq, xstride, q, acc);
+}
+
+// line_chains for one token with the row's line words in LDS (wrow: the row's
+// first word; line v is words 16 v .. 16 v + 15, this lane's is 16 v + q):
+// the weights and vector values of the next G lines are read while the
+// current group is computed.
+template <int MAXB, int G>
+__device__ __forceinline__ void line_chains_lds(const uint64_t* wrow, int nblocks, const float* __restrict__ xs, int q,
+                                                float (&acc)[1][2]) {
+    constexpr int NL = (MAXB + 1) / 2;
+    acc[0][0] = acc[0][1] = 0.0f;
+    nblocks = opaque(nblocks);
+    const uint64_t* wq = wrow + q;
+    const float* xq = xs + line_column(q);
+    uint64_t wv[2][G];
+    float2 xv[2][2 * G];
+#pragma unroll
+    for (int i = 0; i < G && i < NL; ++i) {
+        wv[0][i] = wq[16 * i];
+        xv[0][2 * i] = *reinterpret_cast<const float2*>(xq + 64 * i);
+        xv[0][2 * i + 1] = *reinterpret_cast<const float2*>(xq + 64 * i + 32);
+    }
+#pragma unroll
+    for (int v0 = 0, buf = 0; v0 < NL; v0 += G, buf ^= 1) {
+        if (v0 + G < NL) {
+#pragma unroll
+            for (int i = 0; i < G && v0 + G + i < NL; ++i) {
+                wv[buf ^ 1][i] = wq[16 * (v0 + G + i)];
+                xv[buf ^ 1][2 * i] = *reinterpret_cast<const float2*>(xq + 64 * (v0 + G + i));
+                xv[buf ^ 1][2 * i + 1] = *reinterpret_cast<const float2*>(xq + 64 * (v0 + G + i) + 32);
+            }
+        }
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int i = 0; i < G && v0 + i < NL; ++i) {
+            const int v = v0 + i;
+            uint32_t first, second;
+            line_pairs(wv[buf][i], q, first, second);
+            if (2 * v < nblocks) {
+                acc[0][0] = add_rn(acc[0][0], mul_rn(bf16_lo(first), xv[buf][2 * i].x));
+                acc[0][1] = add_rn(acc[0][1], mul_rn(bf16_hi(first), xv[buf][2 * i].y));
+            }
+            if (2 * v + 1 < nblocks) {
+                acc[0][0] = add_rn(acc[0][0], mul_rn(bf16_lo(second), xv[buf][2 * i + 1].x));
+                acc[0][1] = add_rn(acc[0][1], mul_rn(bf16_hi(second), xv[buf][2 * i + 1].y));
             }
         }
         __builtin_amdgcn_sched_barrier(0);
@@ -416,26 +547,45 @@ __device__ __forceinline__ void wave_topk(const uint16_t* __restrict__ logits, i
 //   the same small vector mostly hit their XCD's L2 instead of queueing on
 //   the few memory channels that hold it, and re-read with agent-scope loads
 //   (past the caches) only the words whose tag is not the current epoch.
-// * Each phase of each layer has a counter that every task of the phase
-//   increments once, right after issuing its stores (no wait for their
-//   acknowledgement: readers check the tags). The task that completes the
-//   count writes the epoch into kFlagCopies flag words; a waiter polls the
-//   copy for its workgroup, so no single word is polled by more than a few
-//   dozen workgroups.
+// * Each phase of each layer has a counter group that every task of the
+//   phase increments once, right after issuing its stores (no wait for their
+//   acknowledgement: readers check the tags). Atomics on one word are
+//   serialised at the coherence point (about 12 ns each: a thousand
+//   simultaneous arrivals on one counter take 12 us), so task j increments
+//   sub-counter j mod kSubCounters, and the task completing a sub-counter
+//   increments the group's top counter. The task completing the top counter
+//   writes the epoch into kFlagCopies flag words; a waiter polls the copy for
+//   its workgroup, so no single word is polled by more than a few dozen
+//   workgroups. The completing task of each counter zeroes it for the next
+//   launch (nothing else touches it in this launch).
 
 constexpr int kFlagCopies = 64;
 constexpr int kFlagStride = 64;  // words between copies (256 bytes: different memory channels)
+constexpr int kSubCounters = 32;
+constexpr int kCounterStride = 64;  // words between counters of a group
+constexpr int kCounterGroupWords = (1 + kSubCounters) * kCounterStride;  // top, then the sub-counters
 
-// Announce a finished task of a phase of `target` tasks. Every wave has issued
-// its tagged stores (program order up to the barrier).
-__device__ __forceinline__ void publish(uint32_t* counter, uint32_t target, uint32_t* flags, uint32_t epoch) {
+// Task j of a phase of n tasks counts itself in `group`; returns true in the
+// task that completes the phase (thread 0 only).
+__device__ __forceinline__ bool count_task(uint32_t* group, int n, int j) {
+    const int sub = j % kSubCounters;
+    const uint32_t sub_target = (uint32_t)((n - sub + kSubCounters - 1) / kSubCounters);
+    const uint32_t top_target = (uint32_t)(n < kSubCounters ? n : kSubCounters);
+    auto* sc = as_global_rw(group + (1 + sub) * kCounterStride);
+    if (__hip_atomic_fetch_add(sc, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + 1u != sub_target) return false;
+    __hip_atomic_store(sc, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    auto* top = as_global_rw(group);
+    if (__hip_atomic_fetch_add(top, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + 1u != top_target) return false;
+    __hip_atomic_store(top, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    return true;
+}
+
+// Announce finished task j of a phase of n tasks. Every wave has issued its
+// tagged stores (program order up to the barrier).
+__device__ __forceinline__ void publish(uint32_t* group, int n, int j, uint32_t* flags, uint32_t epoch) {
     __syncthreads();
-    if (threadIdx.x == 0) {
-        const uint32_t before =
-            __hip_atomic_fetch_add(as_global_rw(counter), 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        if (before + 1u == target) {
-            for (int i = 0; i < kFlagCopies; ++i) coherent_store(flags + i * kFlagStride, epoch);
-        }
+    if (threadIdx.x == 0 && count_task(group, n, j)) {
+        for (int i = 0; i < kFlagCopies; ++i) coherent_store(flags + i * kFlagStride, epoch);
     }
 }
 
@@ -476,10 +626,11 @@ __device__ __forceinline__ bool wait_phase(const uint32_t* flags, uint32_t epoch
 // alone). The first read goes through the caches; words that do not carry
 // `epoch` (a stale cached line, or a store still in flight) are read again past
 // the caches until they do, bounded by the wall-clock limit and the shared
-// error word. Per lane; false on timeout or error.
+// error word. Per lane; false on timeout or error. With `stale`, the number
+// of words the first read found without the epoch.
 template <int N, int STRIDE>
 __device__ __forceinline__ bool load_tagged(uint64_t (&v)[N], const uint64_t* base, int n, uint32_t epoch,
-                                            int32_t* error, uint64_t limit_ticks) {
+                                            int32_t* error, uint64_t limit_ticks, int* stale = nullptr) {
     const auto* g = as_global(base);
 #pragma unroll
     for (int k = 0; k < N; ++k) {
@@ -488,6 +639,12 @@ __device__ __forceinline__ bool load_tagged(uint64_t (&v)[N], const uint64_t* ba
     bool ok = true;
 #pragma unroll
     for (int k = 0; k < N; ++k) ok = ok && (k >= n || has_tag(v[k], epoch));
+    if (stale != nullptr) {
+        int c = 0;
+#pragma unroll
+        for (int k = 0; k < N; ++k) c += (k < n && !has_tag(v[k], epoch)) ? 1 : 0;
+        *stale = c;
+    }
     if (ok) return true;
     const uint64_t start = wall_clock64();
     while (true) {

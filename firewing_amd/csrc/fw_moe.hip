@@ -316,7 +316,7 @@ struct firewing_hip_context {
     uint16_t* xfinal = nullptr;  // [T][H] residual after the last layer
     uint16_t *out = nullptr, *scores = nullptr, *sig = nullptr;
     int32_t* ids = nullptr;
-    uint64_t *xw = nullptr, *logits = nullptr, *shared_act = nullptr, *act = nullptr, *selrec = nullptr;  // tagged words
+    uint64_t *xw = nullptr, *logits = nullptr, *shared_act = nullptr, *act = nullptr;  // tagged words
     uint32_t* counters = nullptr;
     uint32_t* flags = nullptr;  // phase flags (epoch of the completed phase)
     int32_t* error = nullptr;
@@ -418,7 +418,6 @@ void launch_decode(firewing_hip_context* c, size_t first, size_t n, int T, int o
     p.gi = p.ls - 2;
     p.shared_act = c->shared_act;
     p.act = c->act;
-    p.selrec = c->selrec;
     p.x_final = x_final;
     p.out = c->out;
     p.ids = c->ids;
@@ -438,13 +437,36 @@ void launch_decode(firewing_hip_context* c, size_t first, size_t n, int T, int o
     // Roles: the combine role gets one workgroup per C task of a layer where
     // the grid allows (so every task's down rows are in flight before the
     // gate/up phase ends), at most half of the grid. The rows role takes one
-    // B task per workgroup and layer; B tasks beyond that go to the combine
-    // role, ahead of its C tasks, instead of a second round on the rows role.
-    const int grid = c->grid[T];
-    p.g_comb = std::min(p.n_c, grid / 2);
-    p.g_rows = grid - p.g_comb;
-    p.nb_rows = std::min(p.n_b, p.g_rows);
-    if (p.g_comb < 1 || p.g_rows < 1) throw HipError{"decode grid too small for its roles"};
+    // B task per workgroup and layer. B tasks beyond that: with one token, when
+    // they come to two gate/up pairs per C task, wave 0 of each C task computes
+    // them (the one-token kernel, which requires this: every C task of a layer
+    // is resident at once and publishes its pairs before waiting for the
+    // phase); otherwise they go to the combine role ahead of its C tasks (the
+    // kernels for two or more tokens, which also run one-token steps that
+    // cannot be fused).
+    auto roles = [&](int kt) {
+        const int grid = c->grid[kt];
+        p.g_comb = std::min(p.n_c, grid / 2);
+        p.g_rows = grid - p.g_comb;
+        p.nb_rows = std::min(p.n_b, p.g_rows);
+        if (p.g_comb < 1 || p.g_rows < 1) throw HipError{"decode grid too small for its roles"};
+    };
+    int kt = T;  // token count of the kernel variant
+    p.cpairs = 0;
+    if (T == 1) {
+        roles(1);
+        const int mbh = sh.hidden > 2048 ? 80 : 64;
+        const int mbi = std::max(sh.intermediate, sh.shared_intermediate) > 512 ? 32 : 16;
+        if (fused_combine(1, mbh, mbi) && p.g_comb == p.n_c && K + 1 <= kDirectVectors && I % 256 == 0 &&
+            Is % 256 == 0 && H % 512 == 0 &&
+            (long)S * (long)I - (long)p.nb_rows * kPairsPerTask == 2L * p.n_c)
+            p.cpairs = 2;
+        else
+            kt = 2;
+    }
+    if (kt != 1) roles(kt);
+    p.n_gu = p.n_shared + (p.cpairs > 0 ? p.nb_rows + p.n_c : p.n_b);
+    p.cu_count = c->cu_count;
     p.trace = c->trace;
     // The kernel reads its parameters from a device copy; upload only on change
     // (the copy is stream-ordered before the launch; pageable source, staged).
@@ -458,8 +480,8 @@ void launch_decode(firewing_hip_context* c, size_t first, size_t n, int T, int o
     c->epoch = c->epoch + 1 == 0 ? 1 : c->epoch + 1;
     uint32_t epoch = c->epoch;
     void* args[] = {&dp, &epoch};
-    const void* fn = decode_kernel(c, T);
-    check(hipLaunchCooperativeKernel(fn, dim3(grid), dim3(256), args, 0, s),
+    const void* fn = decode_kernel(c, kt);
+    check(hipLaunchCooperativeKernel(fn, dim3(c->grid[kt]), dim3(256), args, 0, s),
           "hipLaunchCooperativeKernel(k_moe_decode)");
 }
 
@@ -724,12 +746,14 @@ bool firewing_hip_create(const firewing_hip_shape* shape, firewing_hip_context**
         c->shared_down.assign(L, nullptr);
         std::vector<DecodeLayer> layers(L);
         for (size_t l = 0; l < L; ++l) {
-            c->router[l] = dalloc<uint16_t>((E + 1) * H);
-            c->gate_up[l] = dalloc<uint16_t>(E * 2 * I * H);
-            c->down[l] = dalloc<uint16_t>(E * H * I);
-            c->shared_gate[l] = dalloc<uint16_t>(Is * H);
-            c->shared_up[l] = dalloc<uint16_t>(Is * H);
-            c->shared_down[l] = dalloc<uint16_t>(H * Is);
+            c->router[l] = dalloc<uint16_t>((E + 1) * H + kLineSharePad / 2);
+            c->gate_up[l] = dalloc<uint16_t>(E * 2 * I * H + kLineSharePad / 2);
+            c->down[l] = dalloc<uint16_t>(E * H * I + kLineSharePad / 2);
+            // gate and up rows of the shared expert in one allocation (the
+            // decode kernel addresses both from shared_gate)
+            c->shared_gate[l] = dalloc<uint16_t>(2 * Is * H + kLineSharePad / 2);
+            c->shared_up[l] = c->shared_gate[l] + Is * H;
+            c->shared_down[l] = dalloc<uint16_t>(H * Is + kLineSharePad / 2);
             layers[l] = DecodeLayer{c->router[l], c->gate_up[l], c->down[l], c->shared_gate[l],
                                     c->shared_up[l], c->shared_down[l]};
         }
@@ -752,12 +776,10 @@ bool firewing_hip_create(const firewing_hip_shape* shape, firewing_hip_context**
         check(hipMemset(c->logits, 0, L * T * logit_stride((int)E) / 2 * 8), "hipMemset");
         check(hipMemset(c->shared_act, 0, L * T * Is / 2 * 8), "hipMemset");
         check(hipMemset(c->act, 0, L * S * T * I / 2 * 8), "hipMemset");
-        c->selrec = dalloc<uint64_t>(L * record_words((int)T, (int)K));
-        check(hipMemset(c->selrec, 0, L * record_words((int)T, (int)K) * 8), "hipMemset");
-        c->counters = dalloc<uint32_t>(L * kCountersPerLayer + 1);
+        c->counters = dalloc<uint32_t>((L * kCountersPerLayer + 1) * kCounterGroupWords);
         c->error = dalloc<int32_t>(1);
         c->d_params = dalloc<DecodeParams>(1);
-        check(hipMemset(c->counters, 0, (L * kCountersPerLayer + 1) * 4), "hipMemset counters");
+        check(hipMemset(c->counters, 0, (L * kCountersPerLayer + 1) * kCounterGroupWords * 4), "hipMemset counters");
         c->flags = dalloc<uint32_t>(L * kCountersPerLayer * kFlagCopies * kFlagStride);
         check(hipMemset(c->flags, 0, L * kCountersPerLayer * kFlagCopies * kFlagStride * 4), "hipMemset flags");
         check(hipMemset(c->error, 0, 4), "hipMemset error");
@@ -789,11 +811,11 @@ void firewing_hip_destroy(firewing_hip_context* c) {
     freev(c->router);
     freev(c->gate_up);
     freev(c->down);
+    c->shared_up.clear();  // inside the shared_gate allocations
     freev(c->shared_gate);
-    freev(c->shared_up);
     freev(c->shared_down);
     void* bufs[] = {c->d_layers, c->d_weight_table, c->xin, c->xfinal, c->out, c->ids, c->scores,
-                    c->sig, c->xw, c->logits, c->shared_act, c->act, c->selrec, c->counters, c->flags,
+                    c->sig, c->xw, c->logits, c->shared_act, c->act, c->counters, c->flags,
                     c->error, c->d_params};
     for (void* b : bufs)
         if (b) (void)hipFree(b);
@@ -1125,7 +1147,7 @@ extern "C" bool firewing_hip_debug_traced_step(firewing_hip_context* c, const ui
         const size_t L = c->shape.layers, H = c->shape.hidden;
         const size_t E = c->shape.experts, K = c->shape.top_k, I = c->shape.intermediate;
         const size_t Is = c->shape.shared_intermediate;
-        size_t per_layer = (E + 15) / 16 + 1 + (Is + 7) / 8 + K * tokens * (I / 8) + H / 4 + 1;
+        size_t per_layer = (E + 15) / 16 + 1 + (Is + 7) / 8 + K * tokens * (I / 8) + H / 4;
         size_t n = L * per_layer;
         if (cap < n * kTraceWords) return fail("trace buffer too small");
         c->trace = dalloc<uint64_t>(n * kTraceWords);
@@ -1147,6 +1169,15 @@ bool firewing_hip_synchronize(firewing_hip_context* c) {
     return guarded([&] {
         if (!c) return fail("synchronize: null context");
         return check_device_error(c, c->stream);
+    });
+}
+
+bool firewing_hip_set_wait_timeout(firewing_hip_context* c, double seconds) {
+    return guarded([&] {
+        if (!c) return fail("set_wait_timeout: null context");
+        if (!(seconds > 0.0 && seconds <= 600.0)) return fail("set_wait_timeout: seconds must be in (0, 600]");
+        c->timeout_seconds = seconds;
+        return true;
     });
 }
 

@@ -83,6 +83,7 @@ _SIGNATURES = {
     "firewing_hip_moe_step_dev": (_b, [_vp, _vp, _sz, ctypes.c_int, _b, _vp, _vp, _vp, _vp, _vp]),
     "firewing_hip_moe_step": (_b, [_vp, _u16p, _sz, ctypes.c_int, _b, _u16p, _u16p, _vp, _u16p]),
     "firewing_hip_synchronize": (_b, [_vp]),
+    "firewing_hip_set_wait_timeout": (_b, [_vp, ctypes.c_double]),
     "firewing_hip_synth_hidden": (None, [ctypes.c_uint64, ctypes.c_uint32, ctypes.c_uint32,
                                          ctypes.c_uint32, _b, _u16p]),
     "firewing_hip_expf_host": (None, [ctypes.POINTER(ctypes.c_float), ctypes.POINTER(ctypes.c_float), _sz]),
@@ -342,6 +343,10 @@ class MoeContext:
 
     def synchronize(self) -> None:
         _call("firewing_hip_synchronize", self._h)
+
+    def set_wait_timeout(self, seconds: float) -> None:
+        """Time limit of each dependency wait inside the persistent kernel."""
+        _call("firewing_hip_set_wait_timeout", self._h, float(seconds))
 
 
 def header_symbols() -> list[str]:

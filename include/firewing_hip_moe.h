@@ -184,6 +184,13 @@ bool firewing_hip_moe_step(firewing_hip_context* ctx, const uint16_t* hidden, si
  * (a persistent-kernel dependency wait that timed out). */
 bool firewing_hip_synchronize(firewing_hip_context* ctx);
 
+/* Time limit of each dependency wait inside the persistent kernel, in seconds
+ * (0 < seconds <= 600; default 10, or FIREWING_WAIT_TIMEOUT_S at create). A
+ * wait that exceeds it ends the launch with the timeout error; the next launch
+ * starts clean. No counterpart in the reference (the Metal path waits on
+ * command-buffer completion, src/metal_moe.rs:351-358). */
+bool firewing_hip_set_wait_timeout(firewing_hip_context* ctx, double seconds);
+
 /* Seeded synthetic hidden vectors of the benchmark workload (host memory):
  * bf16(N(0,1)) RMS-normalised, x[H-1] = 1.0 when bias_feature (the constant
  * feature that carries the Zipf router bias). No counterpart in the reference,

@@ -217,6 +217,33 @@ def test_step_tiny_chained(tiny_ctx):
     assert first_diff(resid, cur) is None
 
 
+def test_step_after_timed_out_launch(tiny_ctx):
+    # A wait limit of 10 ns makes the chained step's dependency waits time
+    # out (forced from the host; every workgroup still exits). The failed
+    # launch leaves phase counters partly counted; the next launch with the
+    # normal limit must still be exact.
+    rng = np.random.default_rng(12)
+    ws = [tiny_weights(rng) for _ in range(3)]
+    for l, w in enumerate(ws):
+        install(tiny_ctx, l, w)
+    x = rand_bf16(rng, TINY["hidden"]).reshape(1, -1)
+    tiny_ctx.set_wait_timeout(1e-8)
+    try:
+        with pytest.raises(hm.FirewingError, match="time limit"):
+            tiny_ctx.moe_step(x, bias_feature=False)
+    finally:
+        tiny_ctx.set_wait_timeout(10.0)
+    for _ in range(2):
+        resid, blocks, ids, _ = tiny_ctx.moe_step(x, bias_feature=False)
+        cur = x[0].copy()
+        for l, w in enumerate(ws):
+            ref = fo.sparse_moe_block(TINY, w, fo.rms_norm_bf16(cur))
+            assert list(ids[l, 0]) == list(ref["ids"])
+            assert first_diff(blocks[l, 0], ref["out"]) is None
+            cur = np.array([fo.add_bf16(int(a), int(b)) for a, b in zip(cur, ref["out"])], dtype=np.uint16)
+        assert first_diff(resid[0], cur) is None
+
+
 def test_block_rejects_bad_arguments(tiny_ctx):
     x = np.zeros((5, TINY["hidden"]), dtype=np.uint16)
     with pytest.raises(hm.FirewingError, match="tokens"):
