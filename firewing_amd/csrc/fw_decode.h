@@ -116,6 +116,11 @@ constexpr int kTraceWords = 18;  // start, dependency met, end, wg << 8 | kind, 
         if (threadIdx.x == 0 && p.trace != nullptr && (slot_) >= 0)                \
             p.trace[(size_t)(slot_) * kTraceWords + 4 + (k)] = wall_clock64();     \
     } while (0)
+#define FW_TRACE_MARK_IF(cond_, slot_, k)                                          \
+    do {                                                                           \
+        if ((cond_) && p.trace != nullptr && (slot_) >= 0)                         \
+            p.trace[(size_t)(slot_) * kTraceWords + 4 + (k)] = wall_clock64();     \
+    } while (0)
 #define FW_TRACE_VALUE(slot_, k, v)                                                \
     do {                                                                           \
         if (threadIdx.x == 0 && p.trace != nullptr && (slot_) >= 0)                \
@@ -136,6 +141,7 @@ constexpr int kTraceWords = 18;  // start, dependency met, end, wg << 8 | kind, 
 #else
 #define FW_TRACE_STAMP(var)
 #define FW_TRACE_MARK(slot_, k)
+#define FW_TRACE_MARK_IF(cond_, slot_, k)
 #define FW_TRACE_VALUE(slot_, k, v)
 #define FW_TRACE_WRITE(slot_, kind, a, b, c)
 #endif
@@ -198,6 +204,7 @@ struct DecodeShared {
     int32_t nvec;
     int32_t nunion;
     int32_t flag;
+    int32_t red[kThreads / 64];  // workgroup reductions (one word per wave)
     int32_t trace_stale;  // profiling builds: stale words of the last block-input read
 };
 
@@ -248,7 +255,7 @@ __device__ __forceinline__ bool load_input(const DecodeParams& p, int li, uint32
         ok = load_tagged<NT * kXWords, kThreads>(v, p.xw + (size_t)li * pairs + threadIdx.x, n, epoch, p.error,
                                                  p.limit_ticks, &stale);
 #ifdef FW_DECODE_TRACE
-        stale = __syncthreads_count(stale);
+        stale = wg_count(sh.red, stale);
         if (threadIdx.x == 0) sh.trace_stale = stale;
 #endif
         (void)stale;
@@ -259,7 +266,7 @@ __device__ __forceinline__ bool load_input(const DecodeParams& p, int li, uint32
             if (k < n) *reinterpret_cast<float2*>(xs + 2 * i) = make_float2(bf16_lo(w), bf16_hi(w));
         }
     }
-    return __syncthreads_and(ok) != 0;
+    return wg_all(sh.red, ok) != 0;
 }
 
 // In the chained step the block input is the pre-norm of the residual
@@ -298,7 +305,7 @@ __device__ __forceinline__ void normalise_input(const DecodeParams& p, SH& sh) {
         float ss = add_rn(add_rn(pair, __shfl_down(pair, 2, kWave)), 0.0f);
         if (lane == 0) sh.inv[w] = 1.0f / sqrtf(add_rn(ss / (float)n, 1e-6f));
     }
-    __syncthreads();
+    wg_sync();
     for (int t = 0; t < T; ++t) {
         const float inv = sh.inv[t];
         float* r = xs + t * n;
@@ -308,7 +315,7 @@ __device__ __forceinline__ void normalise_input(const DecodeParams& p, SH& sh) {
             r[i] = hv;
         }
     }
-    __syncthreads();
+    wg_sync();
 }
 
 // ---- expert selection ------------------------------------------------------------------
@@ -328,7 +335,7 @@ __device__ __forceinline__ bool load_logits(const DecodeParams& p, int li, uint3
     for (int k = 0; k < kWords; ++k) {
         if (k < n) lg2[threadIdx.x + k * kThreads] = (uint32_t)v[k];
     }
-    return __syncthreads_and(ok) != 0;
+    return wg_all(sh.red, ok) != 0;
 }
 
 // Top-k of every token (src/router.rs:241-247 total order) and the union of
@@ -345,7 +352,7 @@ __device__ __forceinline__ void select_experts(const DecodeParams& p, SH& sh, in
         wave_topk<TK>(sh.lg + w * LS, E, K, sh.ids + w * kMaxTopK);
     }
     FW_TRACE_MARK(slot_trace, 4);
-    __syncthreads();
+    wg_sync();
     FW_TRACE_MARK(slot_trace, 5);
     // The union, by wave 0 in registers: lane l holds entries l and l + 64 of
     // the T * K selections (entry i = token i / K, rank i % K); every loop
@@ -420,7 +427,7 @@ __device__ __forceinline__ void select_experts(const DecodeParams& p, SH& sh, in
         if (lane == 0) sh.nunion = nunion;
     }
     FW_TRACE_MARK(slot_trace, 6);
-    __syncthreads();
+    wg_sync();
 }
 
 // Scores of the selected experts (token t on the wave first_wave + t relative
@@ -443,9 +450,11 @@ __device__ __forceinline__ void score_experts(const DecodeParams& p, int li, SH&
 #pragma unroll
         for (int off = 32; off >= 1; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off, kWave));
         for (int e = lane; e < E; e += kWave) ew[e] = expf_glibc(add_rn(from_bf16(lt[e]), -mx), sh.exp2tab);
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+        // the exponentials are this wave's own: order its LDS writes before
+        // lane 0 reads them (no wait on the wave's memory loads)
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
         __builtin_amdgcn_wave_barrier();
-        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
         // one sequential sum in index order (lane 0, reading four values at a
         // time when the token's row is 16-byte aligned)
         float den = -0.0f;
@@ -489,7 +498,7 @@ __device__ __forceinline__ void score_experts(const DecodeParams& p, int li, SH&
             if (host_outputs) p.sig[(size_t)li * T + w] = sg;
         }
     }
-    if (barrier) __syncthreads();
+    if (barrier) wg_sync();
 }
 
 // ---- tasks ----------------------------------------------------------------------------
@@ -726,7 +735,7 @@ __device__ __forceinline__ bool stage_acts(const DecodeParams& p, int li, uint32
         }
         sh.nvec = n;
     }
-    __syncthreads();
+    wg_sync();
     if (mb == 0) FW_TRACE_MARK(slot, 7);
     const int nvec = uniform(sh.nvec);
     uint32_t* dst = reinterpret_cast<uint32_t*>(sh.xs);
@@ -763,7 +772,7 @@ __device__ __forceinline__ bool stage_acts(const DecodeParams& p, int li, uint32
                 for (int r = 0; r < kRound; ++r)
                     for (int c = 0; c < kChunks; ++c)
                         stale += (v0 + r < nvec && tid + c * kThreads < I / 2 && !has_tag(x[r][c], epoch)) ? 1 : 0;
-                const int total = __syncthreads_count(stale);
+                const int total = wg_count(sh.red, stale);
                 if (tid == 0 && p.trace != nullptr && slot >= 0) p.trace[(size_t)slot * kTraceWords + 4 + 6] = total;
             }
 #endif
@@ -803,7 +812,7 @@ __device__ __forceinline__ bool stage_acts(const DecodeParams& p, int li, uint32
             }
         }
     }
-    return __syncthreads_and(ok) != 0;
+    return wg_all(sh.red, ok) != 0;
 }
 
 // The sweep of down_row_lds (STRIDE: words between activation pairs, 2 for
@@ -859,7 +868,9 @@ __device__ __forceinline__ uint32_t down_row_lds(const LineShare<MAXB>& r, int n
 // word m * stride (stride = max(I, Is) / 2, a multiple of 128); then words
 // without the epoch are read again past the caches until they carry it.
 template <int MBI, class SH>
-__device__ __forceinline__ bool stage_acts_direct(const DecodeParams& p, int li, uint32_t epoch, SH& sh, int U) {
+__device__ __forceinline__ bool stage_acts_direct(const DecodeParams& p, int li, uint32_t epoch, SH& sh, int U,
+                                                  int slot = -1) {
+    (void)slot;
     const int I = p.I, Is = p.Is;
     const int stride = max(I, Is) / 2;
     const int parts = stride / 128;  // 1 KB parts: 64 lanes x 16 bytes
@@ -877,11 +888,18 @@ __device__ __forceinline__ bool stage_acts_direct(const DecodeParams& p, int li,
         }
     }
     __builtin_amdgcn_s_waitcnt(0);
-    __syncthreads();
+    // profiling: when each wave's loads have all landed
+    FW_TRACE_MARK_IF(lane == 0 && w == 0, slot, 7);
+    FW_TRACE_MARK_IF(lane == 0 && w == 1, slot, 8);
+    FW_TRACE_MARK_IF(lane == 0 && w == 2, slot, 9);
+    FW_TRACE_MARK_IF(lane == 0 && w == 3, slot, 3);
+    wg_sync();
     bool ok = true;
-    for (int i = threadIdx.x; i < (U + 1) * stride; i += kThreads) {
-        const int m = i / stride, wd = i - m * stride;
-        if (wd < (m == 0 ? Is / 2 : I / 2) && !has_tag(raw[i], epoch)) {
+    for (int m = 0; m <= U; ++m) {
+        const int len = m == 0 ? Is / 2 : I / 2;
+        for (int wd = threadIdx.x; wd < len; wd += kThreads) {
+            uint64_t* word = raw + (size_t)m * stride + wd;
+            if (has_tag(*word, epoch)) continue;
             const uint64_t* src = source(m) + wd;
             const uint64_t start = wall_clock64();
             uint64_t v;
@@ -894,10 +912,10 @@ __device__ __forceinline__ bool stage_acts_direct(const DecodeParams& p, int li,
                     break;
                 }
             }
-            raw[i] = v;
+            *word = v;
         }
     }
-    return __syncthreads_and(ok) != 0;
+    return wg_all(sh.red, ok) != 0;
 }
 
 // C task j of layer li: hidden rows 4j .. 4j + 3. Matrix m of the task: m = 0
@@ -960,7 +978,7 @@ __device__ __forceinline__ bool combine_task(const DecodeParams& p, uint32_t epo
     if (j == 0 && p.order == 0) {
         int nan = 0;
         for (int e = tid; e < T * p.ls; e += kThreads) nan |= (e % p.ls < p.E) && ((sh.lg[e] & 0x7fffu) > 0x7f80u);
-        if (__syncthreads_or(nan) && tid == 0) atomicCAS(p.error, 0, 2);
+        if (wg_any(sh.red, nan) && tid == 0) atomicCAS(p.error, 0, 2);
     }
     if (st.scored != li || j == 0) {
         score_experts<NT>(p, li, sh, j == 0);
@@ -1012,13 +1030,13 @@ __device__ __forceinline__ bool combine_task(const DecodeParams& p, uint32_t epo
             if (sb <= 8 && 8 < sb + SB) FW_DOWN_DOT(rs2, mb + w + 8);
             if (sb <= 12 && 12 < sb + SB) FW_DOWN_DOT(rs3, mb + w + 12);
             // the next staging overwrites these vectors
-            __syncthreads();
+            wg_sync();
         }
     }
 #undef FW_DOWN_DOT
 #undef FW_ISSUE_DOWN
     FW_TRACE_MARK(slot, 0);
-    if (!__syncthreads_and(ok)) return false;
+    if (!wg_all(sh.red, ok)) return false;
     if (mixer) {
         const int tt = mt, gg = mg;
         // src/decoder_layer.rs:528-545: weighted = bf16(down * score), summed in
@@ -1054,7 +1072,7 @@ __device__ __forceinline__ bool combine_task(const DecodeParams& p, uint32_t epo
             if (li + 1 == p.nlayers && p.x_final != nullptr) reinterpret_cast<uint32_t*>(p.x_final)[at] = x2;
         }
     }
-    if (!__syncthreads_and(ok)) return false;
+    if (!wg_all(sh.red, ok)) return false;
     FW_TRACE_MARK(slot, 1);
     publish(phase_counters(p, li, kCntC), p.n_c, j, phase_flags(p, li, kCntC), epoch);
     FW_TRACE_STAMP(t2);
@@ -1118,14 +1136,19 @@ __device__ __forceinline__ bool combine_task_fused(const DecodeParams& p, uint32
             }
         }
     }
+    // down rows (wave 1 scores first: it then has no loads in flight for the
+    // scoring code to wait on; its rows are needed only after the gate/up phase)
+    auto issue_down = [&]() {
 #pragma unroll
-    for (int k = 0; k < 3; ++k) {
-        const int m = w + 4 * k;
-        if (m >= 1 && m <= U) {
-            const uint16_t* wm = L.down + (size_t)uniform(sh.sorted[m - 1]) * (size_t)H * I;
-            line_issue(c[k], wm + (size_t)r0 * I, (uint32_t)(g * I * 2), q);
+        for (int k = 0; k < 3; ++k) {
+            const int m = w + 4 * k;
+            if (m >= 1 && m <= U) {
+                const uint16_t* wm = L.down + (size_t)uniform(sh.sorted[m - 1]) * (size_t)H * I;
+                line_issue(c[k], wm + (size_t)r0 * I, (uint32_t)(g * I * 2), q);
+            }
         }
-    }
+    };
+    if (w != 1) issue_down();
     // route weights and the shared-gate sigmoid (exponentials above the block
     // input); task 0 also reports the layer's ids, scores and sigmoid and
     // rejects a NaN logit (src/decoder_layer.rs:279-281)
@@ -1133,24 +1156,20 @@ __device__ __forceinline__ bool combine_task_fused(const DecodeParams& p, uint32
     if (j == 0 && p.order == 0) {
         int nan = 0;
         for (int e = tid; e < p.ls; e += kThreads) nan |= (e < p.E) && ((sh.lg[e] & 0x7fffu) > 0x7f80u);
-        if (__syncthreads_or(nan) && tid == 0) atomicCAS(p.error, 0, 2);
+        if (wg_any(sh.red, nan) && tid == 0) atomicCAS(p.error, 0, 2);
     }
-#ifdef FW_DECODE_TRACE
-    if (w != 0) {
-        // profiling: when this wave's down rows have arrived
-        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-        FW_TRACE_MARK(slot, 9);
-    }
-#endif
     // wave 1 scores while the lead wave runs the pairs (the publish below
     // synchronises both before anything reads the scores)
     score_experts<NT>(p, li, sh, j == 0, kMaxHidden, 1, false);
+    FW_TRACE_MARK_IF(w == 1 && lane == 0, slot, 6);
     st.scored = li;
+    if (w == 1) issue_down();
     // lead wave: the two pairs' dots and SwiGLU (src/expert.rs:514-571) once
     // its copies into LDS have landed; lane 0 stores the word of both
     // activations
     if (w == 0) {
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        FW_TRACE_MARK_IF(lane == 0, slot, 10);
         float acc[1][2];
         line_chains_lds<MBH, 2>(brows + g * (H / 4), H / 32, sh.xs, q, acc);
         float d = tree32_reduce_lines(acc[0][0], acc[0][1]);
@@ -1161,6 +1180,7 @@ __device__ __forceinline__ bool combine_task_fused(const DecodeParams& p, uint32
         const uint32_t a1 = (uint32_t)__shfl((int)a, (lane + 2 * kLanesPerRow) & 63, kWave);
         if (lane == 0)
             coherent_store64(p.act + (size_t)(li * p.S + bs) * (I / 2) + pr / 2, tagged(a | (a1 << 16), epoch));
+        FW_TRACE_MARK_IF(lane == 0, slot, 11);
     }
     publish(phase_counters(p, li, kCntGateUp), p.n_gu, p.n_shared + p.nb_rows + j, phase_flags(p, li, kCntGateUp),
             epoch);
@@ -1180,12 +1200,11 @@ __device__ __forceinline__ bool combine_task_fused(const DecodeParams& p, uint32
             rin = (uint32_t)v[0];
         }
     }
-    FW_TRACE_MARK(slot, 3);
     if (!wait_phase(phase_flags(p, li, kCntGateUp), epoch, p.error, p.limit_ticks, &sh.flag)) return false;
     FW_TRACE_STAMP(t1);
     // every activation vector of the task at once (matrices 0..U <= 11)
     st.loaded = st.staged = -1;
-    if (!stage_acts_direct<MBI>(p, li, epoch, sh, U)) return false;
+    if (!stage_acts_direct<MBI>(p, li, epoch, sh, U, slot)) return false;
     FW_TRACE_MARK(slot, 4);
     // payloads: the low halves of the tagged words
     const uint32_t* act_lds = reinterpret_cast<const uint32_t*>(sh.xs);
@@ -1199,7 +1218,7 @@ __device__ __forceinline__ bool combine_task_fused(const DecodeParams& p, uint32
         }
     }
     FW_TRACE_MARK(slot, 0);
-    if (!__syncthreads_and(ok)) return false;
+    if (!wg_all(sh.red, ok)) return false;
     if (mixer) {
         const int gg = rt;
         // src/decoder_layer.rs:528-545: weighted = bf16(down * score), summed in
@@ -1233,7 +1252,7 @@ __device__ __forceinline__ bool combine_task_fused(const DecodeParams& p, uint32
             if (li + 1 == p.nlayers && p.x_final != nullptr) reinterpret_cast<uint32_t*>(p.x_final)[at] = x2;
         }
     }
-    if (!__syncthreads_and(ok)) return false;
+    if (!wg_all(sh.red, ok)) return false;
     FW_TRACE_MARK(slot, 1);
     publish(phase_counters(p, li, kCntC), p.n_c, j, phase_flags(p, li, kCntC), epoch);
     FW_TRACE_STAMP(t2);
@@ -1301,7 +1320,7 @@ __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(N
 k_moe_decode(const DecodeParams* __restrict__ P, uint32_t epoch) {
     __shared__ DecodeShared<NT, MBI> sh;
     if (threadIdx.x < 32) sh.exp2tab[threadIdx.x] = c_exp2_table[threadIdx.x];
-    __syncthreads();
+    wg_sync();
     const int b = (int)blockIdx.x;
     const int G = (int)gridDim.x;
     if (b < P->g_rows) {
@@ -1311,7 +1330,7 @@ k_moe_decode(const DecodeParams* __restrict__ P, uint32_t epoch) {
     }
     // Completed counters zero themselves. After a failure some are left
     // partly counted: the last workgroup out then zeroes them all.
-    __syncthreads();
+    wg_sync();
     if (threadIdx.x == 0) {
         uint32_t* done = P->counters + (size_t)P->nlayers * kCountersPerLayer * kCounterGroupWords;
         if (count_task(done, G, b) && coherent_load(P->error) != 0) {

@@ -533,6 +533,33 @@ __device__ __forceinline__ void wave_topk(const uint16_t* __restrict__ logits, i
     }
 }
 
+// ---- workgroup barriers ----------------------------------------------------------
+//
+// Barrier for LDS exchange between the waves of a workgroup: the wave's LDS
+// (and scalar memory) operations complete, then s_barrier. Unlike
+// __syncthreads, whose workgroup-scope fence also waits for every global load
+// and store the wave has in flight, it lets prefetched weight rows keep
+// streaming across it. The waves of a workgroup exchange data only through
+// LDS (between workgroups, tagged words carry their own validity).
+__device__ __forceinline__ void wg_sync() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+// Number of the workgroup's threads with a nonzero predicate (red: four LDS
+// words), and the all / any forms; every thread calls them.
+__device__ __forceinline__ int wg_count(int32_t* red, int pred) {
+    const int c = (int)__popcll(__ballot(pred != 0));
+    if (lane_id() == 0) red[wave_id()] = c;
+    wg_sync();
+    const int total = red[0] + red[1] + red[2] + red[3];
+    wg_sync();
+    return total;
+}
+__device__ __forceinline__ bool wg_all(int32_t* red, bool pred) { return wg_count(red, !pred) == 0; }
+__device__ __forceinline__ bool wg_any(int32_t* red, bool pred) { return wg_count(red, pred) != 0; }
+
 // ---- inter-workgroup synchronisation for the persistent kernel ----------------------
 //
 // The per-XCD L2 caches are not coherent with each other, and no cache is
@@ -583,7 +610,7 @@ __device__ __forceinline__ bool count_task(uint32_t* group, int n, int j) {
 // Announce finished task j of a phase of n tasks. Every wave has issued its
 // tagged stores (program order up to the barrier).
 __device__ __forceinline__ void publish(uint32_t* group, int n, int j, uint32_t* flags, uint32_t epoch) {
-    __syncthreads();
+    wg_sync();
     if (threadIdx.x == 0 && count_task(group, n, j)) {
         for (int i = 0; i < kFlagCopies; ++i) coherent_store(flags + i * kFlagStride, epoch);
     }
@@ -616,9 +643,9 @@ __device__ __forceinline__ bool wait_phase(const uint32_t* flags, uint32_t epoch
         }
         *lds_flag = ok;
     }
-    __syncthreads();
+    wg_sync();
     int32_t ok = *lds_flag;
-    __syncthreads();
+    wg_sync();
     return ok != 0;
 }
 
