@@ -168,8 +168,11 @@ constexpr int kBatchMatrices = 16;  // C task: matrices per register batch (4 pe
 // the tagged words of twelve activation vectors.
 constexpr int kDirectVectors = 12;
 constexpr int kBRowsAt = kMaxHidden + kMaxExperts;  // words
-constexpr int kFusedWords = kBRowsAt + 2 * kMaxHidden > kDirectVectors * 16 * 16 * 2 ? kBRowsAt + 2 * kMaxHidden
-                                                                                      : kDirectVectors * 16 * 16 * 2;
+// words between the four gate/up rows: 64 bytes past a row, so the four lane
+// groups reading the same line offset of their rows hit different LDS banks
+constexpr int kBRowStride = kMaxHidden / 2 + 16;
+constexpr int kFusedWords = kBRowsAt + 4 * kBRowStride > kDirectVectors * 16 * 16 * 2 ? kBRowsAt + 4 * kBRowStride
+                                                                                       : kDirectVectors * 16 * 16 * 2;
 __host__ __device__ constexpr int stage_words(int NT, int MBI) {
     return (NT == 1 && MBI <= 16) ? kFusedWords
            : NT * kMaxHidden > (kBatchMatrices * NT * MBI * 16 < 8192 ? kBatchMatrices * NT * MBI * 16 : 8192)
@@ -280,30 +283,41 @@ __device__ __forceinline__ void normalise_input(const DecodeParams& p, SH& sh) {
     const int T = p.T, n = p.H;
     float* xs = sh.xs;
     const int w = rel_wave(p), lane = lane_id();
+    // Lane L < 32 of token t's wave sums chain j = bit-reverse of L (five
+    // bits): the tree's partners (j, j + 16), (j, j + 8), (j, j + 4) are then
+    // lanes L ^ 1, L ^ 2, L ^ 4 of one row (DPP), and its last four values
+    // lanes 0, 16, 8, 24.
+    const int j = (int)(__builtin_bitreverse32((uint32_t)lane) >> 27);
+    auto finish = [&](float c, int t) {
+        c = add_rn(c, dpp_f32<kDppQuadXor1>(c));  // a1[j] = c[j] + c[j+16]
+        c = add_rn(c, dpp_f32<kDppQuadXor2>(c));  // a2[j] = a1[j] + a1[j+8]
+        c = add_rn(c, dpp_f32<kDppRowRor4>(c));   // a3[j] = a2[j] + a2[j+4]
+        const float a0 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, c), 0));
+        const float a1 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, c), 16));
+        const float a2 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, c), 8));
+        const float a3 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, c), 24));
+        const float ss = add_rn(add_rn(add_rn(a0, a1), add_rn(a2, a3)), 0.0f);
+        if (lane == 0) sh.inv[t] = 1.0f / sqrtf(add_rn(ss / (float)n, 1e-6f));
+    };
     if (w < T) {
         const float* r = xs + w * n;
         float c = 0.0f;
         if (lane < 32) {
-            // one chain per lane, blocks in order; LDS reads batched ahead of the adds
+            // blocks in order; LDS reads batched ahead of the adds
             int b = 0;
             for (; b + 16 <= n / 32; b += 16) {
                 float e[16];
 #pragma unroll
-                for (int i = 0; i < 16; ++i) e[i] = r[32 * (b + i) + lane];
+                for (int i = 0; i < 16; ++i) e[i] = r[32 * (b + i) + j];
 #pragma unroll
                 for (int i = 0; i < 16; ++i) c = add_rn(c, mul_rn(e[i], e[i]));
             }
             for (; b < n / 32; ++b) {
-                float e = r[32 * b + lane];
+                float e = r[32 * b + j];
                 c = add_rn(c, mul_rn(e, e));
             }
         }
-        c = add_rn(c, __shfl_down(c, 16, kWave));  // a1[j] = c[j] + c[j+16]
-        c = add_rn(c, __shfl_down(c, 8, kWave));   // a2[j] = a1[j] + a1[j+8]
-        c = add_rn(c, __shfl_down(c, 4, kWave));   // a3[j] = a2[j] + a2[j+4]
-        float pair = add_rn(c, __shfl_down(c, 1, kWave));  // (a0+a1) in lane 0, (a2+a3) in lane 2
-        float ss = add_rn(add_rn(pair, __shfl_down(pair, 2, kWave)), 0.0f);
-        if (lane == 0) sh.inv[w] = 1.0f / sqrtf(add_rn(ss / (float)n, 1e-6f));
+        finish(c, w);
     }
     wg_sync();
     for (int t = 0; t < T; ++t) {
@@ -689,8 +703,13 @@ __device__ __forceinline__ bool pairs_task(const DecodeParams& p, uint32_t epoch
         }
         FW_TRACE_MARK(slot, 1);
     }
-    publish(phase_counters(p, li, kCntGateUp), p.n_gu, shared ? js : p.n_shared + js,
-            phase_flags(p, li, kCntGateUp), epoch);
+    if (p.cpairs > 0) {
+        // one-token fused C tasks read the activations by their tags alone
+        wg_sync();
+    } else {
+        publish(phase_counters(p, li, kCntGateUp), p.n_gu, shared ? js : p.n_shared + js,
+                phase_flags(p, li, kCntGateUp), epoch);
+    }
     FW_TRACE_STAMP(t2);
     FW_TRACE_WRITE(slot, shared ? kTaskShared : kTaskGateUp, t0, t1, t2);
     return true;
@@ -1099,7 +1118,7 @@ template <int NT, int MBH, int MBI, int TK, class SH>
 __device__ __forceinline__ bool combine_task_fused(const DecodeParams& p, uint32_t epoch, SH& sh, LdsState& st,
                                                    int li, int j) {
     static_assert(fused_combine(NT, MBH, MBI), "one token");
-    static_assert(stage_words(NT, MBI) >= kBRowsAt + 2 * kMaxHidden, "gate/up rows above the exponentials");
+    static_assert(stage_words(NT, MBI) >= kBRowsAt + 4 * kBRowStride, "gate/up rows above the exponentials");
     static_assert(stage_words(NT, MBI) >= kDirectVectors * MBI * 16 * 2, "tagged words of the staged vectors");
     FW_TRACE_STAMP(t0);
     const int slot = trace_slot(p, li, p.n_router + p.n_shared + p.n_b + j);
@@ -1124,7 +1143,9 @@ __device__ __forceinline__ bool combine_task_fused(const DecodeParams& p, uint32
     // row r (= lane group) of the pairs: gate of pair r / 2 for even r, up for odd
     auto brel = [&](int r) { return ((r & 1) ? I : 0) + (r >> 1); };
     const uint16_t* bbase = L.gate_up + ((size_t)uniform(sh.sorted[bs]) * 2 * I + (fp0 - bs * I)) * H;
-    uint64_t* brows = reinterpret_cast<uint64_t*>(sh.xs + kBRowsAt);  // [4][H / 4]
+    // the four rows of H bf16, H / 2 + 16 words apart (see kBRowStride)
+    uint64_t* brows = reinterpret_cast<uint64_t*>(sh.xs + kBRowsAt);
+    const int bstride = (H / 2 + 16) / 2;  // 8-byte words
     if (w == 0) {
         // 1 KB per wave instruction (16 bytes per lane)
 #pragma unroll
@@ -1132,12 +1153,13 @@ __device__ __forceinline__ bool combine_task_fused(const DecodeParams& p, uint32
             for (int c0 = 0; c0 < H / 512; ++c0) {
                 __builtin_amdgcn_global_load_lds(
                     reinterpret_cast<const void*>(bbase + (size_t)brel(r) * H + c0 * 512 + 8 * lane),
-                    (__attribute__((address_space(3))) void*)(brows + r * (H / 4) + c0 * 128), 16, 0, 0);
+                    (__attribute__((address_space(3))) void*)(brows + r * bstride + c0 * 128), 16, 0, 0);
             }
         }
     }
-    // down rows (wave 1 scores first: it then has no loads in flight for the
-    // scoring code to wait on; its rows are needed only after the gate/up phase)
+    // Down rows: requested once the lead wave's gate/up rows have landed, so
+    // that during the layer's burst the gate/up rows (needed first, by every
+    // B task) go ahead of the down rows (needed only after the gate/up phase).
     auto issue_down = [&]() {
 #pragma unroll
         for (int k = 0; k < 3; ++k) {
@@ -1148,7 +1170,6 @@ __device__ __forceinline__ bool combine_task_fused(const DecodeParams& p, uint32
             }
         }
     };
-    if (w != 1) issue_down();
     // route weights and the shared-gate sigmoid (exponentials above the block
     // input); task 0 also reports the layer's ids, scores and sigmoid and
     // rejects a NaN logit (src/decoder_layer.rs:279-281)
@@ -1163,15 +1184,19 @@ __device__ __forceinline__ bool combine_task_fused(const DecodeParams& p, uint32
     score_experts<NT>(p, li, sh, j == 0, kMaxHidden, 1, false);
     FW_TRACE_MARK_IF(w == 1 && lane == 0, slot, 6);
     st.scored = li;
-    if (w == 1) issue_down();
-    // lead wave: the two pairs' dots and SwiGLU (src/expert.rs:514-571) once
-    // its copies into LDS have landed; lane 0 stores the word of both
-    // activations
     if (w == 0) {
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
         FW_TRACE_MARK_IF(lane == 0, slot, 10);
+    }
+    wg_sync();
+    // (the lead wave issues its own after the pairs: issuing into the burst can
+    // stall it)
+    if (w != 0) issue_down();
+    // lead wave: the two pairs' dots and SwiGLU (src/expert.rs:514-571) from
+    // the rows in LDS; lane 0 stores the word of both activations
+    if (w == 0) {
         float acc[1][2];
-        line_chains_lds<MBH, 2>(brows + g * (H / 4), H / 32, sh.xs, q, acc);
+        line_chains_lds<MBH, 2>(brows + g * bstride, H / 32, sh.xs, q, acc);
         float d = tree32_reduce_lines(acc[0][0], acc[0][1]);
         if (q == 0) d = tree32_finish(d, bbase + (size_t)brel(g) * H, sh.xs, H);
         const uint32_t bits = to_bf16(d);
@@ -1181,10 +1206,8 @@ __device__ __forceinline__ bool combine_task_fused(const DecodeParams& p, uint32
         if (lane == 0)
             coherent_store64(p.act + (size_t)(li * p.S + bs) * (I / 2) + pr / 2, tagged(a | (a1 << 16), epoch));
         FW_TRACE_MARK_IF(lane == 0, slot, 11);
+        issue_down();
     }
-    publish(phase_counters(p, li, kCntGateUp), p.n_gu, p.n_shared + p.nb_rows + j, phase_flags(p, li, kCntGateUp),
-            epoch);
-    FW_TRACE_MARK(slot, 5);
     // the residual words this task updates: one lane of the lead wave per row
     const int rt = w * kWave + lane;
     const bool mixer = rt < kRowsPerCTask;
@@ -1200,7 +1223,12 @@ __device__ __forceinline__ bool combine_task_fused(const DecodeParams& p, uint32
             rin = (uint32_t)v[0];
         }
     }
-    if (!wait_phase(phase_flags(p, li, kCntGateUp), epoch, p.error, p.limit_ticks, &sh.flag)) return false;
+    // No wait for the gate/up phase: the staging below reads every activation
+    // word until it carries this launch's epoch (a word is complete when its
+    // tag is), so the down rows start as soon as the task's own words are in.
+    // The staging overwrites the block input and the gate/up rows: the lead
+    // wave's pairs must be done first.
+    wg_sync();
     FW_TRACE_STAMP(t1);
     // every activation vector of the task at once (matrices 0..U <= 11)
     st.loaded = st.staged = -1;

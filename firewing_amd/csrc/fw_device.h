@@ -44,6 +44,7 @@ constexpr int kDppRowShl1 = 0x101, kDppRowShl2 = 0x102, kDppRowShl4 = 0x104, kDp
 constexpr int kDppRowMirror = 0x140, kDppRowHalfMirror = 0x141;
 constexpr int kDppRowBcast15 = 0x142, kDppRowBcast31 = 0x143;
 constexpr int kDppQuadXor1 = 0xB1, kDppQuadXor2 = 0x4E;  // quad_perm [1,0,3,2], [2,3,0,1]
+constexpr int kDppRowRor4 = 0x124;                       // lane (i + 4) mod 16 of the row
 
 // v from lane (i + n) of the same 16-lane row (0 past the row's end).
 template <int CTRL>
@@ -605,6 +606,14 @@ __device__ __forceinline__ bool count_task(uint32_t* group, int n, int j) {
     if (__hip_atomic_fetch_add(top, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + 1u != top_target) return false;
     __hip_atomic_store(top, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     return true;
+}
+
+// Announce finished task j of a phase of n tasks from one wave that made all of
+// the task's stores (its lane 0 counts; no barrier).
+__device__ __forceinline__ void publish_wave(uint32_t* group, int n, int j, uint32_t* flags, uint32_t epoch) {
+    if (lane_id() == 0 && count_task(group, n, j)) {
+        for (int i = 0; i < kFlagCopies; ++i) coherent_store(flags + i * kFlagStride, epoch);
+    }
 }
 
 // Announce finished task j of a phase of n tasks. Every wave has issued its
