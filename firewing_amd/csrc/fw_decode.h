@@ -1237,39 +1237,40 @@ __device__ __forceinline__ bool combine_task_fused(const DecodeParams& p, uint32
     // payloads: the low halves of the tagged words
     const uint32_t* act_lds = reinterpret_cast<const uint32_t*>(sh.xs);
     const int act_stride = 2 * (max(I, Is) / 2);
+    // Each down-row dot leaves its weighted value: src/decoder_layer.rs:528-545
+    // weighted = bf16(down * score) for slot m - 1 (one token: the slots are
+    // its experts in ascending id, the order of its weights), and
+    // src/decoder_layer.rs:563-575 gated = bf16(shared_down * sigmoid) for m = 0.
 #pragma unroll
     for (int k = 0; k < 3; ++k) {
         const int m = w + 4 * k;
         if (m <= U) {
             const uint32_t bits = down_row_lds<MBI, 2>(c[k], (m == 0 ? Is : I) / 32, act_lds + m * act_stride, q);
-            if (q == 0) sh.res[m * kRowsPerCTask + g] = bits;
+            if (q == 0) {
+                const uint32_t scale = m == 0 ? sh.sig[0] : sh.tweight[m - 1];
+                sh.res[m * kRowsPerCTask + g] = to_bf16(mul_rn(from_bf16(bits), from_bf16(scale)));
+            }
         }
     }
     FW_TRACE_MARK(slot, 0);
     if (!wg_all(sh.red, ok)) return false;
     if (mixer) {
         const int gg = rt;
-        // src/decoder_layer.rs:528-545: weighted = bf16(down * score), summed in
-        // ascending expert order from bf16 zero, rounding after each add
+        // the weighted values summed in ascending expert order from bf16 zero,
+        // rounding after each add, then the gated shared output
         uint32_t mix = to_bf16(0.0f);
         for (int k0 = 0; k0 < K; k0 += 8) {
-            uint32_t d[8], wt[8];
+            uint32_t d[8];
 #pragma unroll
             for (int i = 0; i < 8; ++i) {
-                if (k0 + i < K) {
-                    d[i] = sh.res[(1 + sh.tslot[k0 + i]) * kRowsPerCTask + gg];
-                    wt[i] = sh.tweight[k0 + i];
-                }
+                if (k0 + i < K) d[i] = sh.res[(1 + k0 + i) * kRowsPerCTask + gg];
             }
 #pragma unroll
             for (int i = 0; i < 8; ++i) {
-                if (k0 + i < K) mix = add_bf16(mix, to_bf16(mul_rn(from_bf16(d[i]), from_bf16(wt[i]))));
+                if (k0 + i < K) mix = add_bf16(mix, d[i]);
             }
         }
-        // src/decoder_layer.rs:563-575: gated = bf16(shared_down * sigmoid)
-        const uint32_t sd = sh.res[gg];
-        const uint32_t gated = to_bf16(mul_rn(from_bf16(sd), from_bf16(sh.sig[0])));
-        const uint32_t o = add_bf16(mix, gated);
+        const uint32_t o = add_bf16(mix, sh.res[gg]);
         const uint32_t xn = add_bf16((rin >> (16 * (gg & 1))) & 0xffffu, o);
         const uint32_t o_odd = (uint32_t)__shfl_xor((int)o, 1, kWave);
         const uint32_t x_odd = (uint32_t)__shfl_xor((int)xn, 1, kWave);

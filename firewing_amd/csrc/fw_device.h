@@ -579,9 +579,10 @@ __device__ __forceinline__ bool wg_any(int32_t* red, bool pred) { return wg_coun
 //   phase increments once, right after issuing its stores (no wait for their
 //   acknowledgement: readers check the tags). Atomics on one word are
 //   serialised at the coherence point (about 12 ns each: a thousand
-//   simultaneous arrivals on one counter take 12 us), so task j increments
-//   sub-counter j mod kSubCounters, and the task completing a sub-counter
-//   increments the group's top counter. The task completing the top counter
+//   simultaneous arrivals on one counter take 12 us), so task j of a phase of
+//   more than kDirectCount tasks increments sub-counter j mod kSubCounters,
+//   and the task completing a sub-counter increments the group's top counter
+//   (smaller phases count on the top counter directly). The task completing the top counter
 //   writes the epoch into kFlagCopies flag words; a waiter polls the copy for
 //   its workgroup, so no single word is polled by more than a few dozen
 //   workgroups. The completing task of each counter zeroes it for the next
@@ -592,17 +593,25 @@ constexpr int kFlagStride = 64;  // words between copies (256 bytes: different m
 constexpr int kSubCounters = 32;
 constexpr int kCounterStride = 64;  // words between counters of a group
 constexpr int kCounterGroupWords = (1 + kSubCounters) * kCounterStride;  // top, then the sub-counters
+constexpr int kDirectCount = 64;  // phases of at most this many tasks count on the top counter only
 
 // Task j of a phase of n tasks counts itself in `group`; returns true in the
 // task that completes the phase (thread 0 only).
 __device__ __forceinline__ bool count_task(uint32_t* group, int n, int j) {
+    auto* top = as_global_rw(group);
+    if (n <= kDirectCount) {
+        // few tasks: one level (one round trip)
+        if (__hip_atomic_fetch_add(top, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + 1u != (uint32_t)n)
+            return false;
+        __hip_atomic_store(top, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        return true;
+    }
     const int sub = j % kSubCounters;
     const uint32_t sub_target = (uint32_t)((n - sub + kSubCounters - 1) / kSubCounters);
     const uint32_t top_target = (uint32_t)(n < kSubCounters ? n : kSubCounters);
     auto* sc = as_global_rw(group + (1 + sub) * kCounterStride);
     if (__hip_atomic_fetch_add(sc, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + 1u != sub_target) return false;
     __hip_atomic_store(sc, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    auto* top = as_global_rw(group);
     if (__hip_atomic_fetch_add(top, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + 1u != top_target) return false;
     __hip_atomic_store(top, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     return true;
