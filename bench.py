@@ -17,6 +17,10 @@ Prints one JSON line (the driver contract) with:
   cpu_baseline the CPU oracle (the reference's scalar path restated in C) on
               the same input, one host thread, 48 layers, block arithmetic only
   mtp         the same step with 2 and 4 tokens (MTP verify widths)
+  prefill     8192 tokens through one resident block (router, top-10,
+              grouped bf16 MFMA expert GEMMs, ordered combine): tokens/s from
+              HIP events on the launch stream; the grouped GEMMs' MFMA
+              utilisation from the committed rocprofv3 kernel trace
 Progress goes to stderr.
 """
 from __future__ import annotations
@@ -36,6 +40,8 @@ sys.path.insert(0, str(ROOT))
 METRIC = "MoE decode µs/token (batch 1, 48 layers) + HBM GB/s; 8K prefill tokens/s"
 SHAPE = dict(hidden=2048, intermediate=512, experts=512, top_k=10, shared_intermediate=512)
 HBM_PEAK_GBPS = 8000.0
+BF16_PEAK_TFLOPS = 2500.0  # dense bf16 MFMA
+PREFILL_TOKENS = 8192
 
 
 def log(msg: str) -> None:
@@ -115,6 +121,76 @@ def copy_calibration(rt, hm) -> None:
     log(f"copy calibration: 3 x {COPY_CALIBRATION_BYTES} bytes")
 
 
+def prefill_flops(ids: np.ndarray, tokens: int) -> dict:
+    """Algorithmic flops of the many-token block: routed expert GEMMs (one
+    gate/up [2I,H] and one down [H,I] product per (token, expert) pair), the
+    shared expert (every token) and the exact router."""
+    H, I, E, Is = SHAPE["hidden"], SHAPE["intermediate"], SHAPE["experts"], SHAPE["shared_intermediate"]
+    pairs = int(ids.size)
+    return {"routed_gemm": 2 * pairs * (2 * I * H + H * I),
+            "shared_gemm": 2 * tokens * (2 * Is * H + H * Is),
+            "router": 2 * tokens * (E + 1) * H}
+
+
+def read_prefill_profile() -> dict | None:
+    """Average durations (us) of the prefill kernels from the committed
+    rocprofv3 summary of this workload, or None."""
+    path = ROOT / "profiles" / "k_pf_prefill_8k_kernel_trace.md"
+    if not path.is_file():
+        return None
+    out = {}
+    for line in path.read_text().splitlines():
+        if line.startswith("avg_us "):
+            _, name, value = line.split()
+            out[name] = float(value)
+    return out or None
+
+
+def bench_prefill(rt, hm, ctx, args) -> dict:
+    T = PREFILL_TOKENS
+    x_host = hm.synth_hidden(args.seed, T, SHAPE["hidden"], True, first_token=100000)
+    got = ctx.prefill_block(0, x_host)
+    flops = prefill_flops(got["selected_experts"], T)
+    x = rt.DeviceArray.from_numpy(x_host)
+    out = rt.DeviceArray(x_host.shape, np.uint16)
+    stream = rt.Stream()
+    for _ in range(2):
+        ctx.prefill_block_dev(0, x.ptr, T, out.ptr, stream=stream.handle)
+    stream.synchronize()
+    steps = max(3, args.steps // 5)
+    start, end = rt.Event(), rt.Event()
+    start.record(stream)
+    for _ in range(steps):
+        ctx.prefill_block_dev(0, x.ptr, T, out.ptr, stream=stream.handle)
+    end.record(stream)
+    stream.synchronize()
+    ctx.synchronize()
+    ms = start.elapsed_ms(end) / steps
+    assert np.array_equal(out.numpy(), got["out"]), "device-pointer prefill differs from host-pointer prefill"
+    total = sum(flops.values())
+    res = {"tokens": T, "us_per_block": round(ms * 1000, 1), "tokens_per_s": round(T / (ms * 1e-3), 1),
+           "pairs": int(got["selected_experts"].size),
+           "max_tokens_per_expert": int(np.bincount(got["selected_experts"].ravel()).max()),
+           "flops": flops, "block_tflops": round(total / (ms * 1e-3) / 1e12, 1)}
+    prof = read_prefill_profile()
+    if prof:
+        gemm_us = prof.get("k_pf_gemm_gate_up", 0.0) + prof.get("k_pf_gemm_down", 0.0)
+        if gemm_us > 0:
+            gemm = flops["routed_gemm"] + flops["shared_gemm"]
+            tf = gemm / (gemm_us * 1e-6) / 1e12
+            res["gemm_roofline"] = {"bound": "mfma", "achieved": round(tf, 1), "peak": BF16_PEAK_TFLOPS,
+                                    "unit": "TFLOP/s", "frac": round(tf / BF16_PEAK_TFLOPS, 4),
+                                    "source": "profiles/k_pf_prefill_8k_kernel_trace.md"}
+        res["kernel_us"] = prof
+    log(f"prefill {T} tokens: {ms * 1000:.1f} us/block, {T / (ms * 1e-3) / 1e6:.2f} M tokens/s")
+    stream.destroy()
+    start.destroy()
+    end.destroy()
+    x.free()
+    out.free()
+    return res
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -124,6 +200,9 @@ def main() -> int:
     ap.add_argument("--seed", type=lambda s: int(s, 0), default=0x46495245)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-mtp", action="store_true")
+    ap.add_argument("--no-prefill", action="store_true")
+    ap.add_argument("--prefill-only", action="store_true",
+                    help="time the 8K-token prefill block alone (for kernel traces)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="also run a 1 GiB plain copy kernel (traffic-counter calibration)")
     args = ap.parse_args()
@@ -135,6 +214,14 @@ def main() -> int:
 
     from firewing_amd import hip_moe as hm
     from firewing_amd import hip_runtime as rt
+
+    if args.prefill_only:
+        ctx = hm.MoeContext(layers=1, **SHAPE)
+        ctx.generate_layers(0, 1, args.seed, True)
+        res = bench_prefill(rt, hm, ctx, args)
+        ctx.close()
+        print(json.dumps({"prefill": res}), flush=True)
+        return 0
 
     L = args.layers
     T = 1
@@ -224,6 +311,9 @@ def main() -> int:
                                "frac": round(gbps / HBM_PEAK_GBPS, 4)}
             log(f"MTP width {width}: {ms * 1000:.1f} us/step, union {np.mean(u):.1f}, {gbps:.0f} GB/s")
         result["mtp"] = mtp
+
+    if not args.no_prefill:
+        result["prefill"] = bench_prefill(rt, hm, ctx, args)
 
     ctx.close()
     x.free()

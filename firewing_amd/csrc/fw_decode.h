@@ -101,6 +101,8 @@ struct DecodeParams {
                                           // by wave 0 of each C task (one token); 0: B tasks on combine
     int n_gu;                             // tasks counted in the gate/up phase
     int cu_count;                         // compute units (workgroup b sits on the CU of b mod cu_count)
+    int input_by_tags;                    // router tasks await their block input by its words' tags
+                                          // alone (no combine phase flag)
     uint64_t* trace;     // profiling builds only
 };
 
@@ -208,6 +210,7 @@ struct DecodeShared {
     int32_t nunion;
     int32_t flag;
     int32_t red[kThreads / 64];  // workgroup reductions (one word per wave)
+    uint32_t rin[kRowsPerCTask];  // C task: the residual words it updates
     int32_t trace_stale;  // profiling builds: stale words of the last block-input read
 };
 
@@ -278,7 +281,8 @@ __device__ __forceinline__ bool load_input(const DecodeParams& p, int li, uint32
 // divided by H; h[H-1] = 1.0 with the bias feature. Wave t normalises token t,
 // in place in LDS.
 template <int NT, class SH>
-__device__ __forceinline__ void normalise_input(const DecodeParams& p, SH& sh) {
+__device__ __forceinline__ void normalise_input(const DecodeParams& p, SH& sh, int slot = -1) {
+    (void)slot;
     if (!p.prenorm) return;
     const int T = p.T, n = p.H;
     float* xs = sh.xs;
@@ -291,7 +295,7 @@ __device__ __forceinline__ void normalise_input(const DecodeParams& p, SH& sh) {
     auto finish = [&](float c, int t) {
         c = add_rn(c, dpp_f32<kDppQuadXor1>(c));  // a1[j] = c[j] + c[j+16]
         c = add_rn(c, dpp_f32<kDppQuadXor2>(c));  // a2[j] = a1[j] + a1[j+8]
-        c = add_rn(c, dpp_f32<kDppRowRor4>(c));   // a3[j] = a2[j] + a2[j+4]
+        c = add_rn(c, dpp_f32<kDppRowRead4>(c));   // a3[j] = a2[j] + a2[j+4]
         const float a0 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, c), 0));
         const float a1 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, c), 16));
         const float a2 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, c), 8));
@@ -318,8 +322,10 @@ __device__ __forceinline__ void normalise_input(const DecodeParams& p, SH& sh) {
             }
         }
         finish(c, w);
+        FW_TRACE_MARK_IF(w == 0 && lane == 0, slot, 5);
     }
     wg_sync();
+    FW_TRACE_MARK(slot, 6);
     for (int t = 0; t < T; ++t) {
         const float inv = sh.inv[t];
         float* r = xs + t * n;
@@ -330,6 +336,7 @@ __device__ __forceinline__ void normalise_input(const DecodeParams& p, SH& sh) {
         }
     }
     wg_sync();
+    FW_TRACE_MARK(slot, 7);
 }
 
 // ---- expert selection ------------------------------------------------------------------
@@ -549,7 +556,7 @@ __device__ __forceinline__ bool stage_layer_input(const DecodeParams& p, uint32_
         FW_TRACE_MARK(slot, 2);
         FW_TRACE_VALUE(slot, 4, sh.trace_stale);
     }
-    normalise_input<NT>(p, sh);
+    normalise_input<NT>(p, sh, slot);
     st.staged = li;
     return true;
 }
@@ -590,7 +597,11 @@ __device__ __forceinline__ bool router_task(const DecodeParams& p, uint32_t epoc
     LineShare<MBH> rs;
     if (wave_active && !fold)
         line_issue(rs, L.router + (size_t)row0 * H, (uint32_t)(valid ? rin : 0) * (uint32_t)H * 2u, q);
-    if (li > 0 && !wait_phase(phase_flags(p, li - 1, kCntC), epoch, p.error, p.limit_ticks, &sh.flag)) return false;
+    // one-token steps: the residual words' tags alone say when the block
+    // input is complete (a flag hop less on the layer's critical path)
+    if (li > 0 && !p.input_by_tags &&
+        !wait_phase(phase_flags(p, li - 1, kCntC), epoch, p.error, p.limit_ticks, &sh.flag))
+        return false;
     FW_TRACE_STAMP(t1);
     if (!stage_layer_input<NT>(p, epoch, sh, st, li, slot)) return false;
     FW_TRACE_MARK(slot, 0);
@@ -607,7 +618,9 @@ __device__ __forceinline__ bool router_task(const DecodeParams& p, uint32_t epoc
         }
     } else if (wave_active) {
         float acc[NT][2];
+        FW_TRACE_MARK(slot, 8);
         line_chains<NT, MBH>(rs, H / 32, sh.xs, H, q, acc);
+        FW_TRACE_MARK(slot, 9);
         // groups 0 and 2 store the pairs (row, row + 1); the gate logit goes to
         // its own slot with a zero beside it
         const int at = gate_task ? p.gi : out_index;
@@ -1133,7 +1146,34 @@ __device__ __forceinline__ bool combine_task_fused(const DecodeParams& p, uint32
     if (w == 0) line_issue(c[0], L.shared_down + (size_t)r0 * Is, (uint32_t)(g * Is * 2), q);
     // this task's gate/up pairs need the block input (ready with the previous layer)
     if (li > 0 && !wait_phase(phase_flags(p, li - 1, kCntC), epoch, p.error, p.limit_ticks, &sh.flag)) return false;
-    if (!stage_layer_input<NT>(p, epoch, sh, st, li)) return false;
+    // the residual words this task updates (one lane of the lead wave per
+    // row), taken from the block input before it is normalised in place
+    const int rt = w * kWave + lane;
+    const bool mixer = rt < kRowsPerCTask;
+    const size_t at = ((size_t)r0 + (rt & ~1)) / 2;
+    if (st.staged != li) {
+        if (st.loaded != li) {
+            if (!load_input<NT>(p, li, epoch, sh)) return false;
+            st.loaded = li;
+        }
+        // (the values are bf16 widened exactly; normalise_input overwrites
+        // them only after a workgroup barrier)
+        if (mixer)
+            sh.rin[rt] = (__float_as_uint(sh.xs[2 * at]) >> 16) | (__float_as_uint(sh.xs[2 * at + 1]) & 0xffff0000u);
+        normalise_input<NT>(p, sh);
+        st.staged = li;
+    } else if (mixer) {
+        // (not reached: one C task per workgroup and layer stages its input)
+        uint32_t v0;
+        if (li == 0) {
+            v0 = reinterpret_cast<const uint32_t*>(p.x_in)[at];
+        } else {
+            uint64_t v[1];
+            if (!load_tagged<1, 1>(v, p.xw + (size_t)li * H / 2 + at, 1, epoch, p.error, p.limit_ticks)) return false;
+            v0 = (uint32_t)v[0];
+        }
+        sh.rin[rt] = v0;
+    }
     if (!select_layer<NT, TK>(p, epoch, sh, st, li, slot)) return false;
     FW_TRACE_MARK(slot, 2);
     const int U = uniform(sh.nunion);
@@ -1208,21 +1248,7 @@ __device__ __forceinline__ bool combine_task_fused(const DecodeParams& p, uint32
         FW_TRACE_MARK_IF(lane == 0, slot, 11);
         issue_down();
     }
-    // the residual words this task updates: one lane of the lead wave per row
-    const int rt = w * kWave + lane;
-    const bool mixer = rt < kRowsPerCTask;
-    const size_t at = ((size_t)r0 + (rt & ~1)) / 2;
     bool ok = true;
-    uint32_t rin = 0;
-    if (mixer) {
-        if (li == 0) {
-            rin = reinterpret_cast<const uint32_t*>(p.x_in)[at];
-        } else {
-            uint64_t v[1];
-            ok = load_tagged<1, 1>(v, p.xw + (size_t)li * H / 2 + at, 1, epoch, p.error, p.limit_ticks);
-            rin = (uint32_t)v[0];
-        }
-    }
     // No wait for the gate/up phase: the staging below reads every activation
     // word until it carries this launch's epoch (a word is complete when its
     // tag is), so the down rows start as soon as the task's own words are in.
@@ -1271,7 +1297,7 @@ __device__ __forceinline__ bool combine_task_fused(const DecodeParams& p, uint32
             }
         }
         const uint32_t o = add_bf16(mix, sh.res[gg]);
-        const uint32_t xn = add_bf16((rin >> (16 * (gg & 1))) & 0xffffu, o);
+        const uint32_t xn = add_bf16((sh.rin[gg] >> (16 * (gg & 1))) & 0xffffu, o);
         const uint32_t o_odd = (uint32_t)__shfl_xor((int)o, 1, kWave);
         const uint32_t x_odd = (uint32_t)__shfl_xor((int)xn, 1, kWave);
         if ((gg & 1) == 0) {

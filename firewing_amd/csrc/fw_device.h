@@ -44,7 +44,9 @@ constexpr int kDppRowShl1 = 0x101, kDppRowShl2 = 0x102, kDppRowShl4 = 0x104, kDp
 constexpr int kDppRowMirror = 0x140, kDppRowHalfMirror = 0x141;
 constexpr int kDppRowBcast15 = 0x142, kDppRowBcast31 = 0x143;
 constexpr int kDppQuadXor1 = 0xB1, kDppQuadXor2 = 0x4E;  // quad_perm [1,0,3,2], [2,3,0,1]
-constexpr int kDppRowRor4 = 0x124;                       // lane (i + 4) mod 16 of the row
+// row_ror:n moves values n lanes up the 16-lane row: lane i reads lane
+// (i - n) mod 16. Reading lane (i + 4) mod 16 is therefore row_ror:12.
+constexpr int kDppRowRead4 = 0x12C;                      // lane (i + 4) mod 16 of the row
 
 // v from lane (i + n) of the same 16-lane row (0 past the row's end).
 template <int CTRL>

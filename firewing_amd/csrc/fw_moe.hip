@@ -13,12 +13,14 @@
 #include <cstring>
 #include <new>
 #include <string>
+#include <type_traits>
 #include <vector>
 
 #include "../../include/firewing_hip_moe.h"
 #include "fw_decode.h"
 #include "fw_device.h"
 #include "fw_numerics.h"
+#include "fw_prefill.h"
 #include "fw_synth.h"
 
 using namespace fw;
@@ -327,6 +329,15 @@ struct firewing_hip_context {
     DecodeParams last_params{};
     bool params_valid = false;
     double timeout_seconds = 10.0;  // per dependency wait (FIREWING_WAIT_TIMEOUT_S)
+    // many-token (prefill) scratch, grown to the largest token count seen
+    struct Prefill {
+        size_t tokens = 0;  // capacity
+        uint16_t *x = nullptr, *out = nullptr, *mixture = nullptr, *logits = nullptr, *gate = nullptr;
+        uint16_t *scores = nullptr, *act = nullptr, *weighted = nullptr;
+        int32_t* ids = nullptr;
+        PfGroups g{};
+        std::vector<void*> owned;
+    } pf;
 };
 
 namespace {
@@ -467,6 +478,7 @@ void launch_decode(firewing_hip_context* c, size_t first, size_t n, int T, int o
     if (kt != 1) roles(kt);
     p.n_gu = p.n_shared + (p.cpairs > 0 ? p.nb_rows + p.n_c : p.n_b);
     p.cu_count = c->cu_count;
+    p.input_by_tags = p.cpairs > 0 ? 1 : 0;
     p.trace = c->trace;
     // The kernel reads its parameters from a device copy; upload only on change
     // (the copy is stream-ordered before the launch; pageable source, staged).
@@ -819,6 +831,8 @@ void firewing_hip_destroy(firewing_hip_context* c) {
                     c->error, c->d_params};
     for (void* b : bufs)
         if (b) (void)hipFree(b);
+    for (void* b : c->pf.owned)
+        if (b) (void)hipFree(b);
     if (c->stream) (void)hipStreamDestroy(c->stream);
     delete c;
 }
@@ -1010,6 +1024,181 @@ bool firewing_hip_mixture_bf16(firewing_hip_context* c, size_t layer, const uint
                            dw.as<uint16_t>(), (int)count, (int)H, dmix.as<uint16_t>());
         check(hipGetLastError(), "k_mixture launch");
         download(mixture, dmix.ptr, H * 2, s);
+        check(hipStreamSynchronize(s), "hipStreamSynchronize");
+        return true;
+    });
+}
+
+// ---- many-token block (prefill) ----
+
+static constexpr size_t kMaxPrefillTokens = 65536;
+
+static bool prefill_args_ok(firewing_hip_context* c, size_t layer, size_t tokens, int order, std::string* why) {
+    if (!c) {
+        *why = "null context";
+        return false;
+    }
+    const firewing_hip_shape& sh = c->shape;
+    if (tokens == 0 || tokens > kMaxPrefillTokens) {
+        *why = "tokens must be in [1, 65536]";
+        return false;
+    }
+    if (order != FIREWING_HIP_LOGITS_TREE32) {
+        *why = "the many-token block computes the in-model (TREE32) logits only";
+        return false;
+    }
+    if (layer >= sh.layers) {
+        *why = "layer out of range";
+        return false;
+    }
+    if (sh.hidden % 128 || sh.intermediate % 64 || sh.shared_intermediate % 64) {
+        *why = "the many-token block needs hidden % 128 == 0 and intermediate sizes % 64 == 0";
+        return false;
+    }
+    return true;
+}
+
+// Scratch for `tokens` tokens (grown, never shrunk).
+static void prefill_reserve(firewing_hip_context* c, size_t tokens) {
+    auto& f = c->pf;
+    if (f.tokens >= tokens) return;
+    check(hipStreamSynchronize(c->stream), "hipStreamSynchronize");
+    for (void* b : f.owned)
+        if (b) (void)hipFree(b);
+    f.owned.clear();
+    const firewing_hip_shape& sh = c->shape;
+    const size_t T = tokens, H = sh.hidden, E = sh.experts, K = sh.top_k;
+    const size_t Imax = std::max(sh.intermediate, sh.shared_intermediate);
+    const size_t P = T * K + T, G = E + 1, tiles = P / kPfTileM + G + 1;
+    auto take = [&](auto*& ptr, size_t count) {
+        using T_ = std::remove_pointer_t<std::remove_reference_t<decltype(ptr)>>;
+        ptr = dalloc<T_>(count);
+        f.owned.push_back(ptr);
+    };
+    take(f.x, T * H);
+    take(f.out, T * H);
+    take(f.mixture, T * H);
+    take(f.logits, T * E);
+    take(f.gate, T);
+    take(f.scores, T * K);
+    take(f.ids, T * K);
+    take(f.act, P * Imax);
+    take(f.weighted, P * H);
+    take(f.g.counts, G);
+    take(f.g.cursor, G);
+    take(f.g.offsets, G + 1);
+    take(f.g.tile_group, tiles);
+    take(f.g.tile_row0, tiles);
+    take(f.g.tiles, 1);
+    take(f.g.pair_token, P);
+    take(f.g.pair_scale, P);
+    take(f.g.pair_of, T * K);
+    f.tokens = tokens;
+}
+
+// The many-token block on device buffers x [T][H] -> out [T][H]; the
+// selection stays in c->pf (ids, scores, logits, gate logits, mixture).
+static void launch_prefill(firewing_hip_context* c, size_t layer, const uint16_t* x, size_t tokens, uint16_t* out,
+                           bool keep_mixture, hipStream_t s) {
+    auto& f = c->pf;
+    const firewing_hip_shape& sh = c->shape;
+    const int T = (int)tokens, H = (int)sh.hidden, E = (int)sh.experts, K = (int)sh.top_k;
+    const int I = (int)sh.intermediate, Is = (int)sh.shared_intermediate, Imax = std::max(I, Is);
+    const int P = T * K + T, G = E + 1, max_tiles = P / kPfTileM + G + 1;
+    hipLaunchKernelGGL(k_pf_router, dim3((T + kPfRouterTokens - 1) / kPfRouterTokens, (G + kPfRouterRows - 1) / kPfRouterRows),
+                       dim3(256), 0, s, x, T, H, c->router[layer], E, f.logits, f.gate);
+    check(hipGetLastError(), "k_pf_router launch");
+    hipLaunchKernelGGL(k_select, dim3(T), dim3(64), 0, s, f.logits, E, K, f.ids, f.scores, 1, c->error);
+    check(hipGetLastError(), "k_select launch");
+    hipLaunchKernelGGL(k_pf_zero, dim3((G + 255) / 256), dim3(256), 0, s, f.g.counts, G);
+    hipLaunchKernelGGL(k_pf_zero, dim3((G + 255) / 256), dim3(256), 0, s, f.g.cursor, G);
+    hipLaunchKernelGGL(k_pf_count, dim3((T * K + 255) / 256), dim3(256), 0, s, f.ids, T * K, E, f.g.counts);
+    hipLaunchKernelGGL(k_pf_scan, dim3(1), dim3(1024), 0, s, f.g, E, T);
+    hipLaunchKernelGGL(k_pf_scatter, dim3((P + 255) / 256), dim3(256), 0, s, f.g, f.ids, f.scores, f.gate, T, K, E);
+    check(hipGetLastError(), "grouping launch");
+    PfGemm gu{};
+    gu.a = x;
+    gu.lda = H;
+    gu.w_routed = c->gate_up[layer];
+    gu.w_shared = c->shared_gate[layer];  // shared_up follows it in the same allocation
+    gu.I = I;
+    gu.Is = Is;
+    gu.H = H;
+    gu.E = E;
+    gu.out = f.act;
+    gu.ldo = Imax;
+    gu.n_tiles = Imax / 64;
+    hipLaunchKernelGGL(k_pf_gemm<kPfGateUp>, dim3(max_tiles * gu.n_tiles), dim3(256), 0, s, gu, f.g);
+    check(hipGetLastError(), "k_pf_gemm gate/up launch");
+    PfGemm dn = gu;
+    dn.a = f.act;
+    dn.lda = Imax;
+    dn.w_routed = c->down[layer];
+    dn.w_shared = c->shared_down[layer];
+    dn.out = f.weighted;
+    dn.ldo = H;
+    dn.n_tiles = H / kPfTileN;
+    hipLaunchKernelGGL(k_pf_gemm<kPfDown>, dim3(max_tiles * dn.n_tiles), dim3(256), 0, s, dn, f.g);
+    check(hipGetLastError(), "k_pf_gemm down launch");
+    hipLaunchKernelGGL(k_pf_combine, dim3(T), dim3(256), 0, s, f.weighted, f.g, T, K, H, E, out,
+                       keep_mixture ? f.mixture : nullptr);
+    check(hipGetLastError(), "k_pf_combine launch");
+}
+
+bool firewing_hip_prefill_block_dev(firewing_hip_context* c, size_t layer, const uint16_t* hidden, size_t tokens,
+                                    uint16_t* out, int32_t* ids, uint16_t* scores, void* stream) {
+    return guarded([&] {
+        std::string why;
+        if (!prefill_args_ok(c, layer, tokens, FIREWING_HIP_LOGITS_TREE32, &why)) return fail("prefill_block: " + why);
+        if (!hidden || !out) return fail("prefill_block: null pointer");
+        if (reinterpret_cast<uintptr_t>(hidden) % 16 || reinterpret_cast<uintptr_t>(out) % 16)
+            return fail("prefill_block: hidden and out must be 16-byte aligned");
+        hipStream_t s = stream ? static_cast<hipStream_t>(stream) : c->stream;
+        if (s != c->stream) {
+            // the scratch may be reallocated: order it after the caller's stream
+            check(hipStreamSynchronize(s), "hipStreamSynchronize");
+        }
+        prefill_reserve(c, tokens);
+        const size_t K = c->shape.top_k;
+        launch_prefill(c, layer, hidden, tokens, out, false, s);
+        if (ids) check(hipMemcpyAsync(ids, c->pf.ids, tokens * K * 4, hipMemcpyDeviceToDevice, s), "copy ids");
+        if (scores) check(hipMemcpyAsync(scores, c->pf.scores, tokens * K * 2, hipMemcpyDeviceToDevice, s), "copy scores");
+        return true;
+    });
+}
+
+bool firewing_hip_prefill_block(firewing_hip_context* c, size_t layer, const uint16_t* hidden, size_t tokens,
+                                uint16_t* out, firewing_hip_block_captures* cap) {
+    return guarded([&] {
+        std::string why;
+        if (!prefill_args_ok(c, layer, tokens, FIREWING_HIP_LOGITS_TREE32, &why)) return fail("prefill_block: " + why);
+        if (!hidden || !out) return fail("prefill_block: null pointer");
+        hipStream_t s = c->stream;
+        prefill_reserve(c, tokens);
+        const size_t H = c->shape.hidden, E = c->shape.experts, K = c->shape.top_k;
+        auto& f = c->pf;
+        upload(f.x, hidden, tokens * H * 2, s);
+        launch_prefill(c, layer, f.x, tokens, f.out, cap && cap->routed_mixture, s);
+        if (!check_device_error(c, s)) return false;
+        download(out, f.out, tokens * H * 2, s);
+        if (cap) {
+            if (cap->router_logits) download(cap->router_logits, f.logits, tokens * E * 2, s);
+            if (cap->selected_experts) {
+                std::vector<int32_t> v(tokens * K);
+                download(v.data(), f.ids, v.size() * 4, s);
+                check(hipStreamSynchronize(s), "hipStreamSynchronize");
+                for (size_t i = 0; i < v.size(); ++i) cap->selected_experts[i] = (size_t)v[i];
+            }
+            if (cap->selected_scores) download(cap->selected_scores, f.scores, tokens * K * 2, s);
+            if (cap->routed_mixture) download(cap->routed_mixture, f.mixture, tokens * H * 2, s);
+            if (cap->shared_gate_sigmoid) {
+                // the shared group's pairs follow the routed ones, in token order
+                int32_t off = 0;
+                download(&off, f.g.offsets + E, 4, s);
+                check(hipStreamSynchronize(s), "hipStreamSynchronize");
+                download(cap->shared_gate_sigmoid, f.g.pair_scale + off, tokens * 2, s);
+            }
+        }
         check(hipStreamSynchronize(s), "hipStreamSynchronize");
         return true;
     });

@@ -80,6 +80,8 @@ _SIGNATURES = {
     "firewing_hip_sparse_moe_block": (_b, [_vp, _sz, _u16p, _sz, ctypes.c_int, _u16p,
                                            ctypes.POINTER(BlockCaptures)]),
     "firewing_hip_sparse_moe_block_dev": (_b, [_vp, _sz, _vp, _sz, ctypes.c_int, _vp, _vp]),
+    "firewing_hip_prefill_block": (_b, [_vp, _sz, _u16p, _sz, _u16p, ctypes.POINTER(BlockCaptures)]),
+    "firewing_hip_prefill_block_dev": (_b, [_vp, _sz, _vp, _sz, _vp, _vp, _vp, _vp]),
     "firewing_hip_moe_step_dev": (_b, [_vp, _vp, _sz, ctypes.c_int, _b, _vp, _vp, _vp, _vp, _vp]),
     "firewing_hip_moe_step": (_b, [_vp, _u16p, _sz, ctypes.c_int, _b, _u16p, _u16p, _vp, _u16p]),
     "firewing_hip_synchronize": (_b, [_vp]),
@@ -322,6 +324,28 @@ class MoeContext:
                              stream=None) -> None:
         _call("firewing_hip_sparse_moe_block_dev", self._h, layer, _addr(hidden), tokens, order,
               _addr(out), _addr(stream))
+
+    def prefill_block(self, layer: int, hidden) -> dict:
+        """The many-token block (any T): ids, scores and logits bit-exact, outputs
+        within the MFMA accumulation tolerance."""
+        x = _u16(hidden).reshape(-1, self.H)
+        T = x.shape[0]
+        out = np.empty((T, self.H), dtype=np.uint16)
+        logits = np.empty((T, self.E), dtype=np.uint16)
+        ids = np.empty((T, self.K), dtype=np.uint64)
+        scores = np.empty((T, self.K), dtype=np.uint16)
+        mixture = np.empty((T, self.H), dtype=np.uint16)
+        sig = np.empty(T, dtype=np.uint16)
+        cap = BlockCaptures(logits.ctypes.data, ids.ctypes.data, scores.ctypes.data, mixture.ctypes.data,
+                            sig.ctypes.data)
+        _call("firewing_hip_prefill_block", self._h, layer, _p16(x), T, _p16(out), ctypes.byref(cap))
+        return {"out": out, "router_logits": logits, "selected_experts": ids.astype(np.int64),
+                "selected_scores": scores, "routed_mixture": mixture, "shared_gate_sigmoid": sig}
+
+    def prefill_block_dev(self, layer: int, hidden, tokens: int, out, ids=None, scores=None,
+                          stream=None) -> None:
+        _call("firewing_hip_prefill_block_dev", self._h, layer, _addr(hidden), tokens, _addr(out),
+              _addr(ids), _addr(scores), _addr(stream))
 
     def moe_step(self, hidden, order: int = LOGITS_TREE32, bias_feature: bool = True):
         """All resident layers chained; returns (residual [T,H], block outputs [L,T,H],

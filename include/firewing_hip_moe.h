@@ -160,6 +160,26 @@ bool firewing_hip_sparse_moe_block_dev(firewing_hip_context* ctx, size_t layer,
                                        const uint16_t* hidden, size_t tokens, int order,
                                        uint16_t* out, void* stream);
 
+/* One sparse-MoE block for many tokens (prefill, T in [1, 65536]) on a
+ * resident layer: the same block as firewing_hip_sparse_moe_block
+ * (src/decoder_layer.rs:460-586 with the in-model TREE32 logits; the reference
+ * runs it token by token), arranged for MFMA: exact router logits, top-k and
+ * scores (bit-exact: src/decoder_layer.rs:278-322), (token, expert) pairs
+ * grouped by expert, grouped bf16 GEMMs for gate/up (+ SwiGLU) and down
+ * (+ route weight), the shared expert as one more group, and the
+ * ascending-id bf16 combine (src/expert.rs:906-956). The expert GEMMs
+ * accumulate in the matrix units' order, so block outputs match the reference
+ * within a bf16 tolerance rather than bit for bit. Host buffers, synchronous;
+ * captures as firewing_hip_sparse_moe_block (routed_mixture supported). */
+bool firewing_hip_prefill_block(firewing_hip_context* ctx, size_t layer, const uint16_t* hidden,
+                                size_t tokens, uint16_t* out, firewing_hip_block_captures* captures);
+
+/* Device-pointer variant: hidden [T, H] and out [T, H] in HBM (16-byte
+ * aligned); ids [T, K] (int32, rank order) and scores [T, K] may be NULL. */
+bool firewing_hip_prefill_block_dev(firewing_hip_context* ctx, size_t layer, const uint16_t* hidden,
+                                    size_t tokens, uint16_t* out, int32_t* ids, uint16_t* scores,
+                                    void* stream);
+
 /* All resident layers for T <= 4 tokens in one persistent launch: the
  * 48-layer decode step the overlap benches emulate with 48 execute_exact()
  * calls (src/overlap_bound.rs:732-734). Layers are chained by a pre-norm

@@ -217,6 +217,55 @@ def test_step_tiny_chained(tiny_ctx):
     assert first_diff(resid, cur) is None
 
 
+def _norms_with_tree(r, partner3):
+    """bf16 rms_norm of every row of r ([N, H] bf16, no bias feature) with the
+    32-chain sum of squares (TREE32) whose third tree level adds chain
+    partner3[j] to chain j (j + 4 in the reference)."""
+    v = (np.asarray(r, np.uint16).astype(np.uint32) << 16).view(np.float32)
+    n, H = v.shape
+    acc = np.zeros((n, 32), np.float32)
+    for b in range(H // 32):
+        blk = v[:, 32 * b:32 * b + 32]
+        acc = (acc + (blk * blk).astype(np.float32)).astype(np.float32)
+    a = acc.copy()
+    a[:, :16] = (a[:, :16] + a[:, 16:]).astype(np.float32)
+    a[:, :8] = (a[:, :8] + a[:, 8:16]).astype(np.float32)
+    a[:, :4] = (a[:, :4] + a[:, partner3]).astype(np.float32)
+    ss = ((a[:, 0] + a[:, 1]).astype(np.float32) + (a[:, 2] + a[:, 3]).astype(np.float32)).astype(np.float32)
+    ss = (ss + np.float32(0)).astype(np.float32)
+    inv = (np.float32(1.0) / np.sqrt((ss / np.float32(H) + np.float32(1e-6)).astype(np.float32))).astype(np.float32)
+    bits = (v * inv[:, None]).astype(np.float32).view(np.uint32)
+    return ((bits + 0x7FFF + ((bits >> 16) & 1)) >> 16).astype(np.uint16)
+
+
+def test_step_prenorm_summation_order(tiny_ctx):
+    # A one-ulp change in the sum of squares rarely shows after the bf16
+    # rounding, so the residuals are chosen (on the CPU, from many random
+    # candidates) where it does: those whose normalised vector changes if the
+    # last tree level paired chain j with j ^ 6 (what a DPP row rotate in the
+    # wrong direction gives) instead of j + 4. A wrong pairing in the kernel
+    # then fails every one of them.
+    rng = np.random.default_rng(21)
+    ws = [tiny_weights(rng) for _ in range(3)]
+    for l, w in enumerate(ws):
+        install(tiny_ctx, l, w)
+    H = TINY["hidden"]
+    cand = rng.standard_normal((200000, H)).astype(np.float32).view(np.uint32)
+    cand = ((cand + 0x7FFF + ((cand >> 16) & 1)) >> 16).astype(np.uint16)
+    right = _norms_with_tree(cand, [4, 5, 6, 7])
+    wrong = _norms_with_tree(cand, [6, 7, 4, 5])
+    picked = cand[(right != wrong).any(axis=1)][:32]
+    assert len(picked) >= 8, len(picked)
+    for x in picked[:4]:
+        assert first_diff(fo.rms_norm_bf16(x), _norms_with_tree(x[None], [4, 5, 6, 7])[0]) is None
+    for i in range(0, len(picked) - len(picked) % 4, 4):
+        x4 = picked[i:i + 4]
+        resid, blocks, _, _ = tiny_ctx.moe_step(x4, bias_feature=False)
+        for t in range(4):
+            ref = fo.sparse_moe_block(TINY, ws[0], fo.rms_norm_bf16(x4[t]))
+            assert first_diff(blocks[0, t], ref["out"]) is None, (i + t)
+
+
 def test_step_after_timed_out_launch(tiny_ctx):
     # A wait limit of 10 ns makes the chained step's dependency waits time
     # out (forced from the host; every workgroup still exits). The failed

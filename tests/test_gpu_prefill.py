@@ -1,0 +1,108 @@
+"""GPU parity of the many-token (prefill) block against the CPU oracle.
+
+Router logits, selected ids, scores and the shared-gate sigmoid are exact-order
+computations: bit-exact. The expert GEMMs run on MFMA, whose accumulation order
+differs from the reference's 32-chain order, so block outputs are compared
+within a tolerance: per token, cosine similarity >= 0.9999 and
+max |got - ref| <= 2^-6 * max |ref| (a few bf16 ulps of the token's largest
+output), with the share of bit-identical outputs reported.
+"""
+import numpy as np
+import pytest
+
+from firewing_amd import hip_moe as hm
+from oracle import fw_oracle as fo
+
+pytestmark = pytest.mark.gpu
+
+SEED = 0x46495245
+CFG = dict(hidden=2048, intermediate=512, experts=512, top_k=10, shared_intermediate=512)
+COSINE_MIN = 0.9999
+ABS_FRACTION = 2.0 ** -6
+
+
+def as_f32(bits):
+    return (np.asarray(bits, dtype=np.uint16).astype(np.uint32) << 16).view(np.float32)
+
+
+def output_error(got, ref):
+    """Per-token cosine and max-abs error relative to the token's largest |ref|."""
+    g, r = as_f32(got).astype(np.float64), as_f32(ref).astype(np.float64)
+    cos = (g * r).sum(-1) / np.maximum(np.linalg.norm(g, axis=-1) * np.linalg.norm(r, axis=-1), 1e-30)
+    rel = np.abs(g - r).max(-1) / np.maximum(np.abs(r).max(-1), 1e-30)
+    exact = float((np.asarray(got) == np.asarray(ref)).mean())
+    return cos, rel, exact
+
+
+def assert_close(got, ref, what):
+    cos, rel, exact = output_error(got, ref)
+    msg = f"{what}: min cosine {cos.min():.7f}, max rel {rel.max():.3e}, bit-identical {exact:.4f}"
+    print(msg)
+    assert cos.min() >= COSINE_MIN, msg
+    assert rel.max() <= ABS_FRACTION, msg
+
+
+@pytest.fixture(scope="module")
+def ctx2():
+    with hm.MoeContext(layers=2, **CFG) as ctx:
+        ctx.generate_layers(0, 2, SEED, True)
+        yield ctx
+
+
+@pytest.mark.parametrize("tokens", [1, 5, 37, 300])
+def test_prefill_matches_oracle(ctx2, tokens):
+    x = fo.synth_hidden(SEED, tokens, CFG["hidden"], first_token=5000 + tokens)
+    got = ctx2.prefill_block(1, x)
+    out, ids, scores, logits = fo.synth_block(CFG, SEED, 1, x)
+    assert np.array_equal(got["router_logits"], logits)
+    assert np.array_equal(got["selected_experts"], ids)
+    assert np.array_equal(got["selected_scores"], scores)
+    assert_close(got["out"], out, f"prefill T={tokens}")
+
+
+def test_prefill_agrees_with_decode_block(ctx2):
+    x = fo.synth_hidden(SEED, 4, CFG["hidden"], first_token=77)
+    pf = ctx2.prefill_block(0, x)
+    dec = ctx2.sparse_moe_block(0, x)
+    for key in ("router_logits", "selected_experts", "selected_scores", "shared_gate_sigmoid"):
+        assert np.array_equal(pf[key], dec[key]), key
+    assert_close(pf["out"], dec["out"], "prefill vs decode T=4")
+
+
+def test_prefill_8k_tokens(ctx2):
+    T = 8192
+    x = fo.synth_hidden(SEED, T, CFG["hidden"], first_token=20000)
+    got = ctx2.prefill_block(1, x)
+    ids, scores, logits = fo.synth_route(CFG, SEED, 1, x)
+    assert np.array_equal(got["router_logits"], logits)
+    assert np.array_equal(got["selected_experts"], ids)
+    assert np.array_equal(got["selected_scores"], scores)
+    # popular experts span many 128-pair tiles; the tail ones one partial tile
+    counts = np.bincount(ids.ravel(), minlength=CFG["experts"])
+    assert counts.max() > 4 * 128 and (counts[counts > 0] < 128).any()
+    rng = np.random.default_rng(3)
+    sample = np.sort(np.concatenate([[0, T - 1], rng.choice(T, 14, replace=False)]))
+    out, _, _, _ = fo.synth_block(CFG, SEED, 1, x[sample])
+    assert_close(got["out"][sample], out, "prefill T=8192 (16 sampled tokens)")
+
+
+def test_prefill_device_variant_matches_host(ctx2):
+    from firewing_amd import hip_runtime as rt
+    T = 200
+    x_host = fo.synth_hidden(SEED, T, CFG["hidden"], first_token=900)
+    ref = ctx2.prefill_block(0, x_host)
+    x = rt.DeviceArray.from_numpy(x_host)
+    out = rt.DeviceArray((T, CFG["hidden"]), np.uint16)
+    ids = rt.DeviceArray((T, CFG["top_k"]), np.int32)
+    ctx2.prefill_block_dev(0, x.ptr, T, out.ptr, ids=ids.ptr)
+    ctx2.synchronize()
+    assert np.array_equal(out.numpy(), ref["out"])
+    assert np.array_equal(ids.numpy(), ref["selected_experts"])
+
+
+def test_prefill_rejects_bad_arguments(ctx2):
+    x = fo.synth_hidden(SEED, 8, CFG["hidden"])
+    with pytest.raises(hm.FirewingError, match="layer out of range"):
+        ctx2.prefill_block(2, x)
+    with pytest.raises(hm.FirewingError, match="tokens must be"):
+        ctx2.prefill_block(0, x[:0])
