@@ -1112,9 +1112,11 @@ static void launch_prefill(firewing_hip_context* c, size_t layer, const uint16_t
     check(hipGetLastError(), "k_select launch");
     hipLaunchKernelGGL(k_pf_zero, dim3((G + 255) / 256), dim3(256), 0, s, f.g.counts, G);
     hipLaunchKernelGGL(k_pf_zero, dim3((G + 255) / 256), dim3(256), 0, s, f.g.cursor, G);
-    hipLaunchKernelGGL(k_pf_count, dim3((T * K + 255) / 256), dim3(256), 0, s, f.ids, T * K, E, f.g.counts);
+    const int chunks = (T * K + kPfChunk - 1) / kPfChunk;
+    hipLaunchKernelGGL(k_pf_count, dim3(chunks), dim3(256), 0, s, f.ids, T * K, E, f.g.counts);
     hipLaunchKernelGGL(k_pf_scan, dim3(1), dim3(1024), 0, s, f.g, E, T);
-    hipLaunchKernelGGL(k_pf_scatter, dim3((P + 255) / 256), dim3(256), 0, s, f.g, f.ids, f.scores, f.gate, T, K, E);
+    hipLaunchKernelGGL(k_pf_scatter, dim3(chunks + (T + 255) / 256), dim3(256), 0, s, f.g, f.ids, f.scores, f.gate,
+                       T, K, E);
     check(hipGetLastError(), "grouping launch");
     PfGemm gu{};
     gu.a = x;
@@ -1128,7 +1130,9 @@ static void launch_prefill(firewing_hip_context* c, size_t layer, const uint16_t
     gu.out = f.act;
     gu.ldo = Imax;
     gu.n_tiles = Imax / 64;
-    hipLaunchKernelGGL(k_pf_gemm<kPfGateUp>, dim3(max_tiles * gu.n_tiles), dim3(256), 0, s, gu, f.g);
+    // m-tiles rounded up to the XCD count (the grid's XCD-aware order)
+    const int m_grid = (max_tiles + kPfXcds - 1) / kPfXcds * kPfXcds;
+    hipLaunchKernelGGL(k_pf_gemm<kPfGateUp>, dim3(m_grid * gu.n_tiles), dim3(256), 0, s, gu, f.g);
     check(hipGetLastError(), "k_pf_gemm gate/up launch");
     PfGemm dn = gu;
     dn.a = f.act;
@@ -1138,7 +1142,7 @@ static void launch_prefill(firewing_hip_context* c, size_t layer, const uint16_t
     dn.out = f.weighted;
     dn.ldo = H;
     dn.n_tiles = H / kPfTileN;
-    hipLaunchKernelGGL(k_pf_gemm<kPfDown>, dim3(max_tiles * dn.n_tiles), dim3(256), 0, s, dn, f.g);
+    hipLaunchKernelGGL(k_pf_gemm<kPfDown>, dim3(m_grid * dn.n_tiles), dim3(256), 0, s, dn, f.g);
     check(hipGetLastError(), "k_pf_gemm down launch");
     hipLaunchKernelGGL(k_pf_combine, dim3(T), dim3(256), 0, s, f.weighted, f.g, T, K, H, E, out,
                        keep_mixture ? f.mixture : nullptr);

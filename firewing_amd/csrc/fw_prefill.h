@@ -126,15 +126,27 @@ __global__ void k_pf_zero(int32_t* __restrict__ a, int n) {
     if (i < n) a[i] = 0;
 }
 
-// (ids outside [0, E) occur only when the top-k rejected a NaN logit and left
+// Selections per expert. Each block takes kPfChunk pairs, counts them in an
+// LDS histogram and adds its nonzero bins to the global counts (popular
+// experts would otherwise serialise thousands of atomics on one address).
+// Ids outside [0, E) occur only when the top-k rejected a NaN logit and left
 // them unwritten; such a launch reports the error and its results are void,
-// but every access stays in bounds)
-__global__ void k_pf_count(const int32_t* __restrict__ ids, int n, int E, int32_t* __restrict__ counts) {
-    const int i = (int)(blockIdx.x * blockDim.x + threadIdx.x);
-    if (i < n) {
+// but every access stays in bounds.
+constexpr int kPfChunk = 4096;
+
+__global__ void __launch_bounds__(256) k_pf_count(const int32_t* __restrict__ ids, int n, int E,
+                                                  int32_t* __restrict__ counts) {
+    __shared__ int32_t hist[kMaxExperts];
+    for (int e = (int)threadIdx.x; e < E; e += 256) hist[e] = 0;
+    __syncthreads();
+    const int i0 = (int)blockIdx.x * kPfChunk, i1 = min(n, i0 + kPfChunk);
+    for (int i = i0 + (int)threadIdx.x; i < i1; i += 256) {
         const int e = ids[i];
-        if (e >= 0 && e < E) atomicAdd(&counts[e], 1);
+        if (e >= 0 && e < E) atomicAdd(&hist[e], 1);
     }
+    __syncthreads();
+    for (int e = (int)threadIdx.x; e < E; e += 256)
+        if (hist[e] != 0) atomicAdd(&counts[e], hist[e]);
 }
 
 // One block of 1024 threads: exclusive scans of the group sizes (pairs and
@@ -183,29 +195,55 @@ __global__ void __launch_bounds__(1024) k_pf_scan(PfGroups g, int E, int T) {
 }
 
 // Pair p of group e for every (token, rank) selection, and the shared group's
-// pair for every token. The order of pairs inside a group follows the
-// atomics; no result depends on it.
-__global__ void k_pf_scatter(PfGroups g, const int32_t* __restrict__ ids, const uint16_t* __restrict__ scores,
-                             const uint16_t* __restrict__ gate_logit, int T, int K, int E) {
-    const int i = (int)(blockIdx.x * blockDim.x + threadIdx.x);
-    if (i < T * K) {
-        const int t = i / K, k = i - t * K;
-        const int e = ids[i];
-        if (e < 0 || e >= E) return;
-        const int slot = g.offsets[e] + atomicAdd(&g.cursor[e], 1);
+// pair for every token. A block takes kPfChunk selections: it ranks them per
+// expert in LDS, reserves one range per expert in the group with a single
+// global atomic, and places each selection at its range + rank. The order of
+// pairs inside a group follows the atomics; no result depends on it.
+__global__ void __launch_bounds__(256) k_pf_scatter(PfGroups g, const int32_t* __restrict__ ids,
+                                                    const uint16_t* __restrict__ scores,
+                                                    const uint16_t* __restrict__ gate_logit, int T, int K, int E) {
+    __shared__ int32_t hist[kMaxExperts];
+    const int n = T * K;
+    const int chunks = (n + kPfChunk - 1) / kPfChunk;
+    if ((int)blockIdx.x >= chunks) {
+        // the shared group: token t is pair offsets[E] + t
+        const int t = ((int)blockIdx.x - chunks) * 256 + (int)threadIdx.x;
+        if (t < T) {
+            const int slot = g.offsets[E] + t;
+            g.pair_token[slot] = t;
+            // src/decoder_layer.rs:563-575: sigmoid of the shared_expert_gate logit
+            g.pair_scale[slot] = sigmoid_bf16(gate_logit[t], c_exp2_table);
+        }
+        return;
+    }
+    for (int e = (int)threadIdx.x; e < E; e += 256) hist[e] = 0;
+    __syncthreads();
+    const int i0 = (int)blockIdx.x * kPfChunk, i1 = min(n, i0 + kPfChunk);
+    constexpr int kPer = kPfChunk / 256;
+    int rank[kPer];
+#pragma unroll
+    for (int u = 0; u < kPer; ++u) {
+        const int i = i0 + (int)threadIdx.x + 256 * u;
+        const int e = i < i1 ? ids[i] : -1;
+        rank[u] = (e >= 0 && e < E) ? atomicAdd(&hist[e], 1) : -1;
+    }
+    __syncthreads();
+    // reserve this block's range in each expert's group
+    for (int e = (int)threadIdx.x; e < E; e += 256)
+        if (hist[e] != 0) hist[e] = g.offsets[e] + atomicAdd(&g.cursor[e], hist[e]);
+    __syncthreads();
+#pragma unroll
+    for (int u = 0; u < kPer; ++u) {
+        if (rank[u] < 0) continue;
+        const int i = i0 + (int)threadIdx.x + 256 * u;
+        const int t = i / K, e = ids[i];
+        const int slot = hist[e] + rank[u];
         g.pair_token[slot] = t;
         g.pair_scale[slot] = scores[i];
         // the expert's position among the token's experts in ascending id
         int asc = 0;
         for (int j = 0; j < K; ++j) asc += ids[t * K + j] < e ? 1 : 0;
         if (asc < K) g.pair_of[t * K + asc] = slot;
-        (void)k;
-    } else if (i < T * K + T) {
-        const int t = i - T * K;
-        const int slot = g.offsets[E] + t;
-        g.pair_token[slot] = t;
-        // src/decoder_layer.rs:563-575: sigmoid of the shared_expert_gate logit
-        g.pair_scale[slot] = sigmoid_bf16(gate_logit[t], c_exp2_table);
     }
 }
 
@@ -213,11 +251,14 @@ __global__ void k_pf_scatter(PfGroups g, const int32_t* __restrict__ ids, const 
 //
 // C[p][n] = sum_k A[p][k] W_g[n][k] for the pairs p of each group g (A rows:
 // the pair's token row of X for gate/up, the pair's activation row for down).
-// Block tile 128 pairs x 128 weight rows x 64 k, four waves of 64 x 64, each
-// 2 x 2 v_mfma_f32_32x32x16_bf16 tiles. Both operands are k-contiguous rows;
-// they travel global -> LDS directly (16 bytes per lane), double-buffered,
-// each 128-byte row chunk stored with its eight 16-byte slots permuted by the
-// row (slot ^ swz(row)) so that the operand reads (32 rows, one slot) spread
+// Block tile 128 pairs x 128 weight rows, four waves of 64 x 64, each 2 x 2
+// v_mfma_f32_32x32x16_bf16 tiles. Both operands are k-contiguous rows; they
+// travel global -> LDS directly (16 bytes per lane) through a ring of
+// kPfStages stages of 32 k, three stages in flight while one is multiplied,
+// so that each workgroup keeps ~48 KB of loads outstanding (the weights are
+// read once per tile row and the workload is bound by streaming them). In a
+// stage each 64-byte row holds its four 16-byte chunks permuted by the row
+// (chunk ^ ((row >> 2) & 3)), so the operand reads (32 rows, one chunk) spread
 // over the LDS banks.
 //
 // kPfGateUp: the tile's weight rows are 64 gate rows and the matching 64 up
@@ -244,16 +285,40 @@ typedef __bf16 pf_bf16x8 __attribute__((ext_vector_type(8)));
 typedef float pf_f32x16 __attribute__((ext_vector_type(16)));
 
 constexpr int kPfTileN = 128;
-constexpr int kPfTileK = 64;
-constexpr int kPfTileBytes = kPfTileM * kPfTileK * 2;  // 16 KB per operand tile
+constexpr int kPfTileK = 32;                           // k per stage
+constexpr int kPfStages = 4;
+constexpr int kPfStageBytes = kPfTileM * kPfTileK * 2;  // 8 KB per operand and stage
 
-__device__ __forceinline__ int pf_swz(int row) { return ((row >> 1) ^ (row << 2)) & 7; }
+__device__ __forceinline__ int pf_swz(int row) { return (row >> 2) & 3; }
+
+// Waits until at most n of this thread's loads are outstanding (n in {0, 4, 8}).
+__device__ __forceinline__ void pf_wait_loads(int n) {
+    if (n >= 8)
+        asm volatile("s_waitcnt vmcnt(8)" ::: "memory");
+    else if (n >= 4)
+        asm volatile("s_waitcnt vmcnt(4)" ::: "memory");
+    else
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+}
+
+// Consecutive workgroups go to the eight XCDs in turn, each XCD with its own
+// L2: workgroup b runs on XCD b % 8. The tiles in use are ordered pair-tile
+// major (all weight tiles of pair tile 0, then of 1, ...; pair tiles are
+// sorted by group) and XCD x takes the x-th eighth of that order: the weight
+// tiles of one pair tile run side by side on one XCD and share its pair rows
+// in L2, and so do the pair tiles of one expert, which share its weights.
+// (Grid: m_grid * n_tiles blocks, m_grid >= the tiles in use, a multiple of 8.)
+constexpr int kPfXcds = 8;
 
 template <int MODE>
 __global__ void __launch_bounds__(256) k_pf_gemm(PfGemm q, PfGroups g) {
-    __shared__ __attribute__((aligned(16))) uint8_t lds[2][2][kPfTileBytes];  // [buffer][A, W]
-    const int mt = (int)blockIdx.x / q.n_tiles, nt = (int)blockIdx.x - mt * q.n_tiles;
-    if (mt >= g.tiles[0]) return;
+    __shared__ __attribute__((aligned(16))) uint8_t lds[kPfStages][2][kPfStageBytes];  // [stage][A, W]
+    const int total = g.tiles[0] * q.n_tiles;
+    const int per = (total + kPfXcds - 1) / kPfXcds;
+    const int seq = (int)blockIdx.x / kPfXcds;
+    const int order = ((int)blockIdx.x % kPfXcds) * per + seq;
+    if (seq >= per || order >= total) return;
+    const int mt = order / q.n_tiles, nt = order - mt * q.n_tiles;
     const int grp = g.tile_group[mt], row0 = g.tile_row0[mt];
     const int rows = min(kPfTileM, g.offsets[grp + 1] - row0);
     const bool shared = grp == q.E;
@@ -271,12 +336,13 @@ __global__ void __launch_bounds__(256) k_pf_gemm(PfGemm q, PfGroups g) {
         wbase = shared ? q.w_shared : q.w_routed + (size_t)grp * q.H * q.I;
     }
     const int tid = (int)threadIdx.x, lane = tid & 63, wv = tid >> 6;
-    // rows this thread's loads cover: wave wv, instruction i -> rows 8 (4 wv + i) + lane / 8
-    const uint16_t* arow[4];
-    const uint16_t* wrow[4];
+    // this thread's loads: wave wv, instruction i -> rows 16 (2 wv + i) + lane / 4, chunk slot lane % 4
+    const uint16_t* arow[2];
+    const uint16_t* wrow[2];
+    int chunk[2];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const int r = 8 * (4 * wv + i) + (lane >> 3);
+    for (int i = 0; i < 2; ++i) {
+        const int r = 16 * (2 * wv + i) + (lane >> 2);
         const int pr = row0 + min(r, rows - 1);
         if constexpr (MODE == kPfGateUp)
             arow[i] = q.a + (size_t)g.pair_token[pr] * q.lda;
@@ -288,18 +354,19 @@ __global__ void __launch_bounds__(256) k_pf_gemm(PfGemm q, PfGroups g) {
         else
             wr = nt * kPfTileN + r;
         wrow[i] = wbase + (size_t)wr * K;
+        chunk[i] = (lane & 3) ^ pf_swz(r);  // the 16-byte chunk this lane's slot holds
     }
-    const int slot = lane & 7;
-    auto load_tile = [&](int buf, int k0) {
+    // (every wave issues the same loads per stage, which the vmcnt waits
+    // below count on: pair rows past the group's end load the group's last
+    // row again, from L2)
+    auto issue = [&](int s, int k0) {
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int r = 8 * (4 * wv + i) + (lane >> 3);
-            const int c = slot ^ pf_swz(r);  // the 16-byte chunk this lane's slot holds
-            __builtin_amdgcn_global_load_lds(reinterpret_cast<const void*>(arow[i] + k0 + 8 * c),
-                                             (__attribute__((address_space(3))) void*)(&lds[buf][0][(4 * wv + i) * 1024]),
+        for (int i = 0; i < 2; ++i) {
+            __builtin_amdgcn_global_load_lds(reinterpret_cast<const void*>(arow[i] + k0 + 8 * chunk[i]),
+                                             (__attribute__((address_space(3))) void*)(&lds[s][0][(2 * wv + i) * 1024]),
                                              16, 0, 0);
-            __builtin_amdgcn_global_load_lds(reinterpret_cast<const void*>(wrow[i] + k0 + 8 * c),
-                                             (__attribute__((address_space(3))) void*)(&lds[buf][1][(4 * wv + i) * 1024]),
+            __builtin_amdgcn_global_load_lds(reinterpret_cast<const void*>(wrow[i] + k0 + 8 * chunk[i]),
+                                             (__attribute__((address_space(3))) void*)(&lds[s][1][(2 * wv + i) * 1024]),
                                              16, 0, 0);
         }
     };
@@ -321,34 +388,35 @@ __global__ void __launch_bounds__(256) k_pf_gemm(PfGemm q, PfGroups g) {
         br[ni] = MODE == kPfGateUp ? 64 * ni + 32 * wn + (lane & 31) : 64 * wn + 32 * ni + (lane & 31);
     const int khalf = lane >> 5;
     const int nk = K / kPfTileK;
-    load_tile(0, 0);
+#pragma unroll
+    for (int s = 0; s < kPfStages - 1; ++s)
+        if (s < nk) issue(s, s * kPfTileK);
     for (int kb = 0; kb < nk; ++kb) {
-        const int buf = kb & 1;
-        // this tile's loads (the only ones in flight) have landed in every wave
-        __builtin_amdgcn_s_waitcnt(0);
-        __syncthreads();
-        if (kb + 1 < nk) load_tile(buf ^ 1, (kb + 1) * kPfTileK);
-        const uint8_t* at = lds[buf][0];
-        const uint8_t* bt = lds[buf][1];
+        // stage kb has landed (4 loads per later stage in flight)
+        pf_wait_loads(4 * min(kPfStages - 2, nk - 1 - kb));
+        // every wave's part of stage kb is in, and every wave is done with
+        // stage kb - 1, whose buffer the issue below refills (an LDS-only
+        // barrier: __syncthreads would also wait for the later stages)
+        wg_sync();
+        if (kb + kPfStages - 1 < nk) issue((kb + kPfStages - 1) % kPfStages, (kb + kPfStages - 1) * kPfTileK);
+        const uint8_t* at = lds[kb % kPfStages][0];
+        const uint8_t* bt = lds[kb % kPfStages][1];
 #pragma unroll
         for (int kk = 0; kk < kPfTileK / 16; ++kk) {
             const int c = 2 * kk + khalf;
             pf_bf16x8 af[2], bf[2];
 #pragma unroll
             for (int mi = 0; mi < 2; ++mi)
-                af[mi] = *reinterpret_cast<const pf_bf16x8*>(at + ar[mi] * 128 + ((c ^ pf_swz(ar[mi])) << 4));
+                af[mi] = *reinterpret_cast<const pf_bf16x8*>(at + ar[mi] * 64 + ((c ^ pf_swz(ar[mi])) << 4));
 #pragma unroll
             for (int ni = 0; ni < 2; ++ni)
-                bf[ni] = *reinterpret_cast<const pf_bf16x8*>(bt + br[ni] * 128 + ((c ^ pf_swz(br[ni])) << 4));
+                bf[ni] = *reinterpret_cast<const pf_bf16x8*>(bt + br[ni] * 64 + ((c ^ pf_swz(br[ni])) << 4));
 #pragma unroll
             for (int mi = 0; mi < 2; ++mi)
 #pragma unroll
                 for (int ni = 0; ni < 2; ++ni)
                     acc[mi][ni] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[mi], bf[ni], acc[mi][ni], 0, 0, 0);
         }
-        // the next iteration's loads overwrite the other buffer only after
-        // this barrier-protected read phase of every wave
-        __syncthreads();
     }
     // epilogue: element e of lane l is C[i][j], i = 8 (e / 4) + 4 (l / 32) + e % 4, j = l % 32
     const int j = lane & 31;
