@@ -1051,8 +1051,8 @@ static bool prefill_args_ok(firewing_hip_context* c, size_t layer, size_t tokens
         *why = "layer out of range";
         return false;
     }
-    if (sh.hidden % 128 || sh.intermediate % 64 || sh.shared_intermediate % 64) {
-        *why = "the many-token block needs hidden % 128 == 0 and intermediate sizes % 64 == 0";
+    if (sh.hidden % 256 || sh.intermediate % 128 || sh.shared_intermediate % 128) {
+        *why = "the many-token block needs hidden % 256 == 0 and intermediate sizes % 128 == 0";
         return false;
     }
     return true;
@@ -1129,10 +1129,20 @@ static void launch_prefill(firewing_hip_context* c, size_t layer, const uint16_t
     gu.E = E;
     gu.out = f.act;
     gu.ldo = Imax;
-    gu.n_tiles = Imax / 64;
+    gu.n_tiles = Imax / kPfActCols;
+    static bool lds_attrs = false;
+    if (!lds_attrs) {
+        check(hipFuncSetAttribute(reinterpret_cast<const void*>(&k_pf_gemm<kPfGateUp>),
+                                  hipFuncAttributeMaxDynamicSharedMemorySize, (int)kPfGemmLds),
+              "hipFuncSetAttribute gate/up");
+        check(hipFuncSetAttribute(reinterpret_cast<const void*>(&k_pf_gemm<kPfDown>),
+                                  hipFuncAttributeMaxDynamicSharedMemorySize, (int)kPfGemmLds),
+              "hipFuncSetAttribute down");
+        lds_attrs = true;
+    }
     // m-tiles rounded up to the XCD count (the grid's XCD-aware order)
     const int m_grid = (max_tiles + kPfXcds - 1) / kPfXcds * kPfXcds;
-    hipLaunchKernelGGL(k_pf_gemm<kPfGateUp>, dim3(m_grid * gu.n_tiles), dim3(256), 0, s, gu, f.g);
+    hipLaunchKernelGGL(k_pf_gemm<kPfGateUp>, dim3(m_grid * gu.n_tiles), dim3(kPfGemmThreads), kPfGemmLds, s, gu, f.g);
     check(hipGetLastError(), "k_pf_gemm gate/up launch");
     PfGemm dn = gu;
     dn.a = f.act;
@@ -1142,7 +1152,7 @@ static void launch_prefill(firewing_hip_context* c, size_t layer, const uint16_t
     dn.out = f.weighted;
     dn.ldo = H;
     dn.n_tiles = H / kPfTileN;
-    hipLaunchKernelGGL(k_pf_gemm<kPfDown>, dim3(m_grid * dn.n_tiles), dim3(256), 0, s, dn, f.g);
+    hipLaunchKernelGGL(k_pf_gemm<kPfDown>, dim3(m_grid * dn.n_tiles), dim3(kPfGemmThreads), kPfGemmLds, s, dn, f.g);
     check(hipGetLastError(), "k_pf_gemm down launch");
     hipLaunchKernelGGL(k_pf_combine, dim3(T), dim3(256), 0, s, f.weighted, f.g, T, K, H, E, out,
                        keep_mixture ? f.mixture : nullptr);

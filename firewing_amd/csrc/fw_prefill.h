@@ -251,17 +251,15 @@ __global__ void __launch_bounds__(256) k_pf_scatter(PfGroups g, const int32_t* _
 //
 // C[p][n] = sum_k A[p][k] W_g[n][k] for the pairs p of each group g (A rows:
 // the pair's token row of X for gate/up, the pair's activation row for down).
-// Block tile 128 pairs x 128 weight rows, four waves of 64 x 64, each 2 x 2
+// Block tile 128 pairs x 256 weight rows, eight waves of 64 x 64, each 2 x 2
 // v_mfma_f32_32x32x16_bf16 tiles. Both operands are k-contiguous rows; they
-// travel global -> LDS directly (16 bytes per lane) through a ring of
-// kPfStages stages of 32 k, three stages in flight while one is multiplied,
-// so that each workgroup keeps ~48 KB of loads outstanding (the weights are
-// read once per tile row and the workload is bound by streaming them). In a
-// stage each 64-byte row holds its four 16-byte chunks permuted by the row
-// (chunk ^ ((row >> 2) & 3)), so the operand reads (32 rows, one chunk) spread
-// over the LDS banks.
+// travel global -> LDS directly (16 bytes per lane) in stages of 64 k, two
+// stages (one loading while the other is multiplied). In a stage each
+// 128-byte row holds its eight 16-byte chunks permuted by the row (chunk ^
+// pf_swz(row)), so the operand reads (32 rows, one chunk) spread over the LDS
+// banks.
 //
-// kPfGateUp: the tile's weight rows are 64 gate rows and the matching 64 up
+// kPfGateUp: the tile's weight rows are 128 gate rows and the matching 128 up
 // rows; the epilogue rounds both to bf16 and writes SwiGLU (src/expert.rs:
 // 562-571) to act[p][n]. kPfDown: the epilogue writes bf16(bf16(C) * scale[p])
 // (route weighting src/decoder_layer.rs:528-545, shared gating 563-575).
@@ -278,28 +276,20 @@ struct PfGemm {
     int E;
     uint16_t* out;              // gate/up: act [P][ldo]; down: weighted rows [P][H]
     int ldo;
-    int n_tiles;                // weight-row tiles per m-tile in the grid
+    int n_tiles;                // weight-row tiles per pair tile
 };
 
 typedef __bf16 pf_bf16x8 __attribute__((ext_vector_type(8)));
 typedef float pf_f32x16 __attribute__((ext_vector_type(16)));
 
-constexpr int kPfTileN = 128;
-constexpr int kPfTileK = 32;                           // k per stage
-constexpr int kPfStages = 4;
-constexpr int kPfStageBytes = kPfTileM * kPfTileK * 2;  // 8 KB per operand and stage
+constexpr int kPfTileN = 256;                            // weight rows per tile
+constexpr int kPfTileK = 64;                             // k per stage
+constexpr int kPfGemmThreads = 512;
+constexpr int kPfABytes = kPfTileM * kPfTileK * 2;       // 16 KB
+constexpr int kPfWBytes = kPfTileN * kPfTileK * 2;       // 32 KB
+constexpr int kPfActCols = kPfTileN / 2;                 // gate/up: activation columns per tile
 
-__device__ __forceinline__ int pf_swz(int row) { return (row >> 2) & 3; }
-
-// Waits until at most n of this thread's loads are outstanding (n in {0, 4, 8}).
-__device__ __forceinline__ void pf_wait_loads(int n) {
-    if (n >= 8)
-        asm volatile("s_waitcnt vmcnt(8)" ::: "memory");
-    else if (n >= 4)
-        asm volatile("s_waitcnt vmcnt(4)" ::: "memory");
-    else
-        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-}
+__device__ __forceinline__ int pf_swz(int row) { return ((row >> 1) ^ (row << 2)) & 7; }
 
 // Consecutive workgroups go to the eight XCDs in turn, each XCD with its own
 // L2: workgroup b runs on XCD b % 8. The tiles in use are ordered pair-tile
@@ -311,8 +301,8 @@ __device__ __forceinline__ void pf_wait_loads(int n) {
 constexpr int kPfXcds = 8;
 
 template <int MODE>
-__global__ void __launch_bounds__(256) k_pf_gemm(PfGemm q, PfGroups g) {
-    __shared__ __attribute__((aligned(16))) uint8_t lds[kPfStages][2][kPfStageBytes];  // [stage][A, W]
+__global__ void __launch_bounds__(kPfGemmThreads) k_pf_gemm(PfGemm q, PfGroups g) {
+    extern __shared__ __attribute__((aligned(16))) uint8_t pf_lds[];  // [2 stages][A | W]
     const int total = g.tiles[0] * q.n_tiles;
     const int per = (total + kPfXcds - 1) / kPfXcds;
     const int seq = (int)blockIdx.x / kPfXcds;
@@ -327,7 +317,7 @@ __global__ void __launch_bounds__(256) k_pf_gemm(PfGemm q, PfGroups g) {
     int K;
     const uint16_t* wbase;
     if constexpr (MODE == kPfGateUp) {
-        if (nt * 64 >= Ig) return;
+        if (nt * kPfActCols >= Ig) return;
         K = q.H;
         wbase = shared ? q.w_shared : q.w_routed + (size_t)grp * 2 * q.I * q.H;
     } else {
@@ -336,39 +326,46 @@ __global__ void __launch_bounds__(256) k_pf_gemm(PfGemm q, PfGroups g) {
         wbase = shared ? q.w_shared : q.w_routed + (size_t)grp * q.H * q.I;
     }
     const int tid = (int)threadIdx.x, lane = tid & 63, wv = tid >> 6;
-    // this thread's loads: wave wv, instruction i -> rows 16 (2 wv + i) + lane / 4, chunk slot lane % 4
+    // this thread's loads per stage: 2 pair-row and 4 weight-row instructions
+    // of the wave, 8 rows each: rows 8 (2 wv + i) + lane / 8 and 8 (4 wv + i) + lane / 8
     const uint16_t* arow[2];
-    const uint16_t* wrow[2];
-    int chunk[2];
+    int achunk[2];
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
-        const int r = 16 * (2 * wv + i) + (lane >> 2);
-        const int pr = row0 + min(r, rows - 1);
+        const int r = 8 * (2 * wv + i) + (lane >> 3);
+        const int pr = row0 + min(r, rows - 1);  // rows past the group's end repeat its last
         if constexpr (MODE == kPfGateUp)
             arow[i] = q.a + (size_t)g.pair_token[pr] * q.lda;
         else
             arow[i] = q.a + (size_t)pr * q.lda;
+        achunk[i] = (lane & 7) ^ pf_swz(r);
+    }
+    const uint16_t* wrow[4];
+    int wchunk[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int r = 8 * (4 * wv + i) + (lane >> 3);
         int wr;
-        if constexpr (MODE == kPfGateUp)
-            wr = r < 64 ? nt * 64 + r : Ig + nt * 64 + (r - 64);  // gate rows, then the up rows
+        if constexpr (MODE == kPfGateUp)  // gate rows, then the up rows
+            wr = r < kPfActCols ? nt * kPfActCols + r : Ig + nt * kPfActCols + (r - kPfActCols);
         else
             wr = nt * kPfTileN + r;
         wrow[i] = wbase + (size_t)wr * K;
-        chunk[i] = (lane & 3) ^ pf_swz(r);  // the 16-byte chunk this lane's slot holds
+        wchunk[i] = (lane & 7) ^ pf_swz(r);
     }
-    // (every wave issues the same loads per stage, which the vmcnt waits
-    // below count on: pair rows past the group's end load the group's last
-    // row again, from L2)
+    auto stage = [&](int s) { return pf_lds + s * (kPfABytes + kPfWBytes); };
     auto issue = [&](int s, int k0) {
+        uint8_t* base = stage(s);
 #pragma unroll
-        for (int i = 0; i < 2; ++i) {
-            __builtin_amdgcn_global_load_lds(reinterpret_cast<const void*>(arow[i] + k0 + 8 * chunk[i]),
-                                             (__attribute__((address_space(3))) void*)(&lds[s][0][(2 * wv + i) * 1024]),
+        for (int i = 0; i < 2; ++i)
+            __builtin_amdgcn_global_load_lds(reinterpret_cast<const void*>(arow[i] + k0 + 8 * achunk[i]),
+                                             (__attribute__((address_space(3))) void*)(base + (2 * wv + i) * 1024),
                                              16, 0, 0);
-            __builtin_amdgcn_global_load_lds(reinterpret_cast<const void*>(wrow[i] + k0 + 8 * chunk[i]),
-                                             (__attribute__((address_space(3))) void*)(&lds[s][1][(2 * wv + i) * 1024]),
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+            __builtin_amdgcn_global_load_lds(reinterpret_cast<const void*>(wrow[i] + k0 + 8 * wchunk[i]),
+                                             (__attribute__((address_space(3))) void*)(base + kPfABytes + (4 * wv + i) * 1024),
                                              16, 0, 0);
-        }
     };
     const int wm = wv & 1, wn = wv >> 1;
     pf_f32x16 acc[2][2];
@@ -378,39 +375,37 @@ __global__ void __launch_bounds__(256) k_pf_gemm(PfGemm q, PfGroups g) {
         for (int ni = 0; ni < 2; ++ni)
 #pragma unroll
             for (int e = 0; e < 16; ++e) acc[mi][ni][e] = 0.0f;
-    // operand rows of this lane: A rows wm*64 + 32 mi + lane % 32; weight rows
-    // (gate/up) 32 wn + lane % 32 and 64 + 32 wn + lane % 32, (down) 64 wn + 32 ni + lane % 32
+    // operand rows of this lane: pair rows wm*64 + 32 mi + lane % 32; weight
+    // rows (gate/up) 32 wn + lane % 32 and 128 + 32 wn + lane % 32, (down)
+    // 64 wn + 32 ni + lane % 32
     int ar[2], br[2];
 #pragma unroll
     for (int mi = 0; mi < 2; ++mi) ar[mi] = wm * 64 + 32 * mi + (lane & 31);
 #pragma unroll
     for (int ni = 0; ni < 2; ++ni)
-        br[ni] = MODE == kPfGateUp ? 64 * ni + 32 * wn + (lane & 31) : 64 * wn + 32 * ni + (lane & 31);
+        br[ni] = MODE == kPfGateUp ? kPfActCols * ni + 32 * wn + (lane & 31) : 64 * wn + 32 * ni + (lane & 31);
     const int khalf = lane >> 5;
     const int nk = K / kPfTileK;
-#pragma unroll
-    for (int s = 0; s < kPfStages - 1; ++s)
-        if (s < nk) issue(s, s * kPfTileK);
+    issue(0, 0);
     for (int kb = 0; kb < nk; ++kb) {
-        // stage kb has landed (4 loads per later stage in flight)
-        pf_wait_loads(4 * min(kPfStages - 2, nk - 1 - kb));
-        // every wave's part of stage kb is in, and every wave is done with
-        // stage kb - 1, whose buffer the issue below refills (an LDS-only
-        // barrier: __syncthreads would also wait for the later stages)
+        // stage kb has landed (the only loads in flight), and every wave is
+        // done with stage kb - 1, whose buffer the issue below refills (an
+        // LDS-only barrier: __syncthreads would also wait for that issue)
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
         wg_sync();
-        if (kb + kPfStages - 1 < nk) issue((kb + kPfStages - 1) % kPfStages, (kb + kPfStages - 1) * kPfTileK);
-        const uint8_t* at = lds[kb % kPfStages][0];
-        const uint8_t* bt = lds[kb % kPfStages][1];
+        if (kb + 1 < nk) issue((kb + 1) & 1, (kb + 1) * kPfTileK);
+        const uint8_t* at = stage(kb & 1);
+        const uint8_t* bt = at + kPfABytes;
 #pragma unroll
         for (int kk = 0; kk < kPfTileK / 16; ++kk) {
             const int c = 2 * kk + khalf;
             pf_bf16x8 af[2], bf[2];
 #pragma unroll
             for (int mi = 0; mi < 2; ++mi)
-                af[mi] = *reinterpret_cast<const pf_bf16x8*>(at + ar[mi] * 64 + ((c ^ pf_swz(ar[mi])) << 4));
+                af[mi] = *reinterpret_cast<const pf_bf16x8*>(at + ar[mi] * 128 + ((c ^ pf_swz(ar[mi])) << 4));
 #pragma unroll
             for (int ni = 0; ni < 2; ++ni)
-                bf[ni] = *reinterpret_cast<const pf_bf16x8*>(bt + br[ni] * 64 + ((c ^ pf_swz(br[ni])) << 4));
+                bf[ni] = *reinterpret_cast<const pf_bf16x8*>(bt + br[ni] * 128 + ((c ^ pf_swz(br[ni])) << 4));
 #pragma unroll
             for (int mi = 0; mi < 2; ++mi)
 #pragma unroll
@@ -430,7 +425,7 @@ __global__ void __launch_bounds__(256) k_pf_gemm(PfGemm q, PfGroups g) {
             const int pr = row0 + r;
             if constexpr (MODE == kPfGateUp) {
                 const uint32_t gb = to_bf16(acc[mi][0][e]), ub = to_bf16(acc[mi][1][e]);
-                q.out[(size_t)pr * q.ldo + nt * 64 + 32 * wn + j] = swiglu_bf16(gb, ub, c_exp2_table);
+                q.out[(size_t)pr * q.ldo + nt * kPfActCols + 32 * wn + j] = swiglu_bf16(gb, ub, c_exp2_table);
             } else {
                 const float scale = from_bf16(g.pair_scale[pr]);
 #pragma unroll
@@ -443,6 +438,8 @@ __global__ void __launch_bounds__(256) k_pf_gemm(PfGemm q, PfGroups g) {
         }
     }
 }
+
+constexpr size_t kPfGemmLds = 2 * (kPfABytes + kPfWBytes);  // 96 KB of dynamic LDS
 
 // ---- combine ---------------------------------------------------------------------------
 
