@@ -334,6 +334,7 @@ struct firewing_hip_context {
         size_t tokens = 0;  // capacity
         uint16_t *x = nullptr, *out = nullptr, *mixture = nullptr, *logits = nullptr, *gate = nullptr;
         uint16_t *scores = nullptr, *act = nullptr, *weighted = nullptr;
+        uint16_t* silu = nullptr;  // the SiLU table (built once)
         int32_t* ids = nullptr;
         PfGroups g{};
         std::vector<void*> owned;
@@ -1093,6 +1094,10 @@ static void prefill_reserve(firewing_hip_context* c, size_t tokens) {
     take(f.g.pair_token, P);
     take(f.g.pair_scale, P);
     take(f.g.pair_of, T * K);
+    take(f.silu, 65536);
+    hipLaunchKernelGGL(k_pf_silu_lut, dim3(256), dim3(256), 0, c->stream, f.silu);
+    check(hipGetLastError(), "k_pf_silu_lut launch");
+    check(hipStreamSynchronize(c->stream), "hipStreamSynchronize");
     f.tokens = tokens;
 }
 
@@ -1130,6 +1135,7 @@ static void launch_prefill(firewing_hip_context* c, size_t layer, const uint16_t
     gu.out = f.act;
     gu.ldo = Imax;
     gu.n_tiles = Imax / kPfActCols;
+    gu.silu = f.silu;
     static bool lds_attrs = false;
     if (!lds_attrs) {
         check(hipFuncSetAttribute(reinterpret_cast<const void*>(&k_pf_gemm<kPfGateUp>),

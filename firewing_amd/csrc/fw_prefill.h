@@ -261,7 +261,7 @@ __global__ void __launch_bounds__(256) k_pf_scatter(PfGroups g, const int32_t* _
 //
 // kPfGateUp: the tile's weight rows are 128 gate rows and the matching 128 up
 // rows; the epilogue rounds both to bf16 and writes SwiGLU (src/expert.rs:
-// 562-571) to act[p][n]. kPfDown: the epilogue writes bf16(bf16(C) * scale[p])
+// 562-571, the SiLU from its 65,536-entry table) to act[p][n]. kPfDown: the epilogue writes bf16(bf16(C) * scale[p])
 // (route weighting src/decoder_layer.rs:528-545, shared gating 563-575).
 
 enum PfGemmMode : int { kPfGateUp = 0, kPfDown = 1 };
@@ -277,7 +277,15 @@ struct PfGemm {
     uint16_t* out;              // gate/up: act [P][ldo]; down: weighted rows [P][H]
     int ldo;
     int n_tiles;                // weight-row tiles per pair tile
+    const uint16_t* silu;       // gate/up: the SiLU table (k_pf_silu_lut)
 };
+
+// silu[b] = silu_bf16(b) for all 65,536 bf16 patterns: the lookup form of
+// src/metal_moe.rs:385-392, equal to the computed SiLU on every input.
+__global__ void k_pf_silu_lut(uint16_t* __restrict__ silu) {
+    const int b = (int)(blockIdx.x * blockDim.x + threadIdx.x);
+    if (b < 65536) silu[b] = silu_bf16((uint32_t)b, c_exp2_table);
+}
 
 typedef __bf16 pf_bf16x8 __attribute__((ext_vector_type(8)));
 typedef float pf_f32x16 __attribute__((ext_vector_type(16)));
@@ -290,6 +298,10 @@ constexpr int kPfWBytes = kPfTileN * kPfTileK * 2;       // 32 KB
 constexpr int kPfActCols = kPfTileN / 2;                 // gate/up: activation columns per tile
 
 __device__ __forceinline__ int pf_swz(int row) { return ((row >> 1) ^ (row << 2)) & 7; }
+
+constexpr int kPfStageLds = 2 * (kPfABytes + kPfWBytes);  // the two stages
+constexpr int kPfOutStride = 72;  // u16 per row of a wave's output tile in LDS (64 + 8: banks)
+static_assert(8 * 64 * kPfOutStride * 2 <= kPfStageLds, "output tiles fit in the stages");
 
 // Consecutive workgroups go to the eight XCDs in turn, each XCD with its own
 // L2: workgroup b runs on XCD b % 8. The tiles in use are ordered pair-tile
@@ -326,6 +338,10 @@ __global__ void __launch_bounds__(kPfGemmThreads) k_pf_gemm(PfGemm q, PfGroups g
         wbase = shared ? q.w_shared : q.w_routed + (size_t)grp * q.H * q.I;
     }
     const int tid = (int)threadIdx.x, lane = tid & 63, wv = tid >> 6;
+    // down: the pair weights of the tile's rows, for the epilogue (ordered
+    // before it by the loop's barriers)
+    float* scales = reinterpret_cast<float*>(pf_lds + kPfStageLds);
+    if (MODE == kPfDown && tid < kPfTileM) scales[tid] = from_bf16(g.pair_scale[row0 + min(tid, rows - 1)]);
     // this thread's loads per stage: 2 pair-row and 4 weight-row instructions
     // of the wave, 8 rows each: rows 8 (2 wv + i) + lane / 8 and 8 (4 wv + i) + lane / 8
     const uint16_t* arow[2];
@@ -413,33 +429,49 @@ __global__ void __launch_bounds__(kPfGemmThreads) k_pf_gemm(PfGemm q, PfGroups g
                     acc[mi][ni] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[mi], bf[ni], acc[mi][ni], 0, 0, 0);
         }
     }
-    // epilogue: element e of lane l is C[i][j], i = 8 (e / 4) + 4 (l / 32) + e % 4, j = l % 32
+    // Epilogue: element e of lane l is C[i][j], i = 8 (e / 4) + 4 (l / 32) +
+    // e % 4, j = l % 32. Each wave writes its results into its own LDS tile
+    // (the stages are free once every wave is past the loop), then stores
+    // them as 16-byte row pieces.
+    wg_sync();
     const int j = lane & 31;
+    uint16_t* ot = reinterpret_cast<uint16_t*>(pf_lds) + wv * 64 * kPfOutStride;
 #pragma unroll
     for (int mi = 0; mi < 2; ++mi) {
 #pragma unroll
         for (int e = 0; e < 16; ++e) {
-            const int i = 8 * (e >> 2) + 4 * khalf + (e & 3);
-            const int r = wm * 64 + 32 * mi + i;
-            if (r >= rows) continue;
-            const int pr = row0 + r;
+            const int r = 32 * mi + 8 * (e >> 2) + 4 * khalf + (e & 3);  // row in the wave's tile
             if constexpr (MODE == kPfGateUp) {
+                // swiglu_bf16 with the SiLU read from its table
                 const uint32_t gb = to_bf16(acc[mi][0][e]), ub = to_bf16(acc[mi][1][e]);
-                q.out[(size_t)pr * q.ldo + nt * kPfActCols + 32 * wn + j] = swiglu_bf16(gb, ub, c_exp2_table);
+                ot[r * kPfOutStride + j] = to_bf16(mul_rn(from_bf16(q.silu[gb]), from_bf16(ub)));
             } else {
-                const float scale = from_bf16(g.pair_scale[pr]);
+                const float scale = scales[wm * 64 + r];
 #pragma unroll
                 for (int ni = 0; ni < 2; ++ni) {
                     const uint32_t y = to_bf16(acc[mi][ni][e]);
-                    q.out[(size_t)pr * q.ldo + nt * kPfTileN + 64 * wn + 32 * ni + j] =
-                        to_bf16(mul_rn(from_bf16(y), scale));
+                    ot[r * kPfOutStride + 32 * ni + j] = to_bf16(mul_rn(from_bf16(y), scale));
                 }
             }
         }
     }
+    // (the wave reads back what its other lanes wrote)
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    constexpr int kPieces = MODE == kPfGateUp ? 4 : 8;  // 16-byte pieces per row of the wave's tile
+#pragma unroll
+    for (int u = 0; u < kPieces; ++u) {
+        const int c = lane + kWave * u, r = c / kPieces, pc = c - r * kPieces;
+        if (wm * 64 + r >= rows) continue;
+        const int pr = row0 + wm * 64 + r;
+        const int col = MODE == kPfGateUp ? nt * kPfActCols + 32 * wn + 8 * pc : nt * kPfTileN + 64 * wn + 8 * pc;
+        *reinterpret_cast<uint4*>(q.out + (size_t)pr * q.ldo + col) =
+            *reinterpret_cast<const uint4*>(ot + r * kPfOutStride + 8 * pc);
+    }
 }
 
-constexpr size_t kPfGemmLds = 2 * (kPfABytes + kPfWBytes);  // 96 KB of dynamic LDS
+constexpr size_t kPfGemmLds = kPfStageLds + kPfTileM * 4;  // 96 KB of stages + the pair scales
 
 // ---- combine ---------------------------------------------------------------------------
 
