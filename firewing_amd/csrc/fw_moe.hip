@@ -336,6 +336,7 @@ struct firewing_hip_context {
         uint16_t *scores = nullptr, *act = nullptr, *weighted = nullptr;
         uint16_t* silu = nullptr;  // the SiLU table (built once)
         int32_t* ids = nullptr;
+        int32_t* redo = nullptr;   // [token tiles][row tiles] of k_pf_router_mx
         PfGroups g{};
         std::vector<void*> owned;
     } pf;
@@ -1083,6 +1084,7 @@ static void prefill_reserve(firewing_hip_context* c, size_t tokens) {
     take(f.gate, T);
     take(f.scores, T * K);
     take(f.ids, T * K);
+    take(f.redo, (T + kPfMxTokens - 1) / kPfMxTokens * ((G + kPfMxRows - 1) / kPfMxRows));
     take(f.act, P * Imax);
     take(f.weighted, P * H);
     take(f.g.counts, G);
@@ -1110,8 +1112,28 @@ static void launch_prefill(firewing_hip_context* c, size_t layer, const uint16_t
     const int T = (int)tokens, H = (int)sh.hidden, E = (int)sh.experts, K = (int)sh.top_k;
     const int I = (int)sh.intermediate, Is = (int)sh.shared_intermediate, Imax = std::max(I, Is);
     const int P = T * K + T, G = E + 1, max_tiles = P / kPfTileM + G + 1;
+    static bool lds_attrs = false;
+    if (!lds_attrs) {
+        check(hipFuncSetAttribute(reinterpret_cast<const void*>(&k_pf_router_mx),
+                                  hipFuncAttributeMaxDynamicSharedMemorySize, (int)kPfMxLds),
+              "hipFuncSetAttribute router");
+        check(hipFuncSetAttribute(reinterpret_cast<const void*>(&k_pf_gemm<kPfGateUp>),
+                                  hipFuncAttributeMaxDynamicSharedMemorySize, (int)kPfGemmLds),
+              "hipFuncSetAttribute gate/up");
+        check(hipFuncSetAttribute(reinterpret_cast<const void*>(&k_pf_gemm<kPfDown>),
+                                  hipFuncAttributeMaxDynamicSharedMemorySize, (int)kPfGemmLds),
+              "hipFuncSetAttribute down");
+        lds_attrs = true;
+    }
+    // router logits on the matrix units; tiles whose inputs could meet a
+    // denormal or an overflow there are recomputed on the vector units
+    const int row_tiles = (G + kPfMxRows - 1) / kPfMxRows;
+    const int mx_tiles = (T + kPfMxTokens - 1) / kPfMxTokens * row_tiles;
+    hipLaunchKernelGGL(k_pf_router_mx, dim3((mx_tiles + 7) / 8 * 8), dim3(256), kPfMxLds, s, x, T, H,
+                       c->router[layer], E, f.logits, f.gate, f.redo, row_tiles);
+    check(hipGetLastError(), "k_pf_router_mx launch");
     hipLaunchKernelGGL(k_pf_router, dim3((T + kPfRouterTokens - 1) / kPfRouterTokens, (G + kPfRouterRows - 1) / kPfRouterRows),
-                       dim3(256), 0, s, x, T, H, c->router[layer], E, f.logits, f.gate);
+                       dim3(256), 0, s, x, T, H, c->router[layer], E, f.logits, f.gate, f.redo, row_tiles);
     check(hipGetLastError(), "k_pf_router launch");
     hipLaunchKernelGGL(k_select, dim3(T), dim3(64), 0, s, f.logits, E, K, f.ids, f.scores, 1, c->error);
     check(hipGetLastError(), "k_select launch");
@@ -1136,16 +1158,6 @@ static void launch_prefill(firewing_hip_context* c, size_t layer, const uint16_t
     gu.ldo = Imax;
     gu.n_tiles = Imax / kPfActCols;
     gu.silu = f.silu;
-    static bool lds_attrs = false;
-    if (!lds_attrs) {
-        check(hipFuncSetAttribute(reinterpret_cast<const void*>(&k_pf_gemm<kPfGateUp>),
-                                  hipFuncAttributeMaxDynamicSharedMemorySize, (int)kPfGemmLds),
-              "hipFuncSetAttribute gate/up");
-        check(hipFuncSetAttribute(reinterpret_cast<const void*>(&k_pf_gemm<kPfDown>),
-                                  hipFuncAttributeMaxDynamicSharedMemorySize, (int)kPfGemmLds),
-              "hipFuncSetAttribute down");
-        lds_attrs = true;
-    }
     // m-tiles rounded up to the XCD count (the grid's XCD-aware order)
     const int m_grid = (max_tiles + kPfXcds - 1) / kPfXcds * kPfXcds;
     hipLaunchKernelGGL(k_pf_gemm<kPfGateUp>, dim3(m_grid * gu.n_tiles), dim3(kPfGemmThreads), kPfGemmLds, s, gu, f.g);

@@ -1,7 +1,8 @@
 // Many-token (prefill) sparse-MoE block: the same block as the decode kernel
 // (src/decoder_layer.rs:460-586) for T > 4 tokens, arranged as
 //
-//   router    exact logits for every (token, router row): k_pf_router
+//   router    exact logits for every (token, router row): k_pf_router_mx on
+//             the matrix units, k_pf_router for tiles it flags
 //   select    top-k, scores (k_select), shared-gate sigmoid
 //   group     (token, expert) pairs grouped by expert, the shared expert as
 //             one more group holding every token: k_pf_count, k_pf_scan,
@@ -36,9 +37,16 @@ constexpr int kPfRouterPad = 32;     // LDS row padding (u16): the two halves of
 // (a2 + a3), + 0.0. Eight groups of 32 lanes per block; group g takes tokens
 // 8 (g & 3) .. and rows 8 (g >> 2) .. of the block's tile, lane l of a group
 // chain bitrev5(l), so the tree's partners are DPP neighbours.
+//
+// With `redo` set, a block runs only if the matrix-unit router below flagged
+// its tile (redo[token tile * redo_rows + row tile], tiles of kPfMxTokens
+// tokens and kPfMxRows rows); it then rewrites that tile's logits.
 __global__ void __launch_bounds__(256) k_pf_router(const uint16_t* __restrict__ x, int T, int H,
                                                    const uint16_t* __restrict__ w, int E,
-                                                   uint16_t* __restrict__ logits, uint16_t* __restrict__ gate) {
+                                                   uint16_t* __restrict__ logits, uint16_t* __restrict__ gate,
+                                                   const int32_t* __restrict__ redo, int redo_rows) {
+    static_assert(kPfRouterTokens == 32 && kPfRouterRows == 16, "redo tile mapping assumes 32 x 16 blocks");
+    if (redo && redo[(int)blockIdx.x * redo_rows + (int)blockIdx.y / 2] == 0) return;
     __shared__ __attribute__((aligned(16))) uint16_t xs[kPfRouterTokens][kPfRouterChunk + kPfRouterPad];
     __shared__ __attribute__((aligned(16))) uint16_t ws[kPfRouterRows][kPfRouterChunk + kPfRouterPad];
     const int tid = (int)threadIdx.x, grp = tid >> 5, lane32 = tid & 31;
@@ -100,6 +108,161 @@ __global__ void __launch_bounds__(256) k_pf_router(const uint16_t* __restrict__ 
                 else
                     gate[t] = to_bf16(d);
             }
+        }
+    }
+}
+
+// ---- router on the matrix units ----------------------------------------------------------
+//
+// The same logits from v_mfma_f32_16x16x1_4b_f32 (four 16 x 16 blocks, K = 1):
+// each MFMA step is d = c + a * b for one (chain, token, row), and a product of
+// two bf16 values is exact in f32, so the step equals the reference's multiply
+// then add with their two roundings (src/expert.rs:514-552) — provided no
+// product or partial sum is denormal (the matrix units flush those to zero) and
+// nothing overflows. A workgroup takes 32 tokens x 32 rows; wave v the 16 x 16
+// output tile (tokens 16 (v & 1), rows 16 (v >> 1)) and all 32 chains of it:
+// chain 8 b + s is block b of accumulator set s, so lane l (block l / 16) feeds
+// its 8 sets from one 16-byte LDS read of columns 32 p + 8 (l / 16) .. + 7, and
+// the chains of output (token 4 (l / 16) + r, row l % 16) all sit in lane l,
+// register 4 b + r of the sets: the tree is register arithmetic.
+//
+// Guard: a tile whose staged x or W holds a nonzero |v| < 2^-55 or |v| >= 2^57
+// (Inf and NaN included) is flagged in redo[] and recomputed by k_pf_router.
+// Otherwise every nonzero product lies in [2^-110, 2^114): products and partial
+// sums are multiples of 2^-125, hence zero or normal, and a chain of H / 32
+// terms stays below 2^114 * H / 32 (finite for H < 2^18).
+constexpr int kPfMxTokens = 32;
+constexpr int kPfMxRows = 32;
+constexpr int kPfMxChunk = 256;              // columns per LDS stage
+constexpr int kPfMxStride = kPfMxChunk + 8;  // u16 per LDS row: 528 B, rows 4 banks apart
+constexpr int kPfMxStageRows = kPfMxTokens + kPfMxRows;
+constexpr size_t kPfMxLds = 2 * (size_t)kPfMxStageRows * kPfMxStride * sizeof(uint16_t);  // 67,584 B
+constexpr uint16_t kPfMxSmall = 0x2400;  // |bf16| bits of 2^-55
+constexpr uint16_t kPfMxLarge = 0x5C00;  // |bf16| bits of 2^57
+
+typedef float fw_v16f __attribute__((ext_vector_type(16)));
+typedef uint16_t fw_u16x2 __attribute__((ext_vector_type(2)));
+
+// Running range of the magnitudes of eight staged bf16 values: lo = min(|v| - 1)
+// (zero wraps to 0xFFFF and never counts as small), hi = max |v|, per u16 half.
+__device__ __forceinline__ void mx_range(const uint4& v, fw_u16x2& lo, fw_u16x2& hi) {
+    const uint32_t words[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        const fw_u16x2 a = __builtin_bit_cast(fw_u16x2, words[q] & 0x7FFF7FFFu);
+        lo = __builtin_elementwise_min(lo, a - (fw_u16x2)(1));
+        hi = __builtin_elementwise_max(hi, a);
+    }
+}
+
+// Grid: 8 * ceil(tiles / 8) blocks of 256 threads, tiles = ceil(T / 32) token
+// tiles x redo_rows = ceil((E + 1) / 32) row tiles; kPfMxLds bytes of dynamic
+// LDS. Block b works on tile (b % 8) * ceil(tiles / 8) + b / 8: each XCD takes
+// a contiguous range of token tiles with all their row tiles, so a token
+// tile's rows are read from HBM once and shared in that XCD's L2.
+__global__ void __launch_bounds__(256, 2) k_pf_router_mx(const uint16_t* __restrict__ x, int T, int H,
+                                                         const uint16_t* __restrict__ w, int E,
+                                                         uint16_t* __restrict__ logits, uint16_t* __restrict__ gate,
+                                                         int32_t* __restrict__ redo, int redo_rows) {
+    extern __shared__ __attribute__((aligned(16))) uint8_t mx_lds[];
+    uint16_t(*stage)[kPfMxStageRows][kPfMxStride] = reinterpret_cast<uint16_t(*)[kPfMxStageRows][kPfMxStride]>(mx_lds);
+    const int total = (T + kPfMxTokens - 1) / kPfMxTokens * redo_rows;
+    const int per = (total + 7) / 8;
+    const int seq = (int)blockIdx.x / 8;
+    const int tile = ((int)blockIdx.x % 8) * per + seq;
+    if (seq >= per || tile >= total) return;
+    const int t0 = tile / redo_rows * kPfMxTokens, r0 = tile % redo_rows * kPfMxRows;
+    const int rows = E + 1;
+    const int tid = (int)threadIdx.x, wv = tid >> 6, lane = tid & 63;
+    const int blk = lane >> 4, idx = lane & 15;
+    const int ti = 16 * (wv & 1), rj = 16 * (wv >> 1);
+
+    // staging: 64 rows (32 token rows, then 32 weight rows) of 32 pieces of 16 B
+    const uint16_t* src[8];
+    int srow[8], spiece[8];
+#pragma unroll
+    for (int q = 0; q < 8; ++q) {
+        const int id = tid + 256 * q, row = id >> 5, pc = id & 31;
+        srow[q] = row;
+        spiece[q] = pc;
+        src[q] = row < kPfMxTokens ? x + (size_t)min(t0 + row, T - 1) * H + 8 * pc
+                                   : w + (size_t)min(r0 + row - kPfMxTokens, rows - 1) * H + 8 * pc;
+    }
+    fw_u16x2 lo = (fw_u16x2)(0xFFFF), hi = (fw_u16x2)(0);
+    uint4 pre[8];
+#pragma unroll
+    for (int q = 0; q < 8; ++q) pre[q] = *reinterpret_cast<const uint4*>(src[q]);
+#pragma unroll
+    for (int q = 0; q < 8; ++q) {
+        mx_range(pre[q], lo, hi);
+        *reinterpret_cast<uint4*>(&stage[0][srow[q]][8 * spiece[q]]) = pre[q];
+    }
+    __syncthreads();
+
+    fw_v16f acc[8];
+#pragma unroll
+    for (int s = 0; s < 8; ++s) acc[s] = (fw_v16f)(0.0f);
+    const int chunks = H / kPfMxChunk;
+    for (int c = 0; c < chunks; ++c) {
+        const int buf = c & 1;
+        const bool more = c + 1 < chunks;
+        if (more) {
+#pragma unroll
+            for (int q = 0; q < 8; ++q) pre[q] = *reinterpret_cast<const uint4*>(src[q] + (size_t)(c + 1) * kPfMxChunk);
+        }
+#pragma unroll 2
+        for (int p = 0; p < kPfMxChunk / 32; ++p) {
+            const uint4 xa = *reinterpret_cast<const uint4*>(&stage[buf][ti + idx][32 * p + 8 * blk]);
+            const uint4 wb = *reinterpret_cast<const uint4*>(&stage[buf][kPfMxTokens + rj + idx][32 * p + 8 * blk]);
+            const uint32_t xw[4] = {xa.x, xa.y, xa.z, xa.w};
+            const uint32_t ww[4] = {wb.x, wb.y, wb.z, wb.w};
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                acc[2 * q] = __builtin_amdgcn_mfma_f32_16x16x1f32(__uint_as_float(xw[q] << 16),
+                                                                  __uint_as_float(ww[q] << 16), acc[2 * q], 0, 0, 0);
+                acc[2 * q + 1] = __builtin_amdgcn_mfma_f32_16x16x1f32(__uint_as_float(xw[q] & 0xFFFF0000u),
+                                                                      __uint_as_float(ww[q] & 0xFFFF0000u),
+                                                                      acc[2 * q + 1], 0, 0, 0);
+            }
+        }
+        if (more) {
+#pragma unroll
+            for (int q = 0; q < 8; ++q) {
+                mx_range(pre[q], lo, hi);
+                *reinterpret_cast<uint4*>(&stage[buf ^ 1][srow[q]][8 * spiece[q]]) = pre[q];
+            }
+        }
+        __syncthreads();
+    }
+
+    const bool risky = min((int)lo.x, (int)lo.y) < kPfMxSmall - 1 || max((int)hi.x, (int)hi.y) >= kPfMxLarge;
+    const int flagged = __syncthreads_or(risky ? 1 : 0);
+    if (tid == 0) redo[tile] = flagged ? 1 : 0;
+    if (flagged) return;
+
+    // tree per output: (c + c+16) + (c+8) + (c+4) for the four low chains, then
+    // ((y0 + y1) + (y2 + y3)) + 0.0; chain 8 b + s is acc[s][4 b + r]
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+        float u[16];
+#pragma unroll
+        for (int c = 0; c < 16; ++c) {
+            const int c2 = c + 16;
+            u[c] = add_rn(acc[c & 7][4 * (c >> 3) + r], acc[c2 & 7][4 * (c2 >> 3) + r]);
+        }
+        float v8[8];
+#pragma unroll
+        for (int c = 0; c < 8; ++c) v8[c] = add_rn(u[c], u[c + 8]);
+        float y[4];
+#pragma unroll
+        for (int c = 0; c < 4; ++c) y[c] = add_rn(v8[c], v8[c + 4]);
+        const float d = add_rn(add_rn(add_rn(y[0], y[1]), add_rn(y[2], y[3])), 0.0f);
+        const int t = t0 + ti + 4 * blk + r, row = r0 + rj + idx;
+        if (t < T && row < rows) {
+            if (row < E)
+                logits[(size_t)t * E + row] = to_bf16(d);
+            else
+                gate[t] = to_bf16(d);
         }
     }
 }

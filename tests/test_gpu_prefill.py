@@ -60,6 +60,33 @@ def test_prefill_matches_oracle(ctx2, tokens):
     assert_close(got["out"], out, f"prefill T={tokens}")
 
 
+def test_prefill_router_guard_tiny_and_large_tokens(ctx2):
+    """The router runs on the matrix units, which flush denormal products and
+    partial sums; tiles holding tiny or huge inputs are recomputed on the vector
+    units. One token is scaled to ~2^-131: |x| < 2^-128 and every router weight
+    is below 4 in magnitude (N(0, 0.02) weights, Zipf bias column at most
+    0.45 ln 513), so every product is denormal and a flushing evaluation would
+    give all-zero logits, while the exact ones are mostly nonzero denormals.
+    Another token, scaled to ~2^58, takes the same recompute path. Router
+    logits, ids and scores stay bit-exact for every token, also in the tiles
+    not flagged."""
+    T = 70
+    x = fo.synth_hidden(SEED, T, CFG["hidden"], first_token=900)
+    f = as_f32(x)
+    tiny, huge = 3, 65
+    x[tiny] = np.array([fo.to_bf16(v) for v in (f[tiny].astype(np.float64) * 2.0 ** -131)], dtype=np.uint16)
+    x[huge] = np.array([fo.to_bf16(v) for v in (f[huge].astype(np.float64) * 2.0 ** 58)], dtype=np.uint16)
+    assert np.abs(as_f32(x[tiny])).max() < 2.0 ** -128
+    assert np.abs(as_f32(fo.synth_router_bias(SEED, 1, CFG["experts"]))).max() < 4.0
+    got = ctx2.prefill_block(1, x)
+    ids, scores, logits = fo.synth_route(CFG, SEED, 1, x)
+    tiny_logits = np.abs(as_f32(logits[tiny]))
+    assert (tiny_logits > 0).sum() > CFG["experts"] // 2 and tiny_logits.max() < 2.0 ** -126
+    assert np.array_equal(got["router_logits"], logits)
+    assert np.array_equal(got["selected_experts"], ids)
+    assert np.array_equal(got["selected_scores"], scores)
+
+
 def test_prefill_agrees_with_decode_block(ctx2):
     x = fo.synth_hidden(SEED, 4, CFG["hidden"], first_token=77)
     pf = ctx2.prefill_block(0, x)
