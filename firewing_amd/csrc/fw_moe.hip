@@ -1129,7 +1129,7 @@ static void launch_prefill(firewing_hip_context* c, size_t layer, const uint16_t
     // denormal or an overflow there are recomputed on the vector units
     const int row_tiles = (G + kPfMxRows - 1) / kPfMxRows;
     const int mx_tiles = (T + kPfMxTokens - 1) / kPfMxTokens * row_tiles;
-    hipLaunchKernelGGL(k_pf_router_mx, dim3((mx_tiles + 7) / 8 * 8), dim3(256), kPfMxLds, s, x, T, H,
+    hipLaunchKernelGGL(k_pf_router_mx, dim3((mx_tiles + 7) / 8 * 8), dim3(kPfMxThreads), kPfMxLds, s, x, T, H,
                        c->router[layer], E, f.logits, f.gate, f.redo, row_tiles);
     check(hipGetLastError(), "k_pf_router_mx launch");
     hipLaunchKernelGGL(k_pf_router, dim3((T + kPfRouterTokens - 1) / kPfRouterTokens, (G + kPfRouterRows - 1) / kPfRouterRows),

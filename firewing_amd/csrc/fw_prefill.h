@@ -119,12 +119,16 @@ __global__ void __launch_bounds__(256) k_pf_router(const uint16_t* __restrict__ 
 // two bf16 values is exact in f32, so the step equals the reference's multiply
 // then add with their two roundings (src/expert.rs:514-552) — provided no
 // product or partial sum is denormal (the matrix units flush those to zero) and
-// nothing overflows. A workgroup takes 32 tokens x 32 rows; wave v the 16 x 16
-// output tile (tokens 16 (v & 1), rows 16 (v >> 1)) and all 32 chains of it:
-// chain 8 b + s is block b of accumulator set s, so lane l (block l / 16) feeds
-// its 8 sets from one 16-byte LDS read of columns 32 p + 8 (l / 16) .. + 7, and
-// the chains of output (token 4 (l / 16) + r, row l % 16) all sit in lane l,
-// register 4 b + r of the sets: the tree is register arithmetic.
+// nothing overflows. A workgroup takes 32 tokens x 32 rows in eight waves:
+// wave v takes the 16 x 16 output tile q = v & 3 (tokens 16 (q & 1), rows
+// 16 (q >> 1)) and the chains 16 h .. 16 h + 15, h = v >> 2. Chain 16 h + 4 b + s
+// is block b of accumulator set s, so lane l (block l / 16) feeds its 4 sets
+// from one 8-byte LDS read of columns 32 p + 16 h + 4 (l / 16) .. + 3, and the
+// chains of output (token 4 (l / 16) + r, row l % 16) sit in lane l, register
+// 4 b + r of the sets. The tree's first level (chain c + chain c + 16) pairs
+// the two halves: the h = 1 wave hands its 64 values over through LDS, and the
+// h = 0 wave finishes the tree in registers. 64 accumulator registers per wave
+// leave room for four waves per SIMD.
 //
 // Guard: a tile whose staged x or W holds a nonzero |v| < 2^-55 or |v| >= 2^57
 // (Inf and NaN included) is flagged in redo[] and recomputed by k_pf_router.
@@ -133,12 +137,15 @@ __global__ void __launch_bounds__(256) k_pf_router(const uint16_t* __restrict__ 
 // terms stays below 2^114 * H / 32 (finite for H < 2^18).
 constexpr int kPfMxTokens = 32;
 constexpr int kPfMxRows = 32;
+constexpr int kPfMxThreads = 512;
 constexpr int kPfMxChunk = 256;              // columns per LDS stage
 constexpr int kPfMxStride = kPfMxChunk + 8;  // u16 per LDS row: 528 B, rows 4 banks apart
 constexpr int kPfMxStageRows = kPfMxTokens + kPfMxRows;
+constexpr int kPfMxPieces = kPfMxStageRows * kPfMxChunk / 8 / kPfMxThreads;  // 16-byte pieces per thread
 constexpr size_t kPfMxLds = 2 * (size_t)kPfMxStageRows * kPfMxStride * sizeof(uint16_t);  // 67,584 B
 constexpr uint16_t kPfMxSmall = 0x2400;  // |bf16| bits of 2^-55
 constexpr uint16_t kPfMxLarge = 0x5C00;  // |bf16| bits of 2^57
+static_assert(4 * 64 * 64 * sizeof(float) <= kPfMxLds, "hand-over area fits in the stages");
 
 typedef float fw_v16f __attribute__((ext_vector_type(16)));
 typedef uint16_t fw_u16x2 __attribute__((ext_vector_type(2)));
@@ -155,15 +162,17 @@ __device__ __forceinline__ void mx_range(const uint4& v, fw_u16x2& lo, fw_u16x2&
     }
 }
 
-// Grid: 8 * ceil(tiles / 8) blocks of 256 threads, tiles = ceil(T / 32) token
-// tiles x redo_rows = ceil((E + 1) / 32) row tiles; kPfMxLds bytes of dynamic
-// LDS. Block b works on tile (b % 8) * ceil(tiles / 8) + b / 8: each XCD takes
-// a contiguous range of token tiles with all their row tiles, so a token
-// tile's rows are read from HBM once and shared in that XCD's L2.
-__global__ void __launch_bounds__(256, 2) k_pf_router_mx(const uint16_t* __restrict__ x, int T, int H,
-                                                         const uint16_t* __restrict__ w, int E,
-                                                         uint16_t* __restrict__ logits, uint16_t* __restrict__ gate,
-                                                         int32_t* __restrict__ redo, int redo_rows) {
+// Grid: 8 * ceil(tiles / 8) blocks of kPfMxThreads threads, tiles =
+// ceil(T / 32) token tiles x redo_rows = ceil((E + 1) / 32) row tiles;
+// kPfMxLds bytes of dynamic LDS. Block b works on tile (b % 8) * ceil(tiles / 8)
+// + b / 8: each XCD takes a contiguous range of token tiles with all their row
+// tiles, so a token tile's rows are read from HBM once and shared in that
+// XCD's L2.
+__global__ void __launch_bounds__(kPfMxThreads, 4) k_pf_router_mx(const uint16_t* __restrict__ x, int T, int H,
+                                                                  const uint16_t* __restrict__ w, int E,
+                                                                  uint16_t* __restrict__ logits,
+                                                                  uint16_t* __restrict__ gate,
+                                                                  int32_t* __restrict__ redo, int redo_rows) {
     extern __shared__ __attribute__((aligned(16))) uint8_t mx_lds[];
     uint16_t(*stage)[kPfMxStageRows][kPfMxStride] = reinterpret_cast<uint16_t(*)[kPfMxStageRows][kPfMxStride]>(mx_lds);
     const int total = (T + kPfMxTokens - 1) / kPfMxTokens * redo_rows;
@@ -175,61 +184,74 @@ __global__ void __launch_bounds__(256, 2) k_pf_router_mx(const uint16_t* __restr
     const int rows = E + 1;
     const int tid = (int)threadIdx.x, wv = tid >> 6, lane = tid & 63;
     const int blk = lane >> 4, idx = lane & 15;
-    const int ti = 16 * (wv & 1), rj = 16 * (wv >> 1);
+    const int quad = wv & 3, half = wv >> 2;
+    const int ti = 16 * (quad & 1), rj = 16 * (quad >> 1);
+    const int col = 16 * half + 4 * blk;  // first column of this lane's chains in a 32-column block
 
     // staging: 64 rows (32 token rows, then 32 weight rows) of 32 pieces of 16 B
-    const uint16_t* src[8];
-    int srow[8], spiece[8];
+    const uint16_t* src[kPfMxPieces];
+    int dst[kPfMxPieces];
 #pragma unroll
-    for (int q = 0; q < 8; ++q) {
-        const int id = tid + 256 * q, row = id >> 5, pc = id & 31;
-        srow[q] = row;
-        spiece[q] = pc;
+    for (int q = 0; q < kPfMxPieces; ++q) {
+        const int id = tid + kPfMxThreads * q, row = id >> 5, pc = id & 31;
+        dst[q] = row * kPfMxStride + 8 * pc;
         src[q] = row < kPfMxTokens ? x + (size_t)min(t0 + row, T - 1) * H + 8 * pc
                                    : w + (size_t)min(r0 + row - kPfMxTokens, rows - 1) * H + 8 * pc;
     }
     fw_u16x2 lo = (fw_u16x2)(0xFFFF), hi = (fw_u16x2)(0);
-    uint4 pre[8];
+    uint4 pre[kPfMxPieces];
 #pragma unroll
-    for (int q = 0; q < 8; ++q) pre[q] = *reinterpret_cast<const uint4*>(src[q]);
+    for (int q = 0; q < kPfMxPieces; ++q) pre[q] = *reinterpret_cast<const uint4*>(src[q]);
 #pragma unroll
-    for (int q = 0; q < 8; ++q) {
+    for (int q = 0; q < kPfMxPieces; ++q) {
         mx_range(pre[q], lo, hi);
-        *reinterpret_cast<uint4*>(&stage[0][srow[q]][8 * spiece[q]]) = pre[q];
+        *reinterpret_cast<uint4*>(&stage[0][0][0] + dst[q]) = pre[q];
     }
     __syncthreads();
 
-    fw_v16f acc[8];
+    fw_v16f acc[4];
 #pragma unroll
-    for (int s = 0; s < 8; ++s) acc[s] = (fw_v16f)(0.0f);
+    for (int s = 0; s < 4; ++s) acc[s] = (fw_v16f)(0.0f);
     const int chunks = H / kPfMxChunk;
+    constexpr int kSteps = kPfMxChunk / 32;
     for (int c = 0; c < chunks; ++c) {
         const int buf = c & 1;
         const bool more = c + 1 < chunks;
         if (more) {
 #pragma unroll
-            for (int q = 0; q < 8; ++q) pre[q] = *reinterpret_cast<const uint4*>(src[q] + (size_t)(c + 1) * kPfMxChunk);
+            for (int q = 0; q < kPfMxPieces; ++q)
+                pre[q] = *reinterpret_cast<const uint4*>(src[q] + (size_t)(c + 1) * kPfMxChunk);
         }
-#pragma unroll 2
-        for (int p = 0; p < kPfMxChunk / 32; ++p) {
-            const uint4 xa = *reinterpret_cast<const uint4*>(&stage[buf][ti + idx][32 * p + 8 * blk]);
-            const uint4 wb = *reinterpret_cast<const uint4*>(&stage[buf][kPfMxTokens + rj + idx][32 * p + 8 * blk]);
-            const uint32_t xw[4] = {xa.x, xa.y, xa.z, xa.w};
-            const uint32_t ww[4] = {wb.x, wb.y, wb.z, wb.w};
+        // operands of step p + 1 are read while step p's MFMAs run; the next
+        // stage is checked and stored mid-chunk (its buffer was last read
+        // before the previous barrier)
+        const uint16_t* xrow = &stage[buf][ti + idx][col];
+        const uint16_t* wrow = &stage[buf][kPfMxTokens + rj + idx][col];
+        uint2 xa[2], wb[2];
+        xa[0] = *reinterpret_cast<const uint2*>(xrow);
+        wb[0] = *reinterpret_cast<const uint2*>(wrow);
 #pragma unroll
-            for (int q = 0; q < 4; ++q) {
+        for (int p = 0; p < kSteps; ++p) {
+            if (p + 1 < kSteps) {
+                xa[(p + 1) & 1] = *reinterpret_cast<const uint2*>(xrow + 32 * (p + 1));
+                wb[(p + 1) & 1] = *reinterpret_cast<const uint2*>(wrow + 32 * (p + 1));
+            }
+            const uint32_t xw[2] = {xa[p & 1].x, xa[p & 1].y};
+            const uint32_t ww[2] = {wb[p & 1].x, wb[p & 1].y};
+#pragma unroll
+            for (int q = 0; q < 2; ++q) {
                 acc[2 * q] = __builtin_amdgcn_mfma_f32_16x16x1f32(__uint_as_float(xw[q] << 16),
                                                                   __uint_as_float(ww[q] << 16), acc[2 * q], 0, 0, 0);
                 acc[2 * q + 1] = __builtin_amdgcn_mfma_f32_16x16x1f32(__uint_as_float(xw[q] & 0xFFFF0000u),
                                                                       __uint_as_float(ww[q] & 0xFFFF0000u),
                                                                       acc[2 * q + 1], 0, 0, 0);
             }
-        }
-        if (more) {
+            if (p == kSteps - 3 && more) {
 #pragma unroll
-            for (int q = 0; q < 8; ++q) {
-                mx_range(pre[q], lo, hi);
-                *reinterpret_cast<uint4*>(&stage[buf ^ 1][srow[q]][8 * spiece[q]]) = pre[q];
+                for (int q = 0; q < kPfMxPieces; ++q) {
+                    mx_range(pre[q], lo, hi);
+                    *reinterpret_cast<uint4*>(&stage[buf ^ 1][0][0] + dst[q]) = pre[q];
+                }
             }
         }
         __syncthreads();
@@ -240,15 +262,27 @@ __global__ void __launch_bounds__(256, 2) k_pf_router_mx(const uint16_t* __restr
     if (tid == 0) redo[tile] = flagged ? 1 : 0;
     if (flagged) return;
 
+    // hand-over: value k = 16 s + 4 b + r of the h = 1 wave of tile q at
+    // xch[q][k][lane] (the stages are free after the last barrier)
+    float* xch = reinterpret_cast<float*>(mx_lds) + quad * 64 * 64 + lane;
+    if (half == 1) {
+#pragma unroll
+        for (int s = 0; s < 4; ++s)
+#pragma unroll
+            for (int k = 0; k < 16; ++k) xch[(16 * s + k) * 64] = acc[s][k];
+    }
+    __syncthreads();
+    if (half == 1) return;
     // tree per output: (c + c+16) + (c+8) + (c+4) for the four low chains, then
-    // ((y0 + y1) + (y2 + y3)) + 0.0; chain 8 b + s is acc[s][4 b + r]
+    // ((y0 + y1) + (y2 + y3)) + 0.0; chain 4 b + s is acc[s][4 b + r] here and
+    // chain 16 + 4 b + s the partner's value 16 s + 4 b + r
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
         float u[16];
 #pragma unroll
         for (int c = 0; c < 16; ++c) {
-            const int c2 = c + 16;
-            u[c] = add_rn(acc[c & 7][4 * (c >> 3) + r], acc[c2 & 7][4 * (c2 >> 3) + r]);
+            const int s = c & 3, b = c >> 2;
+            u[c] = add_rn(acc[s][4 * b + r], xch[(16 * s + 4 * b + r) * 64]);
         }
         float v8[8];
 #pragma unroll
