@@ -496,7 +496,8 @@ constexpr int kPfActCols = kPfTileN / 2;                 // gate/up: activation 
 
 __device__ __forceinline__ int pf_swz(int row) { return ((row >> 1) ^ (row << 2)) & 7; }
 
-constexpr int kPfStageLds = 2 * (kPfABytes + kPfWBytes);  // the two stages
+constexpr int kPfStages = 3;                              // stages in the LDS ring
+constexpr int kPfStageLds = kPfStages * (kPfABytes + kPfWBytes);
 constexpr int kPfOutStride = 72;  // u16 per row of a wave's output tile in LDS (64 + 8: banks)
 static_assert(8 * 64 * kPfOutStride * 2 <= kPfStageLds, "output tiles fit in the stages");
 
@@ -599,15 +600,21 @@ __global__ void __launch_bounds__(kPfGemmThreads) k_pf_gemm(PfGemm q, PfGroups g
         br[ni] = MODE == kPfGateUp ? kPfActCols * ni + 32 * wn + (lane & 31) : 64 * wn + 32 * ni + (lane & 31);
     const int khalf = lane >> 5;
     const int nk = K / kPfTileK;
+    // three stages: loads run two stages ahead of the MFMAs
     issue(0, 0);
+    if (nk > 1) issue(1, kPfTileK);
     for (int kb = 0; kb < nk; ++kb) {
-        // stage kb has landed (the only loads in flight), and every wave is
-        // done with stage kb - 1, whose buffer the issue below refills (an
-        // LDS-only barrier: __syncthreads would also wait for that issue)
-        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        // stage kb has landed (only stage kb + 1's six loads per lane may
+        // still be in flight), and every wave is done with stage kb - 1,
+        // whose buffer the issue below refills (an LDS-only barrier:
+        // __syncthreads would also wait for the loads in flight)
+        if (kb + 1 < nk)
+            asm volatile("s_waitcnt vmcnt(6)" ::: "memory");
+        else
+            asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
         wg_sync();
-        if (kb + 1 < nk) issue((kb + 1) & 1, (kb + 1) * kPfTileK);
-        const uint8_t* at = stage(kb & 1);
+        if (kb + 2 < nk) issue((kb + 2) % kPfStages, (kb + 2) * kPfTileK);
+        const uint8_t* at = stage(kb % kPfStages);
         const uint8_t* bt = at + kPfABytes;
 #pragma unroll
         for (int kk = 0; kk < kPfTileK / 16; ++kk) {
@@ -668,7 +675,7 @@ __global__ void __launch_bounds__(kPfGemmThreads) k_pf_gemm(PfGemm q, PfGroups g
     }
 }
 
-constexpr size_t kPfGemmLds = kPfStageLds + kPfTileM * 4;  // 96 KB of stages + the pair scales
+constexpr size_t kPfGemmLds = kPfStageLds + kPfTileM * 4;  // 144 KB of stages + the pair scales
 
 // ---- combine ---------------------------------------------------------------------------
 
