@@ -41,6 +41,7 @@ METRIC = "MoE decode µs/token (batch 1, 48 layers) + HBM GB/s; 8K prefill token
 SHAPE = dict(hidden=2048, intermediate=512, experts=512, top_k=10, shared_intermediate=512)
 HBM_PEAK_GBPS = 8000.0
 BF16_PEAK_TFLOPS = 2500.0  # dense bf16 MFMA
+F32_PEAK_TFLOPS = 157.3  # dense fp32 MFMA
 PREFILL_TOKENS = 8192
 
 
@@ -181,6 +182,13 @@ def bench_prefill(rt, hm, ctx, args) -> dict:
             res["gemm_roofline"] = {"bound": "mfma", "achieved": round(tf, 1), "peak": BF16_PEAK_TFLOPS,
                                     "unit": "TFLOP/s", "frac": round(tf / BF16_PEAK_TFLOPS, 4),
                                     "source": "profiles/k_pf_prefill_8k_kernel_trace.md"}
+        router_us = prof.get("k_pf_router_mx", 0.0) + prof.get("k_pf_router", 0.0)
+        if router_us > 0:
+            tf = flops["router"] / (router_us * 1e-6) / 1e12
+            res["router_roofline"] = {"bound": "mfma", "dtype": "f32 (bf16 operands, one product per step)",
+                                      "achieved": round(tf, 1), "peak": F32_PEAK_TFLOPS, "unit": "TFLOP/s",
+                                      "frac": round(tf / F32_PEAK_TFLOPS, 4),
+                                      "source": "profiles/k_pf_prefill_8k_kernel_trace.md"}
         res["kernel_us"] = prof
     log(f"prefill {T} tokens: {ms * 1000:.1f} us/block, {T / (ms * 1e-3) / 1e6:.2f} M tokens/s")
     stream.destroy()
