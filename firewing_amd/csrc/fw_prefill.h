@@ -581,7 +581,11 @@ __global__ void __launch_bounds__(kPfGemmThreads) k_pf_gemm(PfGemm q, PfGroups g
                                              (__attribute__((address_space(3))) void*)(base + kPfABytes + (4 * wv + i) * 1024),
                                              16, 0, 0);
     };
+    // A tile of at most 64 pairs spreads its 64 x 256 outputs over all eight
+    // waves (32 x 64 each, one MFMA row); loads and barriers are unchanged.
+    const bool half = rows <= kPfTileM / 2;
     const int wm = wv & 1, wn = wv >> 1;
+    const int rbase = half ? 32 * wm : 64 * wm;  // first tile row of this wave
     pf_f32x16 acc[2][2];
 #pragma unroll
     for (int mi = 0; mi < 2; ++mi)
@@ -589,12 +593,12 @@ __global__ void __launch_bounds__(kPfGemmThreads) k_pf_gemm(PfGemm q, PfGroups g
         for (int ni = 0; ni < 2; ++ni)
 #pragma unroll
             for (int e = 0; e < 16; ++e) acc[mi][ni][e] = 0.0f;
-    // operand rows of this lane: pair rows wm*64 + 32 mi + lane % 32; weight
+    // operand rows of this lane: pair rows rbase + 32 mi + lane % 32; weight
     // rows (gate/up) 32 wn + lane % 32 and 128 + 32 wn + lane % 32, (down)
     // 64 wn + 32 ni + lane % 32
     int ar[2], br[2];
 #pragma unroll
-    for (int mi = 0; mi < 2; ++mi) ar[mi] = wm * 64 + 32 * mi + (lane & 31);
+    for (int mi = 0; mi < 2; ++mi) ar[mi] = rbase + 32 * mi + (lane & 31);
 #pragma unroll
     for (int ni = 0; ni < 2; ++ni)
         br[ni] = MODE == kPfGateUp ? kPfActCols * ni + 32 * wn + (lane & 31) : 64 * wn + 32 * ni + (lane & 31);
@@ -620,17 +624,19 @@ __global__ void __launch_bounds__(kPfGemmThreads) k_pf_gemm(PfGemm q, PfGroups g
         for (int kk = 0; kk < kPfTileK / 16; ++kk) {
             const int c = 2 * kk + khalf;
             pf_bf16x8 af[2], bf[2];
-#pragma unroll
-            for (int mi = 0; mi < 2; ++mi)
-                af[mi] = *reinterpret_cast<const pf_bf16x8*>(at + ar[mi] * 128 + ((c ^ pf_swz(ar[mi])) << 4));
+            af[0] = *reinterpret_cast<const pf_bf16x8*>(at + ar[0] * 128 + ((c ^ pf_swz(ar[0])) << 4));
+            if (!half) af[1] = *reinterpret_cast<const pf_bf16x8*>(at + ar[1] * 128 + ((c ^ pf_swz(ar[1])) << 4));
 #pragma unroll
             for (int ni = 0; ni < 2; ++ni)
                 bf[ni] = *reinterpret_cast<const pf_bf16x8*>(bt + br[ni] * 128 + ((c ^ pf_swz(br[ni])) << 4));
 #pragma unroll
-            for (int mi = 0; mi < 2; ++mi)
+            for (int ni = 0; ni < 2; ++ni)
+                acc[0][ni] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[0], bf[ni], acc[0][ni], 0, 0, 0);
+            if (!half) {
 #pragma unroll
                 for (int ni = 0; ni < 2; ++ni)
-                    acc[mi][ni] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[mi], bf[ni], acc[mi][ni], 0, 0, 0);
+                    acc[1][ni] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[1], bf[ni], acc[1][ni], 0, 0, 0);
+            }
         }
     }
     // Epilogue: element e of lane l is C[i][j], i = 8 (e / 4) + 4 (l / 32) +
@@ -642,6 +648,7 @@ __global__ void __launch_bounds__(kPfGemmThreads) k_pf_gemm(PfGemm q, PfGroups g
     uint16_t* ot = reinterpret_cast<uint16_t*>(pf_lds) + wv * 64 * kPfOutStride;
 #pragma unroll
     for (int mi = 0; mi < 2; ++mi) {
+        if (mi == 1 && half) break;
 #pragma unroll
         for (int e = 0; e < 16; ++e) {
             const int r = 32 * mi + 8 * (e >> 2) + 4 * khalf + (e & 3);  // row in the wave's tile
@@ -650,7 +657,7 @@ __global__ void __launch_bounds__(kPfGemmThreads) k_pf_gemm(PfGemm q, PfGroups g
                 const uint32_t gb = to_bf16(acc[mi][0][e]), ub = to_bf16(acc[mi][1][e]);
                 ot[r * kPfOutStride + j] = to_bf16(mul_rn(from_bf16(q.silu[gb]), from_bf16(ub)));
             } else {
-                const float scale = scales[wm * 64 + r];
+                const float scale = scales[rbase + r];
 #pragma unroll
                 for (int ni = 0; ni < 2; ++ni) {
                     const uint32_t y = to_bf16(acc[mi][ni][e]);
@@ -664,11 +671,12 @@ __global__ void __launch_bounds__(kPfGemmThreads) k_pf_gemm(PfGemm q, PfGroups g
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
     constexpr int kPieces = MODE == kPfGateUp ? 4 : 8;  // 16-byte pieces per row of the wave's tile
+    const int wave_rows = half ? 32 : 64;
 #pragma unroll
     for (int u = 0; u < kPieces; ++u) {
         const int c = lane + kWave * u, r = c / kPieces, pc = c - r * kPieces;
-        if (wm * 64 + r >= rows) continue;
-        const int pr = row0 + wm * 64 + r;
+        if (r >= wave_rows || rbase + r >= rows) continue;
+        const int pr = row0 + rbase + r;
         const int col = MODE == kPfGateUp ? nt * kPfActCols + 32 * wn + 8 * pc : nt * kPfTileN + 64 * wn + 8 * pc;
         *reinterpret_cast<uint4*>(q.out + (size_t)pr * q.ldo + col) =
             *reinterpret_cast<const uint4*>(ot + r * kPfOutStride + 8 * pc);
