@@ -699,20 +699,43 @@ __device__ __forceinline__ bool pairs_task(const DecodeParams& p, uint32_t epoch
             if (!stage_layer_input<NT>(p, epoch, sh, st, li)) return false;
             FW_TRACE_MARK(slot, 0);
         }
-        float acc[NT][2];
-        line_chains<NT, MBH>(rs, H / 32, sh.xs, H, q, acc);
-        // gate (groups 0, 1) meets up (groups 2, 3): lane l takes lane l + 32;
-        // group 0 stores the pair (pair, pair + 1) with group 1's result
+        // three or four tokens: only the tokens in the mask (every token for
+        // the shared expert), compacted in token order; one or two tokens:
+        // every token, stored where the mask has it (registers for a second
+        // code path would spill). Each token's arithmetic is the same.
+        auto dots = [&](auto count) {
+            constexpr int NA = decltype(count)::value;
+            int tok[NA], xoff[NA];
+            uint32_t m = mask;
 #pragma unroll
-        for (int tt = 0; tt < NT; ++tt) {
-            float d = tree32_reduce_lines(acc[tt][0], acc[tt][1]);
-            if (q == 0) d = tree32_finish(d, wrow, sh.xs + tt * H, H);
-            const uint32_t bits = to_bf16(d);
-            const uint32_t up = (uint32_t)__shfl((int)bits, (lane + 32) & 63, kWave);
-            const uint32_t a = swiglu_bf16(bits, up, sh.exp2tab);
-            const uint32_t b = (uint32_t)__shfl((int)a, (lane + kLanesPerRow) & 63, kWave);
-            if (g == 0 && q == 0 && (mask & (1u << tt)))
-                coherent_store64(act_out + (size_t)tt * act_stride + out_index / 2, tagged(a | (b << 16), epoch));
+            for (int i = 0; i < NA; ++i) {
+                tok[i] = NA == NT ? i : __builtin_ctz(m);
+                xoff[i] = tok[i] * H;
+                m &= m - 1u;
+            }
+            float acc[NA][2];
+            line_chains_at<NA, MBH>(rs, H / 32, sh.xs, xoff, q, acc);
+            // gate (groups 0, 1) meets up (groups 2, 3): lane l takes lane l + 32;
+            // group 0 stores the pair (pair, pair + 1) with group 1's result
+#pragma unroll
+            for (int i = 0; i < NA; ++i) {
+                const int tt = tok[i];
+                float d = tree32_reduce_lines(acc[i][0], acc[i][1]);
+                if (q == 0) d = tree32_finish(d, wrow, sh.xs + tt * H, H);
+                const uint32_t bits = to_bf16(d);
+                const uint32_t up = (uint32_t)__shfl((int)bits, (lane + 32) & 63, kWave);
+                const uint32_t a = swiglu_bf16(bits, up, sh.exp2tab);
+                const uint32_t b = (uint32_t)__shfl((int)a, (lane + kLanesPerRow) & 63, kWave);
+                if (g == 0 && q == 0 && (mask & (1u << tt)))
+                    coherent_store64(act_out + (size_t)tt * act_stride + out_index / 2, tagged(a | (b << 16), epoch));
+            }
+        };
+        if constexpr (NT <= 2) {
+            dots(std::integral_constant<int, NT>{});
+        } else {
+            // a union expert always has a token (its mask is never empty)
+            const int na = __builtin_popcount(mask & ((1u << NT) - 1u));
+            if (na > 0) with_count<1, NT>(na, dots);
         }
         FW_TRACE_MARK(slot, 1);
     }

@@ -17,6 +17,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <type_traits>
+
 #include "fw_numerics.h"
 
 namespace fw {
@@ -300,15 +302,15 @@ __device__ __forceinline__ int line_column(int q) { return 4 * (q & 7) + 2 * (q 
 // The pipelined sweep of line_chains (NT <= 2), G lines per group.
 template <int NT, int MAXB, int G>
 __device__ __forceinline__ void line_sweep(const LineShare<MAXB>& r, int nblocks, const float* __restrict__ xq,
-                                           int xstride, int q, float (&acc)[NT][2]) {
+                                           const int (&xoff)[NT], int q, float (&acc)[NT][2]) {
     constexpr int NL = (MAXB + 1) / 2;  // lines
     float2 xv[2][NT][2 * G];
 #pragma unroll
     for (int i = 0; i < G && i < NL; ++i) {
 #pragma unroll
         for (int t = 0; t < NT; ++t) {
-            xv[0][t][2 * i] = *reinterpret_cast<const float2*>(xq + t * xstride + 64 * i);
-            xv[0][t][2 * i + 1] = *reinterpret_cast<const float2*>(xq + t * xstride + 64 * i + 32);
+            xv[0][t][2 * i] = *reinterpret_cast<const float2*>(xq + xoff[t] + 64 * i);
+            xv[0][t][2 * i + 1] = *reinterpret_cast<const float2*>(xq + xoff[t] + 64 * i + 32);
         }
     }
 #pragma unroll
@@ -318,7 +320,7 @@ __device__ __forceinline__ void line_sweep(const LineShare<MAXB>& r, int nblocks
             for (int i = 0; i < G && v0 + G + i < NL; ++i) {
 #pragma unroll
                 for (int t = 0; t < NT; ++t) {
-                    const float* xa = xq + t * xstride + 64 * (v0 + G + i);
+                    const float* xa = xq + xoff[t] + 64 * (v0 + G + i);
                     xv[buf ^ 1][t][2 * i] = *reinterpret_cast<const float2*>(xa);
                     xv[buf ^ 1][t][2 * i + 1] = *reinterpret_cast<const float2*>(xa + 32);
                 }
@@ -351,13 +353,13 @@ __device__ __forceinline__ void line_sweep(const LineShare<MAXB>& r, int nblocks
     }
 }
 
-// Chains of one row for NT tokens against f32 vectors in LDS (stride xstride);
-// nblocks is uniform. Every token is computed. The vector values of the next
+// Chains of one row for NT tokens against f32 vectors in LDS (token t's at
+// xs + xoff[t], uniform offsets); nblocks is uniform. The vector values of the next
 // group of G lines are read from LDS while the current group is computed (G
 // = 0: 4 lines for one token, 2 for two; fewer registers with a smaller G).
 template <int NT, int MAXB, int G = 0>
-__device__ __forceinline__ void line_chains(const LineShare<MAXB>& r, int nblocks, const float* __restrict__ xs,
-                                            int xstride, int q, float (&acc)[NT][2]) {
+__device__ __forceinline__ void line_chains_at(const LineShare<MAXB>& r, int nblocks, const float* __restrict__ xs,
+                                               const int (&xoff)[NT], int q, float (&acc)[NT][2]) {
     constexpr int NL = (MAXB + 1) / 2;  // lines
 #pragma unroll
     for (int t = 0; t < NT; ++t) acc[t][0] = acc[t][1] = 0.0f;
@@ -375,7 +377,7 @@ __device__ __forceinline__ void line_chains(const LineShare<MAXB>& r, int nblock
                     const float w0 = bf16_lo(first), w1 = bf16_hi(first);
 #pragma unroll
                     for (int t = 0; t < NT; ++t) {
-                        const float2 x2 = *reinterpret_cast<const float2*>(xq + t * xstride + 64 * v);
+                        const float2 x2 = *reinterpret_cast<const float2*>(xq + xoff[t] + 64 * v);
                         acc[t][0] = add_rn(acc[t][0], mul_rn(w0, x2.x));
                         acc[t][1] = add_rn(acc[t][1], mul_rn(w1, x2.y));
                     }
@@ -384,7 +386,7 @@ __device__ __forceinline__ void line_chains(const LineShare<MAXB>& r, int nblock
                     const float w0 = bf16_lo(second), w1 = bf16_hi(second);
 #pragma unroll
                     for (int t = 0; t < NT; ++t) {
-                        const float2 x2 = *reinterpret_cast<const float2*>(xq + t * xstride + 64 * v + 32);
+                        const float2 x2 = *reinterpret_cast<const float2*>(xq + xoff[t] + 64 * v + 32);
                         acc[t][0] = add_rn(acc[t][0], mul_rn(w0, x2.x));
                         acc[t][1] = add_rn(acc[t][1], mul_rn(w1, x2.y));
                     }
@@ -394,7 +396,31 @@ __device__ __forceinline__ void line_chains(const LineShare<MAXB>& r, int nblock
         }
         return;
     }
-    line_sweep<NT, MAXB, G != 0 ? G : (NT == 1 ? 4 : 2)>(r, nblocks, xq, xstride, q, acc);
+    line_sweep<NT, MAXB, G != 0 ? G : (NT == 1 ? 4 : 2)>(r, nblocks, xq, xoff, q, acc);
+}
+
+// line_chains_at with token t's vector at xs + t * xstride.
+template <int NT, int MAXB, int G = 0>
+__device__ __forceinline__ void line_chains(const LineShare<MAXB>& r, int nblocks, const float* __restrict__ xs,
+                                            int xstride, int q, float (&acc)[NT][2]) {
+    int xoff[NT];
+#pragma unroll
+    for (int t = 0; t < NT; ++t) xoff[t] = t * xstride;
+    line_chains_at<NT, MAXB, G>(r, nblocks, xs, xoff, q, acc);
+}
+
+// f(std::integral_constant<int, n>) for a uniform n in [LO, HI] (n > HI runs HI).
+template <int LO, int HI, class F>
+__device__ __forceinline__ void with_count(int n, F&& f) {
+    if constexpr (LO < HI) {
+        if (n == LO) {
+            f(std::integral_constant<int, LO>{});
+            return;
+        }
+        with_count<LO + 1, HI>(n, f);
+    } else {
+        f(std::integral_constant<int, HI>{});
+    }
 }
 
 // line_chains for one token with the row's line words in LDS (wrow: the row's
