@@ -620,6 +620,8 @@ __global__ void __launch_bounds__(kPfGemmThreads) k_pf_gemm(PfGemm q, PfGroups g
         if (kb + 2 < nk) issue((kb + 2) % kPfStages, (kb + 2) * kPfTileK);
         const uint8_t* at = stage(kb % kPfStages);
         const uint8_t* bt = at + kPfABytes;
+        // raised wave priority while this wave feeds the matrix pipe
+        __builtin_amdgcn_s_setprio(1);
 #pragma unroll
         for (int kk = 0; kk < kPfTileK / 16; ++kk) {
             const int c = 2 * kk + khalf;
@@ -638,6 +640,7 @@ __global__ void __launch_bounds__(kPfGemmThreads) k_pf_gemm(PfGemm q, PfGroups g
                     acc[1][ni] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[1], bf[ni], acc[1][ni], 0, 0, 0);
             }
         }
+        __builtin_amdgcn_s_setprio(0);
     }
     // Epilogue: element e of lane l is C[i][j], i = 8 (e / 4) + 4 (l / 32) +
     // e % 4, j = l % 32. Each wave writes its results into its own LDS tile
