@@ -1137,8 +1137,7 @@ static void launch_prefill(firewing_hip_context* c, size_t layer, const uint16_t
     check(hipGetLastError(), "k_pf_router launch");
     hipLaunchKernelGGL(k_select, dim3(T), dim3(64), 0, s, f.logits, E, K, f.ids, f.scores, 1, c->error);
     check(hipGetLastError(), "k_select launch");
-    hipLaunchKernelGGL(k_pf_zero, dim3((G + 255) / 256), dim3(256), 0, s, f.g.counts, G);
-    hipLaunchKernelGGL(k_pf_zero, dim3((G + 255) / 256), dim3(256), 0, s, f.g.cursor, G);
+    hipLaunchKernelGGL(k_pf_zero, dim3((G + 255) / 256), dim3(256), 0, s, f.g.counts, f.g.cursor, G);
     const int chunks = (T * K + kPfChunk - 1) / kPfChunk;
     hipLaunchKernelGGL(k_pf_count, dim3(chunks), dim3(256), 0, s, f.ids, T * K, E, f.g.counts);
     hipLaunchKernelGGL(k_pf_scan, dim3(1), dim3(1024), 0, s, f.g, E, T);

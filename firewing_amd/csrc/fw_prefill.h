@@ -318,9 +318,9 @@ struct PfGroups {
 
 constexpr int kPfTileM = 128;  // pairs per GEMM tile
 
-__global__ void k_pf_zero(int32_t* __restrict__ a, int n) {
+__global__ void k_pf_zero(int32_t* __restrict__ a, int32_t* __restrict__ b, int n) {
     const int i = (int)(blockIdx.x * blockDim.x + threadIdx.x);
-    if (i < n) a[i] = 0;
+    if (i < n) a[i] = b[i] = 0;
 }
 
 // Selections per expert. Each block takes kPfChunk pairs, counts them in an
