@@ -450,11 +450,11 @@ __global__ void __launch_bounds__(256) k_pf_scatter(PfGroups g, const int32_t* _
 // the pair's token row of X for gate/up, the pair's activation row for down).
 // Block tile 128 pairs x 256 weight rows, eight waves of 64 x 64, each 2 x 2
 // v_mfma_f32_32x32x16_bf16 tiles. Both operands are k-contiguous rows; they
-// travel global -> LDS directly (16 bytes per lane) in stages of 64 k, two
-// stages (one loading while the other is multiplied). In a stage each
-// 128-byte row holds its eight 16-byte chunks permuted by the row (chunk ^
-// pf_swz(row)), so the operand reads (32 rows, one chunk) spread over the LDS
-// banks.
+// travel global -> LDS directly (16 bytes per lane) in stages of 32 k, a ring
+// of three stages (loads two stages ahead of the MFMAs) in 72 KB, so two
+// workgroups share a CU (four waves per SIMD). In a stage each 64-byte row
+// holds its four 16-byte chunks permuted by the row (chunk ^ pf_swz(row)), so
+// the operand reads (32 rows, one chunk) spread over the LDS banks.
 //
 // kPfGateUp: the tile's weight rows are 128 gate rows and the matching 128 up
 // rows; the epilogue rounds both to bf16 and writes SwiGLU (src/expert.rs:
@@ -488,16 +488,19 @@ typedef __bf16 pf_bf16x8 __attribute__((ext_vector_type(8)));
 typedef float pf_f32x16 __attribute__((ext_vector_type(16)));
 
 constexpr int kPfTileN = 256;                            // weight rows per tile
-constexpr int kPfTileK = 64;                             // k per stage
+constexpr int kPfTileK = 32;                             // k per stage (64-byte rows)
 constexpr int kPfGemmThreads = 512;
-constexpr int kPfABytes = kPfTileM * kPfTileK * 2;       // 16 KB
-constexpr int kPfWBytes = kPfTileN * kPfTileK * 2;       // 32 KB
+constexpr int kPfABytes = kPfTileM * kPfTileK * 2;       // 8 KB
+constexpr int kPfWBytes = kPfTileN * kPfTileK * 2;       // 16 KB
 constexpr int kPfActCols = kPfTileN / 2;                 // gate/up: activation columns per tile
 
-__device__ __forceinline__ int pf_swz(int row) { return ((row >> 1) ^ (row << 2)) & 7; }
+// 16-byte chunk c of row r sits at chunk c ^ pf_swz(r) of the row's 64 bytes:
+// the 16 rows that one 16-byte read per lane touches (and any 8 of them in
+// order) then fall on distinct bank groups.
+__device__ __forceinline__ int pf_swz(int row) { return ((row >> 1) ^ (row >> 3)) & 3; }
 
 constexpr int kPfStages = 3;                              // stages in the LDS ring
-constexpr int kPfStageLds = kPfStages * (kPfABytes + kPfWBytes);
+constexpr int kPfStageLds = kPfStages * (kPfABytes + kPfWBytes);  // 72 KB: two workgroups per CU
 constexpr int kPfOutStride = 72;  // u16 per row of a wave's output tile in LDS (64 + 8: banks)
 static_assert(8 * 64 * kPfOutStride * 2 <= kPfStageLds, "output tiles fit in the stages");
 
@@ -511,7 +514,7 @@ static_assert(8 * 64 * kPfOutStride * 2 <= kPfStageLds, "output tiles fit in the
 constexpr int kPfXcds = 8;
 
 template <int MODE>
-__global__ void __launch_bounds__(kPfGemmThreads) k_pf_gemm(PfGemm q, PfGroups g) {
+__global__ void __launch_bounds__(kPfGemmThreads, 4) k_pf_gemm(PfGemm q, PfGroups g) {
     extern __shared__ __attribute__((aligned(16))) uint8_t pf_lds[];  // [2 stages][A | W]
     const int total = g.tiles[0] * q.n_tiles;
     const int per = (total + kPfXcds - 1) / kPfXcds;
@@ -540,45 +543,46 @@ __global__ void __launch_bounds__(kPfGemmThreads) k_pf_gemm(PfGemm q, PfGroups g
     // before it by the loop's barriers)
     float* scales = reinterpret_cast<float*>(pf_lds + kPfStageLds);
     if (MODE == kPfDown && tid < kPfTileM) scales[tid] = from_bf16(g.pair_scale[row0 + min(tid, rows - 1)]);
-    // this thread's loads per stage: 2 pair-row and 4 weight-row instructions
-    // of the wave, 8 rows each: rows 8 (2 wv + i) + lane / 8 and 8 (4 wv + i) + lane / 8
-    const uint16_t* arow[2];
-    int achunk[2];
+    // this thread's loads per stage: 1 pair-row and 2 weight-row instructions
+    // of the wave, 16 rows each (one 1 KB LDS block per instruction, lane l at
+    // byte 16 l): rows 16 wv + lane / 4 and 16 (2 wv + i) + lane / 4
+    const uint16_t* arow[1];
+    int achunk[1];
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
-        const int r = 8 * (2 * wv + i) + (lane >> 3);
+    for (int i = 0; i < 1; ++i) {
+        const int r = 16 * wv + (lane >> 2);
         const int pr = row0 + min(r, rows - 1);  // rows past the group's end repeat its last
         if constexpr (MODE == kPfGateUp)
             arow[i] = q.a + (size_t)g.pair_token[pr] * q.lda;
         else
             arow[i] = q.a + (size_t)pr * q.lda;
-        achunk[i] = (lane & 7) ^ pf_swz(r);
+        achunk[i] = (lane & 3) ^ pf_swz(r);
     }
-    const uint16_t* wrow[4];
-    int wchunk[4];
+    const uint16_t* wrow[2];
+    int wchunk[2];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const int r = 8 * (4 * wv + i) + (lane >> 3);
+    for (int i = 0; i < 2; ++i) {
+        const int r = 16 * (2 * wv + i) + (lane >> 2);
         int wr;
         if constexpr (MODE == kPfGateUp)  // gate rows, then the up rows
             wr = r < kPfActCols ? nt * kPfActCols + r : Ig + nt * kPfActCols + (r - kPfActCols);
         else
             wr = nt * kPfTileN + r;
         wrow[i] = wbase + (size_t)wr * K;
-        wchunk[i] = (lane & 7) ^ pf_swz(r);
+        wchunk[i] = (lane & 3) ^ pf_swz(r);
     }
     auto stage = [&](int s) { return pf_lds + s * (kPfABytes + kPfWBytes); };
     auto issue = [&](int s, int k0) {
         uint8_t* base = stage(s);
 #pragma unroll
-        for (int i = 0; i < 2; ++i)
+        for (int i = 0; i < 1; ++i)
             __builtin_amdgcn_global_load_lds(reinterpret_cast<const void*>(arow[i] + k0 + 8 * achunk[i]),
-                                             (__attribute__((address_space(3))) void*)(base + (2 * wv + i) * 1024),
+                                             (__attribute__((address_space(3))) void*)(base + (wv + i) * 1024),
                                              16, 0, 0);
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
+        for (int i = 0; i < 2; ++i)
             __builtin_amdgcn_global_load_lds(reinterpret_cast<const void*>(wrow[i] + k0 + 8 * wchunk[i]),
-                                             (__attribute__((address_space(3))) void*)(base + kPfABytes + (4 * wv + i) * 1024),
+                                             (__attribute__((address_space(3))) void*)(base + kPfABytes + (2 * wv + i) * 1024),
                                              16, 0, 0);
     };
     // A tile of at most 64 pairs spreads its 64 x 256 outputs over all eight
@@ -608,12 +612,12 @@ __global__ void __launch_bounds__(kPfGemmThreads) k_pf_gemm(PfGemm q, PfGroups g
     issue(0, 0);
     if (nk > 1) issue(1, kPfTileK);
     for (int kb = 0; kb < nk; ++kb) {
-        // stage kb has landed (only stage kb + 1's six loads per lane may
+        // stage kb has landed (only stage kb + 1's three loads per lane may
         // still be in flight), and every wave is done with stage kb - 1,
         // whose buffer the issue below refills (an LDS-only barrier:
         // __syncthreads would also wait for the loads in flight)
         if (kb + 1 < nk)
-            asm volatile("s_waitcnt vmcnt(6)" ::: "memory");
+            asm volatile("s_waitcnt vmcnt(3)" ::: "memory");
         else
             asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
         wg_sync();
@@ -626,11 +630,11 @@ __global__ void __launch_bounds__(kPfGemmThreads) k_pf_gemm(PfGemm q, PfGroups g
         for (int kk = 0; kk < kPfTileK / 16; ++kk) {
             const int c = 2 * kk + khalf;
             pf_bf16x8 af[2], bf[2];
-            af[0] = *reinterpret_cast<const pf_bf16x8*>(at + ar[0] * 128 + ((c ^ pf_swz(ar[0])) << 4));
-            if (!half) af[1] = *reinterpret_cast<const pf_bf16x8*>(at + ar[1] * 128 + ((c ^ pf_swz(ar[1])) << 4));
+            af[0] = *reinterpret_cast<const pf_bf16x8*>(at + ar[0] * 64 + ((c ^ pf_swz(ar[0])) << 4));
+            if (!half) af[1] = *reinterpret_cast<const pf_bf16x8*>(at + ar[1] * 64 + ((c ^ pf_swz(ar[1])) << 4));
 #pragma unroll
             for (int ni = 0; ni < 2; ++ni)
-                bf[ni] = *reinterpret_cast<const pf_bf16x8*>(bt + br[ni] * 128 + ((c ^ pf_swz(br[ni])) << 4));
+                bf[ni] = *reinterpret_cast<const pf_bf16x8*>(bt + br[ni] * 64 + ((c ^ pf_swz(br[ni])) << 4));
 #pragma unroll
             for (int ni = 0; ni < 2; ++ni)
                 acc[0][ni] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[0], bf[ni], acc[0][ni], 0, 0, 0);
@@ -686,7 +690,7 @@ __global__ void __launch_bounds__(kPfGemmThreads) k_pf_gemm(PfGemm q, PfGroups g
     }
 }
 
-constexpr size_t kPfGemmLds = kPfStageLds + kPfTileM * 4;  // 144 KB of stages + the pair scales
+constexpr size_t kPfGemmLds = kPfStageLds + kPfTileM * 4;  // 72 KB of stages + the pair scales
 
 // ---- combine ---------------------------------------------------------------------------
 
