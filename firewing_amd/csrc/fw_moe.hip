@@ -450,7 +450,8 @@ void launch_decode(firewing_hip_context* c, size_t first, size_t n, int T, int o
     // Roles: the combine role gets one workgroup per C task of a layer where
     // the grid allows (so every task's down rows are in flight before the
     // gate/up phase ends), at most half of the grid. The rows role takes one
-    // B task per workgroup and layer. B tasks beyond that: with one token, when
+    // B task per workgroup and layer (the kernels for two or more tokens: as
+    // many as even out the two roles' lists). B tasks beyond that: with one token, when
     // they come to two gate/up pairs per C task, wave 0 of each C task computes
     // them (the one-token kernel, which requires this: every C task of a layer
     // is resident at once and publishes its pairs before waiting for the
@@ -462,6 +463,13 @@ void launch_decode(firewing_hip_context* c, size_t first, size_t n, int T, int o
         p.g_comb = std::min(p.n_c, grid / 2);
         p.g_rows = grid - p.g_comb;
         p.nb_rows = std::min(p.n_b, p.g_rows);
+        if (kt >= 2) {
+            // several B tasks per rows workgroup: even out the two roles'
+            // task lists, a C task counted as two B tasks (the B tasks left to
+            // the combine role are the last union slots, often empty)
+            const int even = (p.n_b + 2 * p.n_c - p.n_router - p.n_shared) / 2;
+            p.nb_rows = std::min(p.n_b, std::max(p.nb_rows, even));
+        }
         if (p.g_comb < 1 || p.g_rows < 1) throw HipError{"decode grid too small for its roles"};
     };
     int kt = T;  // token count of the kernel variant
