@@ -45,7 +45,7 @@ struct Exp2Table {
 // 2^(r/32) from a cubic. Restated here with the operation order that glibc's
 // x86-64 FMA build evaluates (the reduction and the polynomial fused), which
 // reproduces glibc 2.35 expf, and therefore Rust f32::exp on Linux, on all 2^32
-// inputs (tests/test_numerics_host.py). The table is a constant computed
+// inputs (tests/test_abi_host.py, test_expf_matches_glibc_on_all_floats). The table is a constant computed
 // from 2^(i/32) in fw_exp2_table().
 FW_HD float expf_glibc(float x, const uint64_t* tab) {
     const double kInvLn2N = 0x1.71547652b82fep+0 * 32.0;

@@ -41,7 +41,8 @@ enum fw_synth_tensor {
 /* Weight standard deviation for every synthetic weight tensor. */
 #define FW_SYNTH_WEIGHT_SIGMA 0.02
 /* Zipf exponent of expert popularity and the bias slope that realises it
- * (calibrated by firewing_amd/zipf_calibration.py for H=2048, E=512, K=10). */
+ * (calibrated by tests/golden/zipf_calibration.py for H=2048, E=512, K=10;
+ * the realised exponent is checked by tests/test_workload.py). */
 #define FW_SYNTH_ZIPF_S 1.1
 #define FW_SYNTH_ZIPF_BIAS_SLOPE 0.45
 

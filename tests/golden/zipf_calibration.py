@@ -8,8 +8,8 @@ top-K selection frequency of the popularity ranks 3..300 follows a power law
 of exponent -s (Zipf s = 1.1) by Monte Carlo on that logit model; the chosen
 value is FW_SYNTH_ZIPF_BIAS_SLOPE in firewing_amd/csrc/fw_synth.h. The two
 most popular experts saturate (selected for most tokens), so the fit excludes
-them. The realised frequencies of the real synthetic layers are measured and
-reported by the tests and the benchmark.
+them. tests/test_workload.py fits the same exponent on the selections of the
+real synthetic layers (the oracle's exact route of seeded tokens).
 """
 from __future__ import annotations
 

@@ -376,3 +376,114 @@ def test_expf_is_glibc_on_known_values():
     assert y[0] == 1.0 and y[1] == 1.0
     assert y[2] == np.float32(2.7182817)
     assert y[3] == 0.0 and np.isinf(y[4]) and y[5] == 0.0 and np.isinf(y[6])
+
+
+# ---- pins whose failure a plausible oracle mistake would cause ----------------------
+
+def _bf16_rne_f64(value: float) -> float:
+    """Round an f64 to the nearest bf16 value, ties to even (8 significant
+    bits), by exact rational arithmetic: independent of the oracle's float
+    path."""
+    from fractions import Fraction
+    import math
+    if value == 0.0:
+        return 0.0
+    v = Fraction(value)
+    sign = -1 if v < 0 else 1
+    v = abs(v)
+    e = math.floor(math.log2(v))
+    while Fraction(2) ** e > v:
+        e -= 1
+    while Fraction(2) ** (e + 1) <= v:
+        e += 1
+    ulp = Fraction(2) ** (e - 7)
+    q, r = divmod(v, ulp)
+    if r * 2 > ulp or (r * 2 == ulp and q % 2 == 1):
+        q += 1
+    return sign * float(q * ulp)
+
+
+def test_tiny_expert_swiglu_bits_are_exact():
+    # tests/test_generate_expert_fixture.py:9-27 asserts torch.equal on
+    # bf16(bf16(silu(gate)) * up): silu is rounded to bf16 before the multiply
+    # (src/expert.rs:562-571). Derived here in f64 with exact rounding:
+    #   silu(-3) = -0.1422776 -> bf16 -0.142578125; * 2.0  = -0.28515625
+    #   silu(1.5) = 1.2263618 -> bf16 1.2265625; * -3.0 = -3.6796875 -> -3.6875
+    # Without the inner rounding the second would be bf16(-3.67908...) =
+    # -3.671875.
+    import math
+    gate, up = [-3.0, 1.5], [2.0, -3.0]
+    expect = []
+    for g, u in zip(gate, up):
+        silu = _bf16_rne_f64(g / (1.0 + math.exp(-g)))
+        expect.append(_bf16_rne_f64(silu * u))
+    assert expect == [-0.28515625, -3.6875]
+    hidden = bf16([1.0, -2.0])
+    gate_up_w = bf16([1.0, 2.0, 0.5, -0.5, 2.0, 0.0, -1.0, 1.0])
+    out = fo.expert_bf16(gate_up_w, bf16([1.0, 0.0, 0.0, 1.0]), hidden, 2, 2, fo.to_bf16(0.5))
+    assert f32(out["swiglu"]) == expect
+    assert f32(out["down"]) == expect
+    assert f32(out["weighted_down"]) == [v * 0.5 for v in expect]
+
+
+def test_route_renormalises_over_the_selection():
+    # src/router.rs:248-262 and src/decoder_layer.rs:290-306: softmax over all
+    # E logits, then each selected probability divided by the selection's
+    # sum. With 502 unselected experts holding most of the mass, the
+    # un-renormalised probabilities are ~19x smaller than the scores, so an
+    # oracle that skipped the division would fail by far more than the
+    # tolerance; the f64 closed form exp(l_i) / sum_sel exp(l_j) is what the
+    # renormalised score must equal up to f32 rounding and the bf16 output.
+    import math
+    E, K = 512, 10
+    sel_values = [1.0 - 0.125 * i for i in range(K)]      # exact in bf16
+    logits = np.full(E, fo.to_bf16(-0.25), dtype=np.uint16)  # below every selected value
+    chosen = [7, 501, 3, 260, 99, 18, 444, 130, 311, 58]  # rank order of the values above
+    for e, v in zip(chosen, sel_values):
+        logits[e] = fo.to_bf16(v)
+    ids = fo.topk_total_order(logits, K)
+    assert list(ids) == chosen
+    scores = f32(fo.route_scores(logits, ids))
+    z = sum(math.exp(v) for v in sel_values)
+    full = sum(math.exp(v) for v in sel_values) + (E - K) * math.exp(-0.25)
+    for s, v in zip(scores, sel_values):
+        closed = math.exp(v) / z
+        assert abs(s - closed) <= 2 ** -8 * closed, (s, closed)
+        assert closed / (math.exp(v) / full) > 10.0  # skipping renormalisation is far off
+    assert abs(sum(scores) - 1.0) <= K * 2 ** -9
+
+
+def test_block_mixture_runs_in_ascending_expert_id_not_rank():
+    # src/decoder_layer.rs:422-424 (execution order = ascending id) and the
+    # src/expert.rs:1276-1287 pattern: with contributions w0 = -w1 (experts 0
+    # and 1 tie in the router, so their scores are equal) and a small w2 from
+    # the top-ranked expert 2, the ascending-id sum is (w0 + w1) + w2 = w2,
+    # while the rank-order sum (w2 + w0) + w1 loses w2 to rounding and gives 0.
+    # Expert e: gate row 64 -> silu = 64 exactly; up row u_e -> act = 64 u_e;
+    # down = identity, so its down output is 64 u_e: 1024, -1024 and 0.5.
+    shape = {"hidden": 2, "intermediate": 1, "experts": 3, "top_k": 3, "shared_intermediate": 2}
+    u = [16.0, -16.0, 1.0 / 128.0]
+    gate_up = []
+    for ue in u:
+        gate_up += [64.0, 0.0, ue, 0.0]  # rows [gate; up] of [2I, H] = [2, 2]
+    weights = {
+        "router": bf16([0.0, 0.0, 0.0, 0.0, 1.0, 0.0]),  # logits [0, 0, 1]
+        "gate_up": bf16(gate_up),
+        "down": bf16([1.0, 0.0] * 3),                     # [H, I] = [2, 1] per expert
+        "shared_gate": bf16([0.0] * 4),
+        "shared_up": bf16([0.0] * 4),
+        "shared_down": bf16([0.0] * 4),                   # shared output 0
+        "shared_expert_gate": bf16([0.0, 0.0]),
+    }
+    hidden = bf16([1.0, 0.0])
+    res = fo.sparse_moe_block(shape, weights, hidden)
+    assert list(res["ids"]) == [2, 0, 1]  # rank order differs from id order
+    s = f32(res["scores"])               # rank order: experts 2, 0, 1
+    assert s[1] == s[2]
+    w = {0: _bf16_rne_f64(1024.0 * s[1]), 1: _bf16_rne_f64(-1024.0 * s[2]), 2: _bf16_rne_f64(0.5 * s[0])}
+    assert w[0] == -w[1] and 0 < w[2] < 0.5  # below half an ulp of w0 (ulp 1 in [128, 256))
+    ascending = _bf16_rne_f64(_bf16_rne_f64(w[0] + w[1]) + w[2])
+    rank_order = _bf16_rne_f64(_bf16_rne_f64(w[2] + w[0]) + w[1])
+    assert ascending == w[2] and rank_order == 0.0
+    assert f32(res["routed_mixture"])[0] == ascending
+    assert f32(res["out"])[0] == ascending
