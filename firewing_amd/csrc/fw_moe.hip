@@ -11,6 +11,7 @@
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
+#include <mutex>
 #include <new>
 #include <string>
 #include <type_traits>
@@ -203,7 +204,9 @@ __global__ void __launch_bounds__(64) k_select(const uint16_t* __restrict__ logi
         int nan = 0;
         for (int e = lane; e < count; e += kWave) nan |= ((lt[e] & 0x7fffu) > 0x7f80u);
         if (__any(nan)) {
+            // rejected: the token's ids read -1 (device callers see it there)
             if (lane == 0) atomicExch(error, 2);
+            if (lane < k) ids[(size_t)blockIdx.x * k + lane] = -1;
             return;
         }
     }
@@ -522,6 +525,38 @@ bool check_device_error(firewing_hip_context* c, hipStream_t s) {
 
 }  // namespace
 
+// ---- scratch of the entry point that allocates nothing ----------------------------------
+//
+// firewing_hip_route_bf16_noalloc keeps its intermediate logits (when the caller
+// takes none) and the top-k kernel's NaN word here instead of in memory it
+// allocates. One copy per GPU, held until the process ends; in host code the
+// array's name is only a handle: its device address comes from
+// hipGetSymbolAddress, once per device.
+constexpr size_t kRouteScratchHeader = 256;               // the NaN word, then padding
+constexpr size_t kRouteScratchLogitBytes = (size_t)1 << 20;  // logits: tokens * experts * 2 bytes
+static __device__ __align__(256) uint8_t scratch[kRouteScratchHeader + kRouteScratchLogitBytes];
+
+namespace {
+
+constexpr int kMaxScratchDevices = 64;
+std::mutex g_scratch_mutex;
+void* g_scratch_address[kMaxScratchDevices] = {};
+
+// Device address of `scratch` on `device` (the current device).
+void* route_scratch(int device) {
+    if (device < 0 || device >= kMaxScratchDevices) throw HipError{"route_bf16_noalloc: device index out of range"};
+    std::lock_guard<std::mutex> lock(g_scratch_mutex);
+    if (g_scratch_address[device] == nullptr) {
+        void* p = nullptr;
+        check(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)), "hipGetSymbolAddress(scratch)");
+        if (p == nullptr) throw HipError{"hipGetSymbolAddress(scratch) returned null"};
+        g_scratch_address[device] = p;
+    }
+    return g_scratch_address[device];
+}
+
+}  // namespace
+
 // ---- C ABI ------------------------------------------------------------------------------
 
 extern "C" {
@@ -694,6 +729,51 @@ bool firewing_hip_route_bf16(const uint16_t* weight, const uint16_t* hidden, siz
         check(hipStreamSynchronize(nullptr), "hipStreamSynchronize");
         if (err == 2) return fail("decoder-layer router received unsupported logits (NaN)");
         for (size_t i = 0; i < hid.size(); ++i) ids[i] = (size_t)hid[i];
+        return true;
+    });
+}
+
+bool firewing_hip_route_bf16_noalloc(const uint16_t* weight, const uint16_t* hidden, size_t tokens,
+                                     size_t experts, size_t width, size_t top_k, int order, int32_t* ids,
+                                     uint16_t* scores, uint16_t* logits, void* stream) {
+    return guarded([&] {
+        if (!weight || !hidden || !ids || !scores) return fail("route_bf16_noalloc: null pointer");
+        if (tokens == 0 || tokens > 4096) return fail("route_bf16_noalloc: tokens must be in [1, 4096]");
+        if (experts == 0 || experts > (size_t)kMaxExperts)
+            return fail("route_bf16_noalloc: experts must be in [1, 1024]");
+        if (top_k == 0 || top_k > experts || top_k > (size_t)kMaxTopK)
+            return fail("route_bf16_noalloc: top_k must be in [1, min(32, experts)]");
+        if (order != FIREWING_HIP_LOGITS_TREE32 && order != FIREWING_HIP_LOGITS_FOLD)
+            return fail("route_bf16_noalloc: unknown logit order");
+        std::string why;
+        if (!shape_ok_for_linear(experts, width, &why)) return fail("route_bf16_noalloc: " + why);
+        if (width % 2) return fail("route_bf16_noalloc: width must be even");
+        if (reinterpret_cast<uintptr_t>(weight) % 4 || reinterpret_cast<uintptr_t>(hidden) % 2)
+            return fail("route_bf16_noalloc: weight must be 4-byte aligned and hidden 2-byte aligned");
+        if (!logits && tokens * experts * 2 > kRouteScratchLogitBytes)
+            return fail("route_bf16_noalloc: without a logits output, tokens * experts must be <= 524288 "
+                        "(the logits live in the library's 1 MiB scratch)");
+        int device = 0;
+        check(hipGetDevice(&device), "hipGetDevice");
+        char* base = static_cast<char*>(route_scratch(device));
+        int32_t* error = reinterpret_cast<int32_t*>(base);  // written on a NaN logit, read by no one
+        uint16_t* lg = logits ? logits : reinterpret_cast<uint16_t*>(base + kRouteScratchHeader);
+        hipStream_t s = static_cast<hipStream_t>(stream);
+        const size_t per_launch = std::max<size_t>(1, std::min<size_t>(4, 16384 / width));
+        for (size_t t0 = 0; t0 < tokens; t0 += per_launch) {
+            const int T = (int)std::min<size_t>(per_launch, tokens - t0);
+            if (order == FIREWING_HIP_LOGITS_TREE32) {
+                launch_linear(weight, hidden + t0 * width, (int)experts, (int)width, T, lg + t0 * experts, s);
+            } else {
+                hipLaunchKernelGGL(k_linear_fold, dim3((unsigned)((experts + 63) / 64)), dim3(64),
+                                   (size_t)T * width * 4, s, weight, hidden + t0 * width, (int)experts,
+                                   (int)width, T, lg + t0 * experts);
+                check(hipGetLastError(), "k_linear_fold launch");
+            }
+        }
+        hipLaunchKernelGGL(k_select, dim3((unsigned)tokens), dim3(64), 0, s, lg, (int)experts, (int)top_k, ids,
+                           scores, order == FIREWING_HIP_LOGITS_TREE32 ? 1 : 0, error);
+        check(hipGetLastError(), "k_select launch");
         return true;
     });
 }

@@ -67,6 +67,7 @@ _SIGNATURES = {
     "firewing_hip_sigmoid_bf16": (_b, [_u16p, _sz, _u16p]),
     "firewing_hip_topk_bf16": (_b, [_u16p, _sz, _sz, _szp]),
     "firewing_hip_route_bf16": (_b, [_u16p, _u16p, _sz, _sz, _sz, _sz, ctypes.c_int, _szp, _u16p, _u16p]),
+    "firewing_hip_route_bf16_noalloc": (_b, [_vp, _vp, _sz, _sz, _sz, _sz, ctypes.c_int, _vp, _vp, _vp, _vp]),
     "firewing_hip_expert_bf16": (_b, [_u16p, _u16p, _u16p, _sz, _sz, ctypes.c_uint16, _u16p, _u16p,
                                       _u16p, _u16p]),
     "firewing_hip_create": (_b, [ctypes.POINTER(Shape), ctypes.POINTER(_vp)]),
@@ -190,6 +191,14 @@ def route(weight, hidden, experts: int, width: int, top_k: int, order: int = LOG
     _call("firewing_hip_route_bf16", _p16(w), _p16(x), tokens, experts, width, top_k, order, ids,
           _p16(scores), _p16(logits))
     return np.array(list(ids), dtype=np.int64).reshape(tokens, top_k), scores, logits
+
+
+def route_noalloc_dev(weight, hidden, tokens: int, experts: int, width: int, top_k: int, ids, scores,
+                      logits=None, order: int = LOGITS_TREE32, stream=None) -> None:
+    """firewing_hip_route_bf16_noalloc on device addresses (asynchronous on
+    `stream`; ids int32 [T, K], -1 for a rejected token)."""
+    _call("firewing_hip_route_bf16_noalloc", _addr(weight), _addr(hidden), tokens, experts, width, top_k,
+          order, _addr(ids), _addr(scores), _addr(logits), _addr(stream))
 
 
 def expert_bf16(gate_up_weight, down_weight, hidden, hidden_size: int, intermediate: int,

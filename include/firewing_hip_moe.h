@@ -96,6 +96,20 @@ bool firewing_hip_route_bf16(const uint16_t* weight, const uint16_t* hidden, siz
                              size_t experts, size_t width, size_t top_k, int order,
                              size_t* ids, uint16_t* scores, uint16_t* logits);
 
+/* No counterpart in the reference: firewing_hip_route_bf16 for callers that
+ * cannot allocate device memory (code under HIP graph capture, serving loops
+ * that forbid hipMalloc). Same arithmetic and arguments, but device pointers
+ * (weight [E, H] 4-byte aligned, hidden [T, H], ids [T, K] int32 rank order,
+ * scores [T, K], logits [T, E] or NULL) and an asynchronous launch on `stream`
+ * (NULL: the null stream). No allocation: the logits, when `logits` is NULL,
+ * live in a fixed 1 MiB scratch area of the library on each GPU, so then
+ * tokens * experts <= 524288 (larger requests fail). A token whose TREE32
+ * logits hold a NaN is rejected with all its ids set to -1. Calls that overlap
+ * on one GPU share that scratch and race; order them on one stream. */
+bool firewing_hip_route_bf16_noalloc(const uint16_t* weight, const uint16_t* hidden, size_t tokens,
+                                     size_t experts, size_t width, size_t top_k, int order,
+                                     int32_t* ids, uint16_t* scores, uint16_t* logits, void* stream);
+
 /* One routed expert, src/expert.rs:717-751 (gate_up -> SwiGLU -> down ->
  * route weighting); replaces src/metal_bf16.rs:192-212 execute_expert.
  * gate_up_weight [2I, H], down_weight [H, I], hidden [H]; every capture may be
