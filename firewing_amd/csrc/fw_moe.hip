@@ -311,6 +311,9 @@ struct firewing_hip_context {
     int cu_count = 0;
     uint64_t wall_clock_hz = 100000000ULL;
     hipStream_t stream = nullptr;
+    // the context's last queued work, on whichever stream it ran: every call
+    // waits for it and then records its own (calls share the scratch below)
+    hipEvent_t last = nullptr;
     // resident banks
     std::vector<uint16_t*> router;  // [E + 1][H] per layer
     std::vector<uint16_t*> gate_up, down, shared_gate, shared_up, shared_down;
@@ -353,6 +356,23 @@ T* dalloc(size_t count) {
     check(hipMalloc(&p, std::max<size_t>(count, 1) * sizeof(T)), "hipMalloc");
     return static_cast<T*>(p);
 }
+
+// A call's work on stream s runs after every earlier call on the context
+// (whatever stream that used) and becomes the context's last work: the
+// constructor makes s wait for the last recorded work, the destructor records
+// s's queue end (also when the call fails part-way, so nothing queued is left
+// unordered).
+struct Ordered {
+    firewing_hip_context* c;
+    hipStream_t s;
+    Ordered(firewing_hip_context* ctx, void* stream)
+        : c(ctx), s(stream ? static_cast<hipStream_t>(stream) : ctx->stream) {
+        check(hipStreamWaitEvent(s, c->last, 0), "hipStreamWaitEvent");
+    }
+    ~Ordered() { (void)hipEventRecord(c->last, s); }
+    Ordered(const Ordered&) = delete;
+    Ordered& operator=(const Ordered&) = delete;
+};
 
 bool validate_shape(const firewing_hip_shape& s, std::string* why) {
     auto bad = [&](const char* m) {
@@ -496,9 +516,10 @@ void launch_decode(firewing_hip_context* c, size_t first, size_t n, int T, int o
     // The kernel reads its parameters from a device copy; upload only on change
     // (the copy is stream-ordered before the launch; pageable source, staged).
     if (std::memcmp(&p, &c->last_params, sizeof p) != 0 || !c->params_valid) {
-        check(hipMemcpyAsync(c->d_params, &p, sizeof p, hipMemcpyHostToDevice, s), "upload decode params");
         c->last_params = p;
         c->params_valid = true;
+        check(hipMemcpyAsync(c->d_params, &c->last_params, sizeof p, hipMemcpyHostToDevice, s),
+              "upload decode params");
     }
     const DecodeParams* dp = c->d_params;
     // a fresh tag for this launch's exchanged words (0 is never used)
@@ -838,6 +859,7 @@ bool firewing_hip_create(const firewing_hip_shape* shape, firewing_hip_context**
             if (v > 0.0 && v <= 600.0) c->timeout_seconds = v;
         }
         check(hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking), "hipStreamCreate");
+        check(hipEventCreateWithFlags(&c->last, hipEventDisableTiming), "hipEventCreate");
         const size_t L = shape->layers, H = shape->hidden, I = shape->intermediate;
         const size_t E = shape->experts, Is = shape->shared_intermediate, K = shape->top_k;
         c->router.assign(L, nullptr);
@@ -904,6 +926,7 @@ bool firewing_hip_create(const firewing_hip_shape* shape, firewing_hip_context**
 
 void firewing_hip_destroy(firewing_hip_context* c) {
     if (!c) return;
+    if (c->last) (void)hipEventSynchronize(c->last);
     if (c->stream) (void)hipStreamSynchronize(c->stream);
     auto freev = [](std::vector<uint16_t*>& v) {
         for (auto* p : v)
@@ -923,6 +946,7 @@ void firewing_hip_destroy(firewing_hip_context* c) {
         if (b) (void)hipFree(b);
     for (void* b : c->pf.owned)
         if (b) (void)hipFree(b);
+    if (c->last) (void)hipEventDestroy(c->last);
     if (c->stream) (void)hipStreamDestroy(c->stream);
     delete c;
 }
@@ -943,7 +967,8 @@ bool firewing_hip_install_layer(firewing_hip_context* c, size_t layer, const uin
             return fail("install_layer: null tensor");
         const size_t H = c->shape.hidden, I = c->shape.intermediate, E = c->shape.experts;
         const size_t Is = c->shape.shared_intermediate;
-        hipStream_t s = c->stream;
+        Ordered ordered(c, nullptr);
+        hipStream_t s = ordered.s;
         upload(c->router[layer], router, E * H * 2, s);
         upload(c->router[layer] + E * H, shared_expert_gate, H * 2, s);
         upload(c->gate_up[layer], gate_up, E * 2 * I * H * 2, s);
@@ -964,7 +989,8 @@ bool firewing_hip_generate_layers(firewing_hip_context* c, size_t first, size_t 
             return fail("generate_layers: layer range out of bounds");
         const size_t H = c->shape.hidden, I = c->shape.intermediate, E = c->shape.experts;
         const size_t Is = c->shape.shared_intermediate;
-        hipStream_t s = c->stream;
+        Ordered ordered(c, nullptr);
+        hipStream_t s = ordered.s;
         if (!c->d_weight_table) {
             std::vector<uint16_t> table(65536);
             fw_synth_normal_table(FW_SYNTH_WEIGHT_SIGMA, table.data());
@@ -1033,8 +1059,9 @@ bool firewing_hip_read_tensor(firewing_hip_context* c, size_t layer, int tensor,
             default: return fail("read_tensor: unknown tensor id");
         }
         if (first > n || count > n - first) return fail("read_tensor: range out of bounds");
-        download(out, base + first, count * 2, c->stream);
-        check(hipStreamSynchronize(c->stream), "hipStreamSynchronize");
+        Ordered ordered(c, nullptr);
+        download(out, base + first, count * 2, ordered.s);
+        check(hipStreamSynchronize(ordered.s), "hipStreamSynchronize");
         return true;
     });
 }
@@ -1049,7 +1076,8 @@ bool firewing_hip_route(firewing_hip_context* c, size_t layer, const uint16_t* h
         if (order != FIREWING_HIP_LOGITS_TREE32 && order != FIREWING_HIP_LOGITS_FOLD)
             return fail("route: unknown logit order");
         const size_t H = c->shape.hidden, E = c->shape.experts, K = c->shape.top_k;
-        hipStream_t s = c->stream;
+        Ordered ordered(c, nullptr);
+        hipStream_t s = ordered.s;
         DeviceBuffer dx(tokens * H * 2), dl(tokens * E * 2), dids(tokens * K * 4),
             dsc(tokens * K * 2), derr(4);
         upload(dx.ptr, hidden, tokens * H * 2, s);
@@ -1095,7 +1123,8 @@ bool firewing_hip_mixture_bf16(firewing_hip_context* c, size_t layer, const uint
         for (size_t i = 0; i < count; ++i) {
             if (experts[i] >= E) return fail("mixture: expert index is out of range");
         }
-        hipStream_t s = c->stream;
+        Ordered ordered(c, nullptr);
+        hipStream_t s = ordered.s;
         DeviceBuffer dx(H * 2), dgo(2 * I * 2), dact(I * 2), ddo(H * 2), dw(count * H * 2), dmix(H * 2);
         upload(dx.ptr, hidden, H * 2, s);
         for (size_t i = 0; i < count; ++i) {
@@ -1149,10 +1178,12 @@ static bool prefill_args_ok(firewing_hip_context* c, size_t layer, size_t tokens
 }
 
 // Scratch for `tokens` tokens (grown, never shrunk).
-static void prefill_reserve(firewing_hip_context* c, size_t tokens) {
+// Work queued before this call (on any stream) may still use the old
+// buffers: the host waits for the context's last work before freeing them.
+static void prefill_reserve(firewing_hip_context* c, size_t tokens, hipStream_t s) {
     auto& f = c->pf;
     if (f.tokens >= tokens) return;
-    check(hipStreamSynchronize(c->stream), "hipStreamSynchronize");
+    check(hipEventSynchronize(c->last), "hipEventSynchronize");
     for (void* b : f.owned)
         if (b) (void)hipFree(b);
     f.owned.clear();
@@ -1185,9 +1216,8 @@ static void prefill_reserve(firewing_hip_context* c, size_t tokens) {
     take(f.g.pair_scale, P);
     take(f.g.pair_of, T * K);
     take(f.silu, 65536);
-    hipLaunchKernelGGL(k_pf_silu_lut, dim3(256), dim3(256), 0, c->stream, f.silu);
+    hipLaunchKernelGGL(k_pf_silu_lut, dim3(256), dim3(256), 0, s, f.silu);
     check(hipGetLastError(), "k_pf_silu_lut launch");
-    check(hipStreamSynchronize(c->stream), "hipStreamSynchronize");
     f.tokens = tokens;
 }
 
@@ -1272,12 +1302,9 @@ bool firewing_hip_prefill_block_dev(firewing_hip_context* c, size_t layer, const
         if (!hidden || !out) return fail("prefill_block: null pointer");
         if (reinterpret_cast<uintptr_t>(hidden) % 16 || reinterpret_cast<uintptr_t>(out) % 16)
             return fail("prefill_block: hidden and out must be 16-byte aligned");
-        hipStream_t s = stream ? static_cast<hipStream_t>(stream) : c->stream;
-        if (s != c->stream) {
-            // the scratch may be reallocated: order it after the caller's stream
-            check(hipStreamSynchronize(s), "hipStreamSynchronize");
-        }
-        prefill_reserve(c, tokens);
+        Ordered ordered(c, stream);
+        hipStream_t s = ordered.s;
+        prefill_reserve(c, tokens, s);
         const size_t K = c->shape.top_k;
         launch_prefill(c, layer, hidden, tokens, out, false, s);
         if (ids) check(hipMemcpyAsync(ids, c->pf.ids, tokens * K * 4, hipMemcpyDeviceToDevice, s), "copy ids");
@@ -1292,8 +1319,9 @@ bool firewing_hip_prefill_block(firewing_hip_context* c, size_t layer, const uin
         std::string why;
         if (!prefill_args_ok(c, layer, tokens, FIREWING_HIP_LOGITS_TREE32, &why)) return fail("prefill_block: " + why);
         if (!hidden || !out) return fail("prefill_block: null pointer");
-        hipStream_t s = c->stream;
-        prefill_reserve(c, tokens);
+        Ordered ordered(c, nullptr);
+        hipStream_t s = ordered.s;
+        prefill_reserve(c, tokens, s);
         const size_t H = c->shape.hidden, E = c->shape.experts, K = c->shape.top_k;
         auto& f = c->pf;
         upload(f.x, hidden, tokens * H * 2, s);
@@ -1348,7 +1376,8 @@ bool firewing_hip_sparse_moe_block_dev(firewing_hip_context* c, size_t layer,
         if (!hidden || !out) return fail("sparse_moe_block: null pointer");
         if (reinterpret_cast<uintptr_t>(hidden) % 4) return fail("sparse_moe_block: hidden must be 4-byte aligned");
         if (layer >= c->shape.layers) return fail("sparse_moe_block: layer out of range");
-        hipStream_t s = stream ? static_cast<hipStream_t>(stream) : c->stream;
+        Ordered ordered(c, stream);
+        hipStream_t s = ordered.s;
         const size_t H = c->shape.hidden;
         launch_decode(c, layer, 1, (int)tokens, order, false, false, hidden, nullptr, s);
         check(hipMemcpyAsync(out, c->out, tokens * H * 2, hipMemcpyDeviceToDevice, s), "copy output");
@@ -1364,7 +1393,8 @@ bool firewing_hip_sparse_moe_block(firewing_hip_context* c, size_t layer,
         if (!step_args_ok(c, tokens, order, &why)) return fail("sparse_moe_block: " + why);
         if (!hidden || !out) return fail("sparse_moe_block: null pointer");
         if (layer >= c->shape.layers) return fail("sparse_moe_block: layer out of range");
-        hipStream_t s = c->stream;
+        Ordered ordered(c, nullptr);
+        hipStream_t s = ordered.s;
         const size_t H = c->shape.hidden, E = c->shape.experts, K = c->shape.top_k;
         upload(c->xin, hidden, tokens * H * 2, s);
         launch_decode(c, layer, 1, (int)tokens, order, false, false, c->xin, nullptr, s);
@@ -1409,7 +1439,8 @@ bool firewing_hip_moe_step_dev(firewing_hip_context* c, const uint16_t* hidden, 
         if (!hidden || !residual) return fail("moe_step: null pointer");
         if (reinterpret_cast<uintptr_t>(hidden) % 4 || reinterpret_cast<uintptr_t>(residual) % 4)
             return fail("moe_step: hidden and residual must be 4-byte aligned");
-        hipStream_t s = stream ? static_cast<hipStream_t>(stream) : c->stream;
+        Ordered ordered(c, stream);
+        hipStream_t s = ordered.s;
         const size_t L = c->shape.layers, H = c->shape.hidden, K = c->shape.top_k;
         launch_decode(c, 0, L, (int)tokens, order, true, bias_feature, hidden, residual, s);
         if (block_out)
@@ -1431,7 +1462,8 @@ bool firewing_hip_moe_step(firewing_hip_context* c, const uint16_t* hidden, size
         std::string why;
         if (!step_args_ok(c, tokens, order, &why)) return fail("moe_step: " + why);
         if (!hidden || !residual) return fail("moe_step: null pointer");
-        hipStream_t s = c->stream;
+        Ordered ordered(c, nullptr);
+        hipStream_t s = ordered.s;
         const size_t L = c->shape.layers, H = c->shape.hidden, K = c->shape.top_k;
         upload(c->xin, hidden, tokens * H * 2, s);
         launch_decode(c, 0, L, (int)tokens, order, true, bias_feature, c->xin, c->xfinal, s);
@@ -1460,11 +1492,12 @@ extern "C" bool firewing_hip_debug_traced_step(firewing_hip_context* c, const ui
         if (cap < n * kTraceWords) return fail("trace buffer too small");
         c->trace = dalloc<uint64_t>(n * kTraceWords);
         check(hipMemset(c->trace, 0, n * kTraceWords * 8), "hipMemset trace");
-        upload(c->xin, hidden, tokens * H * 2, c->stream);
-        launch_decode(c, 0, L, (int)tokens, 0, true, true, c->xin, nullptr, c->stream);
-        bool ok = check_device_error(c, c->stream);
-        download(out, c->trace, n * kTraceWords * 8, c->stream);
-        check(hipStreamSynchronize(c->stream), "hipStreamSynchronize");
+        Ordered ordered(c, nullptr);
+        upload(c->xin, hidden, tokens * H * 2, ordered.s);
+        launch_decode(c, 0, L, (int)tokens, 0, true, true, c->xin, nullptr, ordered.s);
+        bool ok = check_device_error(c, ordered.s);
+        download(out, c->trace, n * kTraceWords * 8, ordered.s);
+        check(hipStreamSynchronize(ordered.s), "hipStreamSynchronize");
         (void)hipFree(c->trace);
         c->trace = nullptr;
         *tasks = n;
@@ -1476,7 +1509,8 @@ extern "C" bool firewing_hip_debug_traced_step(firewing_hip_context* c, const ui
 bool firewing_hip_synchronize(firewing_hip_context* c) {
     return guarded([&] {
         if (!c) return fail("synchronize: null context");
-        return check_device_error(c, c->stream);
+        Ordered ordered(c, nullptr);  // c->stream waits for the last work on any stream
+        return check_device_error(c, ordered.s);
     });
 }
 

@@ -374,3 +374,45 @@ def test_step_workload_shape_three_layers(ctx3, tokens):
     # a second launch reuses the counters the first one zeroed
     again = ctx3.moe_step(x)
     assert np.array_equal(again[0], resid)
+
+
+def test_calls_on_different_streams_are_ordered(ctx3):
+    # The context's calls share its scratch (launch parameters, phase
+    # counters, prefill buffers). moe_step_dev on one user stream,
+    # prefill_block_dev on another (the first time growing the prefill
+    # scratch) and host-pointer calls on the context's stream follow each
+    # other with no host wait: each must still run after the previous one.
+    from firewing_amd import hip_runtime as rt
+    H = CFG["hidden"]
+    x = fo.synth_hidden(SEED, 1, H, first_token=41)
+    xb = fo.synth_hidden(SEED, 2, H, first_token=42)
+    xp = fo.synth_hidden(SEED, 96, H, first_token=43)
+    xq = fo.synth_hidden(SEED, 300, H, first_token=44)
+    want_step = ctx3.moe_step(x)[0]
+    want_block = ctx3.sparse_moe_block(1, xb)["out"]
+    want_pf = ctx3.prefill_block(0, xp)["out"]
+    a, b = rt.Stream(), rt.Stream()
+    xd, rd = rt.DeviceArray.from_numpy(x), rt.DeviceArray(x.shape, np.uint16)
+    xpd, opd = rt.DeviceArray.from_numpy(xp), rt.DeviceArray(xp.shape, np.uint16)
+    xqd, oqd = rt.DeviceArray.from_numpy(xq), rt.DeviceArray(xq.shape, np.uint16)
+    for i in range(3):
+        ctx3.moe_step_dev(xd.ptr, 1, rd.ptr, stream=a.handle)
+        if i == 0:
+            ctx3.prefill_block_dev(1, xqd.ptr, 300, oqd.ptr, stream=b.handle)  # grows the scratch
+        blk = ctx3.sparse_moe_block(1, xb)["out"]
+        ctx3.prefill_block_dev(0, xpd.ptr, 96, opd.ptr, stream=b.handle)
+        ctx3.moe_step_dev(xd.ptr, 1, rd.ptr, stream=a.handle)
+        pf = ctx3.prefill_block(0, xp)["out"]
+        assert np.array_equal(blk, want_block), i
+        assert np.array_equal(pf, want_pf), i
+    a.synchronize()
+    b.synchronize()
+    ctx3.synchronize()
+    assert np.array_equal(rd.numpy(), want_step)
+    assert np.array_equal(opd.numpy(), want_pf)
+    out_q = oqd.numpy()
+    assert np.array_equal(out_q, ctx3.prefill_block(1, xq)["out"])
+    for arr in (xd, rd, xpd, opd, xqd, oqd):
+        arr.free()
+    a.destroy()
+    b.destroy()
