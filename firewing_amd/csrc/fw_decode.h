@@ -209,6 +209,7 @@ struct DecodeShared {
     int32_t nvec;
     int32_t nunion;
     int32_t flag;
+    int32_t rows_landed;  // one-token C task: its sequence number once the lead wave's gate/up rows are in
     int32_t red[kThreads / 64];  // workgroup reductions (one word per wave)
     uint32_t rin[kRowsPerCTask];  // C task: the residual words it updates
     int32_t trace_stale;  // profiling builds: stale words of the last block-input read
@@ -949,25 +950,39 @@ __device__ __forceinline__ bool stage_acts_direct(const DecodeParams& p, int li,
     FW_TRACE_MARK_IF(lane == 0 && w == 2, slot, 9);
     FW_TRACE_MARK_IF(lane == 0 && w == 3, slot, 3);
     wg_sync();
+    // Thread t's word of vector m is word t (a vector is at most 256 words).
+    // Words without the epoch are read again past the caches, every stale
+    // word of the thread in one pass, until all carry it.
     bool ok = true;
-    for (int m = 0; m <= U; ++m) {
-        const int len = m == 0 ? Is / 2 : I / 2;
-        for (int wd = threadIdx.x; wd < len; wd += kThreads) {
-            uint64_t* word = raw + (size_t)m * stride + wd;
-            if (has_tag(*word, epoch)) continue;
-            const uint64_t* src = source(m) + wd;
-            const uint64_t start = wall_clock64();
-            uint64_t v;
-            while (!has_tag(v = coherent_load64(src), epoch)) {
-                if (coherent_load(p.error) != 0 || wall_clock64() - start > p.limit_ticks) {
-                    int32_t expected = 0;
-                    __hip_atomic_compare_exchange_strong(p.error, &expected, 1, __ATOMIC_RELAXED, __ATOMIC_RELAXED,
-                                                         __HIP_MEMORY_SCOPE_AGENT);
-                    ok = false;
-                    break;
+    const int tid = threadIdx.x;
+    uint32_t stale = 0;
+#pragma unroll
+    for (int m = 0; m < kDirectVectors; ++m) {
+        if (m <= U && tid < (m == 0 ? Is / 2 : I / 2) && !has_tag(raw[(size_t)m * stride + tid], epoch))
+            stale |= 1u << m;
+    }
+    if (stale != 0) {
+        const uint64_t start = wall_clock64();
+        while (stale != 0) {
+            uint64_t v[kDirectVectors];
+#pragma unroll
+            for (int m = 0; m < kDirectVectors; ++m)
+                if (stale & (1u << m)) v[m] = coherent_load64(source(m) + tid);
+#pragma unroll
+            for (int m = 0; m < kDirectVectors; ++m) {
+                if ((stale & (1u << m)) && has_tag(v[m], epoch)) {
+                    raw[(size_t)m * stride + tid] = v[m];
+                    stale &= ~(1u << m);
                 }
             }
-            *word = v;
+            if (stale == 0) break;
+            if (coherent_load(p.error) != 0 || wall_clock64() - start > p.limit_ticks) {
+                int32_t expected = 0;
+                __hip_atomic_compare_exchange_strong(p.error, &expected, 1, __ATOMIC_RELAXED, __ATOMIC_RELAXED,
+                                                     __HIP_MEMORY_SCOPE_AGENT);
+                ok = false;
+                break;
+            }
         }
     }
     return wg_all(sh.red, ok) != 0;
@@ -1156,6 +1171,7 @@ __device__ __forceinline__ bool combine_task_fused(const DecodeParams& p, uint32
     static_assert(fused_combine(NT, MBH, MBI), "one token");
     static_assert(stage_words(NT, MBI) >= kBRowsAt + 4 * kBRowStride, "gate/up rows above the exponentials");
     static_assert(stage_words(NT, MBI) >= kDirectVectors * MBI * 16 * 2, "tagged words of the staged vectors");
+    static_assert(MBI * 16 <= kThreads, "one staged word per thread and vector");
     FW_TRACE_STAMP(t0);
     const int slot = trace_slot(p, li, p.n_router + p.n_shared + p.n_b + j);
     (void)slot;
@@ -1242,22 +1258,27 @@ __device__ __forceinline__ bool combine_task_fused(const DecodeParams& p, uint32
         for (int e = tid; e < p.ls; e += kThreads) nan |= (e < p.E) && ((sh.lg[e] & 0x7fffu) > 0x7f80u);
         if (wg_any(sh.red, nan) && tid == 0) atomicCAS(p.error, 0, 2);
     }
-    // wave 1 scores while the lead wave runs the pairs (the publish below
-    // synchronises both before anything reads the scores)
+    // wave 1 scores while the lead wave runs the pairs (the barrier before
+    // the staging orders both before anything reads the scores or overwrites
+    // the exponentials)
     score_experts<NT>(p, li, sh, j == 0, kMaxHidden, 1, false);
     FW_TRACE_MARK_IF(w == 1 && lane == 0, slot, 6);
     st.scored = li;
+    const int seq = li * p.n_c + j;  // this task's mark in sh.rows_landed
+    if (w != 0) {
+        // the down rows go out once the lead wave's gate/up rows are in (the
+        // gate/up rows, needed first, go ahead of them in the layer's burst)
+        while (__hip_atomic_load(&sh.rows_landed, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) != seq)
+            __builtin_amdgcn_s_sleep(1);
+        issue_down();
+    }
+    // lead wave: as soon as its rows are in LDS (its own loads: no barrier),
+    // the two pairs' dots and SwiGLU (src/expert.rs:514-571); lane 0 stores
+    // the word of both activations
     if (w == 0) {
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
         FW_TRACE_MARK_IF(lane == 0, slot, 10);
-    }
-    wg_sync();
-    // (the lead wave issues its own after the pairs: issuing into the burst can
-    // stall it)
-    if (w != 0) issue_down();
-    // lead wave: the two pairs' dots and SwiGLU (src/expert.rs:514-571) from
-    // the rows in LDS; lane 0 stores the word of both activations
-    if (w == 0) {
+        if (lane == 0) __hip_atomic_store(&sh.rows_landed, seq, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
         float acc[1][2];
         line_chains_lds<MBH, 2>(brows + g * bstride, H / 32, sh.xs, q, acc);
         float d = tree32_reduce_lines(acc[0][0], acc[0][1]);
@@ -1398,6 +1419,7 @@ __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(N
 k_moe_decode(const DecodeParams* __restrict__ P, uint32_t epoch) {
     __shared__ DecodeShared<NT, MBI> sh;
     if (threadIdx.x < 32) sh.exp2tab[threadIdx.x] = c_exp2_table[threadIdx.x];
+    if (threadIdx.x == 0) sh.rows_landed = -1;
     wg_sync();
     const int b = (int)blockIdx.x;
     const int G = (int)gridDim.x;
