@@ -103,6 +103,8 @@ struct DecodeParams {
     int cu_count;                         // compute units (workgroup b sits on the CU of b mod cu_count)
     int input_by_tags;                    // router tasks await their block input by its words' tags
                                           // alone (no combine phase flag)
+    int rank_slots;                       // one token: slot s is the rank-s expert (B tasks run the
+                                          // top-k only up to their own rank), not the s-th smallest id
     uint64_t* trace;     // profiling builds only
 };
 
@@ -200,6 +202,7 @@ struct DecodeShared {
     uint32_t slot_tokens[kMaxTopK * NT];
     int32_t tslot[NT * kMaxTopK];     // [t][k]: slot of the token's k-th expert in ascending id
     int32_t pos[NT * kMaxTopK];       // [t][r]: ascending-id position of the token's rank-r expert
+    int32_t rank_at[kMaxTopK];        // one token: rank of the expert at ascending-id position k
     uint16_t tweight[NT * kMaxTopK];  // [t][k]: its bf16 score
     uint16_t sig[NT];
     float inv[NT];
@@ -390,6 +393,7 @@ __device__ __forceinline__ void select_experts(const DecodeParams& p, SH& sh, in
             sh.slot_tokens[rank] = 1u;
             sh.tslot[rank] = rank;
             sh.pos[lane] = rank;
+            sh.rank_at[rank] = lane;
         }
         for (int s2 = K + lane; s2 < S; s2 += kWave) sh.slot_tokens[s2] = 0u;
         if (lane == 0) sh.nunion = K;
@@ -576,6 +580,23 @@ __device__ __forceinline__ bool select_layer(const DecodeParams& p, uint32_t epo
     return true;
 }
 
+// One token with rank-ordered slots: the expert of rank r (of layer li) into
+// sh.ids[r], from a top-k that stops after r + 1 rounds. Leaves no complete
+// selection in LDS.
+template <int TK, class SH>
+__device__ __forceinline__ bool select_rank(const DecodeParams& p, uint32_t epoch, SH& sh, LdsState& st, int li,
+                                            int r, int slot) {
+    if (!wait_phase(phase_flags(p, li, kCntRouter), epoch, p.error, p.limit_ticks, &sh.flag)) return false;
+    FW_TRACE_MARK(slot, 2);
+    if (!load_logits<1>(p, li, epoch, sh)) return false;
+    FW_TRACE_MARK(slot, 3);
+    if (rel_wave(p) == 0) wave_topk<TK>(sh.lg, p.E, r + 1, sh.ids);
+    FW_TRACE_MARK(slot, 4);
+    wg_sync();
+    st.selected = -1;
+    return true;
+}
+
 // R task j of layer li: 16 router rows, or the shared_expert_gate row.
 template <int NT, int MBH, class SH>
 __device__ __forceinline__ bool router_task(const DecodeParams& p, uint32_t epoch, SH& sh, LdsState& st,
@@ -675,11 +696,19 @@ __device__ __forceinline__ bool pairs_task(const DecodeParams& p, uint32_t epoch
                 return false;
             if (!stage_layer_input<NT>(p, epoch, sh, st, li)) return false;
         }
-        if (!select_layer<NT, TK>(p, epoch, sh, st, li, slot)) return false;
-        FW_TRACE_MARK(slot, 0);
-        work = s < uniform(sh.nunion);
-        const int e = work ? uniform(sh.sorted[s]) : 0;
-        mask = work ? (uint32_t)uniform((int)sh.slot_tokens[s]) : 0u;
+        int e;
+        if (p.rank_slots) {
+            if (!select_rank<TK>(p, epoch, sh, st, li, s, slot)) return false;
+            FW_TRACE_MARK(slot, 0);
+            e = uniform(sh.ids[s]);
+            mask = 1u;
+        } else {
+            if (!select_layer<NT, TK>(p, epoch, sh, st, li, slot)) return false;
+            FW_TRACE_MARK(slot, 0);
+            work = s < uniform(sh.nunion);
+            e = work ? uniform(sh.sorted[s]) : 0;
+            mask = work ? (uint32_t)uniform((int)sh.slot_tokens[s]) : 0u;
+        }
         wbase = L.gate_up + (size_t)e * 2 * I * H;
         up = I;
         pair0 = (js - s * per_slot) * kPairsPerTask;
@@ -848,7 +877,8 @@ __device__ __forceinline__ bool stage_acts(const DecodeParams& p, int li, uint32
             }
             if (all) break;
             if (pass == 0) start = wall_clock64();
-            if (coherent_load(p.error) != 0 || wall_clock64() - start > p.limit_ticks) {
+            // the shared error word on every 8th pass
+            if (((pass & 7) == 7 && coherent_load(p.error) != 0) || wall_clock64() - start > p.limit_ticks) {
                 int32_t expected = 0;
                 __hip_atomic_compare_exchange_strong(p.error, &expected, 1, __ATOMIC_RELAXED, __ATOMIC_RELAXED,
                                                      __HIP_MEMORY_SCOPE_AGENT);
@@ -963,6 +993,7 @@ __device__ __forceinline__ bool stage_acts_direct(const DecodeParams& p, int li,
     }
     if (stale != 0) {
         const uint64_t start = wall_clock64();
+        uint32_t polls = 0;
         while (stale != 0) {
             uint64_t v[kDirectVectors];
 #pragma unroll
@@ -976,7 +1007,7 @@ __device__ __forceinline__ bool stage_acts_direct(const DecodeParams& p, int li,
                 }
             }
             if (stale == 0) break;
-            if (coherent_load(p.error) != 0 || wall_clock64() - start > p.limit_ticks) {
+            if (((++polls & 7) == 0 && coherent_load(p.error) != 0) || wall_clock64() - start > p.limit_ticks) {
                 int32_t expected = 0;
                 __hip_atomic_compare_exchange_strong(p.error, &expected, 1, __ATOMIC_RELAXED, __ATOMIC_RELAXED,
                                                      __HIP_MEMORY_SCOPE_AGENT);
@@ -1221,7 +1252,9 @@ __device__ __forceinline__ bool combine_task_fused(const DecodeParams& p, uint32
     const int pr = fp0 - bs * I + (g >> 1);
     // row r (= lane group) of the pairs: gate of pair r / 2 for even r, up for odd
     auto brel = [&](int r) { return ((r & 1) ? I : 0) + (r >> 1); };
-    const uint16_t* bbase = L.gate_up + ((size_t)uniform(sh.sorted[bs]) * 2 * I + (fp0 - bs * I)) * H;
+    // slot s: the rank-s expert (rank-ordered slots), else the s-th smallest id
+    auto slot_expert = [&](int s) { return uniform(p.rank_slots ? sh.ids[s] : sh.sorted[s]); };
+    const uint16_t* bbase = L.gate_up + ((size_t)slot_expert(bs) * 2 * I + (fp0 - bs * I)) * H;
     // the four rows of H bf16, H / 2 + 16 words apart (see kBRowStride)
     uint64_t* brows = reinterpret_cast<uint64_t*>(sh.xs + kBRowsAt);
     const int bstride = (H / 2 + 16) / 2;  // 8-byte words
@@ -1244,7 +1277,7 @@ __device__ __forceinline__ bool combine_task_fused(const DecodeParams& p, uint32
         for (int k = 0; k < 3; ++k) {
             const int m = w + 4 * k;
             if (m >= 1 && m <= U) {
-                const uint16_t* wm = L.down + (size_t)uniform(sh.sorted[m - 1]) * (size_t)H * I;
+                const uint16_t* wm = L.down + (size_t)slot_expert(m - 1) * (size_t)H * I;
                 line_issue(c[k], wm + (size_t)r0 * I, (uint32_t)(g * I * 2), q);
             }
         }
@@ -1317,7 +1350,9 @@ __device__ __forceinline__ bool combine_task_fused(const DecodeParams& p, uint32
         if (m <= U) {
             const uint32_t bits = down_row_lds<MBI, 2>(c[k], (m == 0 ? Is : I) / 32, act_lds + m * act_stride, q);
             if (q == 0) {
-                const uint32_t scale = m == 0 ? sh.sig[0] : sh.tweight[m - 1];
+                // the slot's route weight (tweight is by ascending-id position)
+                const uint32_t scale =
+                    m == 0 ? sh.sig[0] : sh.tweight[p.rank_slots ? sh.pos[m - 1] : m - 1];
                 sh.res[m * kRowsPerCTask + g] = to_bf16(mul_rn(from_bf16(bits), from_bf16(scale)));
             }
         }
@@ -1333,7 +1368,8 @@ __device__ __forceinline__ bool combine_task_fused(const DecodeParams& p, uint32
             uint32_t d[8];
 #pragma unroll
             for (int i = 0; i < 8; ++i) {
-                if (k0 + i < K) d[i] = sh.res[(1 + k0 + i) * kRowsPerCTask + gg];
+                // the matrix of the expert at ascending-id position k0 + i
+                if (k0 + i < K) d[i] = sh.res[(1 + (p.rank_slots ? sh.rank_at[k0 + i] : k0 + i)) * kRowsPerCTask + gg];
             }
 #pragma unroll
             for (int i = 0; i < 8; ++i) {

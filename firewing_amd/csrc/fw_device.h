@@ -35,6 +35,12 @@ __device__ __forceinline__ int lane_id() {
     asm volatile("" : "+v"(t));
     return t & (kWave - 1);
 }
+// The workgroup thread index, opaque in the same way.
+__device__ __forceinline__ int thread_id() {
+    int t = (int)threadIdx.x;
+    asm volatile("" : "+v"(t));
+    return t;
+}
 __device__ __forceinline__ int wave_id() {
     int w = __builtin_amdgcn_readfirstlane((int)(threadIdx.x / kWave));
     asm volatile("" : "+s"(w));
@@ -672,8 +678,10 @@ __device__ __forceinline__ bool wait_phase(const uint32_t* flags, uint32_t epoch
         int32_t ok = 1;
         if (coherent_load(f) != epoch) {
             uint64_t start = wall_clock64();
-            while (coherent_load(f) != epoch) {
-                if (coherent_load(error) != 0) {
+            // the shared error word (one address every workgroup reads) on
+            // every 8th poll
+            for (uint32_t poll = 0; coherent_load(f) != epoch; ++poll) {
+                if ((poll & 7) == 7 && coherent_load(error) != 0) {
                     ok = 0;
                     break;
                 }
@@ -720,7 +728,7 @@ __device__ __forceinline__ bool load_tagged(uint64_t (&v)[N], const uint64_t* ba
     }
     if (ok) return true;
     const uint64_t start = wall_clock64();
-    while (true) {
+    for (uint32_t poll = 0;; ++poll) {
 #pragma unroll
         for (int k = 0; k < N; ++k) {
             if (k < n && !has_tag(v[k], epoch))
@@ -730,7 +738,9 @@ __device__ __forceinline__ bool load_tagged(uint64_t (&v)[N], const uint64_t* ba
 #pragma unroll
         for (int k = 0; k < N; ++k) ok = ok && (k >= n || has_tag(v[k], epoch));
         if (ok) return true;
-        if (coherent_load(error) != 0) return false;
+        // the shared error word (one address every workgroup reads) on every
+        // 8th poll
+        if ((poll & 7) == 7 && coherent_load(error) != 0) return false;
         if (wall_clock64() - start > limit_ticks) {
             int32_t expected = 0;
             __hip_atomic_compare_exchange_strong(error, &expected, 1, __ATOMIC_RELAXED, __ATOMIC_RELAXED,

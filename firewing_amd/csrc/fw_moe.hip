@@ -512,6 +512,7 @@ void launch_decode(firewing_hip_context* c, size_t first, size_t n, int T, int o
     p.n_gu = p.n_shared + (p.cpairs > 0 ? p.nb_rows + p.n_c : p.n_b);
     p.cu_count = c->cu_count;
     p.input_by_tags = p.cpairs > 0 ? 1 : 0;
+    p.rank_slots = p.cpairs > 0 ? 1 : 0;  // the fused one-token C task reads rank-ordered slots
     p.trace = c->trace;
     // The kernel reads its parameters from a device copy; upload only on change
     // (the copy is stream-ordered before the launch; pageable source, staged).
