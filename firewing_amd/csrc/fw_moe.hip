@@ -1224,8 +1224,14 @@ static void prefill_reserve(firewing_hip_context* c, size_t tokens, hipStream_t 
 
 // The many-token block on device buffers x [T][H] -> out [T][H]; the
 // selection stays in c->pf (ids, scores, logits, gate logits, mixture).
+// With `marks` (7 events), an event is recorded before the router and after
+// each phase: router logits, selection, grouping, gate/up GEMM, down GEMM,
+// combine.
 static void launch_prefill(firewing_hip_context* c, size_t layer, const uint16_t* x, size_t tokens, uint16_t* out,
-                           bool keep_mixture, hipStream_t s) {
+                           bool keep_mixture, hipStream_t s, hipEvent_t* marks = nullptr) {
+    auto mark = [&](int i) {
+        if (marks) check(hipEventRecord(marks[i], s), "hipEventRecord");
+    };
     auto& f = c->pf;
     const firewing_hip_shape& sh = c->shape;
     const int T = (int)tokens, H = (int)sh.hidden, E = (int)sh.experts, K = (int)sh.top_k;
@@ -1246,6 +1252,7 @@ static void launch_prefill(firewing_hip_context* c, size_t layer, const uint16_t
     }
     // router logits on the matrix units; tiles whose inputs could meet a
     // denormal or an overflow there are recomputed on the vector units
+    mark(0);
     const int row_tiles = (G + kPfMxRows - 1) / kPfMxRows;
     const int mx_tiles = (T + kPfMxTokens - 1) / kPfMxTokens * row_tiles;
     hipLaunchKernelGGL(k_pf_router_mx, dim3((mx_tiles + 7) / 8 * 8), dim3(kPfMxThreads), kPfMxLds, s, x, T, H,
@@ -1254,8 +1261,10 @@ static void launch_prefill(firewing_hip_context* c, size_t layer, const uint16_t
     hipLaunchKernelGGL(k_pf_router, dim3((T + kPfRouterTokens - 1) / kPfRouterTokens, (G + kPfRouterRows - 1) / kPfRouterRows),
                        dim3(256), 0, s, x, T, H, c->router[layer], E, f.logits, f.gate, f.redo, row_tiles);
     check(hipGetLastError(), "k_pf_router launch");
+    mark(1);
     hipLaunchKernelGGL(k_select, dim3(T), dim3(64), 0, s, f.logits, E, K, f.ids, f.scores, 1, c->error);
     check(hipGetLastError(), "k_select launch");
+    mark(2);
     hipLaunchKernelGGL(k_pf_zero, dim3((G + 255) / 256), dim3(256), 0, s, f.g.counts, f.g.cursor, G);
     const int chunks = (T * K + kPfChunk - 1) / kPfChunk;
     hipLaunchKernelGGL(k_pf_count, dim3(chunks), dim3(256), 0, s, f.ids, T * K, E, f.g.counts);
@@ -1263,6 +1272,7 @@ static void launch_prefill(firewing_hip_context* c, size_t layer, const uint16_t
     hipLaunchKernelGGL(k_pf_scatter, dim3(chunks + (T + 255) / 256), dim3(256), 0, s, f.g, f.ids, f.scores, f.gate,
                        T, K, E);
     check(hipGetLastError(), "grouping launch");
+    mark(3);
     PfGemm gu{};
     gu.a = x;
     gu.lda = H;
@@ -1280,6 +1290,7 @@ static void launch_prefill(firewing_hip_context* c, size_t layer, const uint16_t
     const int m_grid = (max_tiles + kPfXcds - 1) / kPfXcds * kPfXcds;
     hipLaunchKernelGGL(k_pf_gemm<kPfGateUp>, dim3(m_grid * gu.n_tiles), dim3(kPfGemmThreads), kPfGemmLds, s, gu, f.g);
     check(hipGetLastError(), "k_pf_gemm gate/up launch");
+    mark(4);
     PfGemm dn = gu;
     dn.a = f.act;
     dn.lda = Imax;
@@ -1290,9 +1301,11 @@ static void launch_prefill(firewing_hip_context* c, size_t layer, const uint16_t
     dn.n_tiles = H / kPfTileN;
     hipLaunchKernelGGL(k_pf_gemm<kPfDown>, dim3(m_grid * dn.n_tiles), dim3(kPfGemmThreads), kPfGemmLds, s, dn, f.g);
     check(hipGetLastError(), "k_pf_gemm down launch");
+    mark(5);
     hipLaunchKernelGGL(k_pf_combine, dim3(T), dim3(256), 0, s, f.weighted, f.g, T, K, H, E, out,
                        keep_mixture ? f.mixture : nullptr);
     check(hipGetLastError(), "k_pf_combine launch");
+    mark(6);
 }
 
 bool firewing_hip_prefill_block_dev(firewing_hip_context* c, size_t layer, const uint16_t* hidden, size_t tokens,
@@ -1310,6 +1323,42 @@ bool firewing_hip_prefill_block_dev(firewing_hip_context* c, size_t layer, const
         launch_prefill(c, layer, hidden, tokens, out, false, s);
         if (ids) check(hipMemcpyAsync(ids, c->pf.ids, tokens * K * 4, hipMemcpyDeviceToDevice, s), "copy ids");
         if (scores) check(hipMemcpyAsync(scores, c->pf.scores, tokens * K * 2, hipMemcpyDeviceToDevice, s), "copy scores");
+        return true;
+    });
+}
+
+bool firewing_hip_prefill_block_profile(firewing_hip_context* c, size_t layer, const uint16_t* hidden,
+                                        size_t tokens, uint16_t* out, void* stream, double* phase_us,
+                                        size_t phases) {
+    return guarded([&] {
+        std::string why;
+        if (!prefill_args_ok(c, layer, tokens, FIREWING_HIP_LOGITS_TREE32, &why)) return fail("prefill_block: " + why);
+        if (!hidden || !out || !phase_us) return fail("prefill_block_profile: null pointer");
+        if (phases != 6) return fail("prefill_block_profile: phases must be 6");
+        if (reinterpret_cast<uintptr_t>(hidden) % 16 || reinterpret_cast<uintptr_t>(out) % 16)
+            return fail("prefill_block: hidden and out must be 16-byte aligned");
+        hipEvent_t marks[7] = {};
+        struct Events {
+            hipEvent_t* e;
+            ~Events() {
+                for (int i = 0; i < 7; ++i)
+                    if (e[i]) (void)hipEventDestroy(e[i]);
+            }
+        } owned{marks};
+        for (int i = 0; i < 7; ++i) check(hipEventCreate(&marks[i]), "hipEventCreate");
+        hipStream_t s;
+        {
+            Ordered ordered(c, stream);
+            s = ordered.s;
+            prefill_reserve(c, tokens, s);
+            launch_prefill(c, layer, hidden, tokens, out, false, s, marks);
+        }
+        check(hipEventSynchronize(marks[6]), "hipEventSynchronize");
+        for (int i = 0; i < 6; ++i) {
+            float ms = 0.0f;
+            check(hipEventElapsedTime(&ms, marks[i], marks[i + 1]), "hipEventElapsedTime");
+            phase_us[i] = 1000.0 * ms;
+        }
         return true;
     });
 }

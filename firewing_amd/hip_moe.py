@@ -83,6 +83,7 @@ _SIGNATURES = {
     "firewing_hip_sparse_moe_block_dev": (_b, [_vp, _sz, _vp, _sz, ctypes.c_int, _vp, _vp]),
     "firewing_hip_prefill_block": (_b, [_vp, _sz, _u16p, _sz, _u16p, ctypes.POINTER(BlockCaptures)]),
     "firewing_hip_prefill_block_dev": (_b, [_vp, _sz, _vp, _sz, _vp, _vp, _vp, _vp]),
+    "firewing_hip_prefill_block_profile": (_b, [_vp, _sz, _vp, _sz, _vp, _vp, ctypes.POINTER(ctypes.c_double), _sz]),
     "firewing_hip_moe_step_dev": (_b, [_vp, _vp, _sz, ctypes.c_int, _b, _vp, _vp, _vp, _vp, _vp]),
     "firewing_hip_moe_step": (_b, [_vp, _u16p, _sz, ctypes.c_int, _b, _u16p, _u16p, _vp, _u16p]),
     "firewing_hip_synchronize": (_b, [_vp]),
@@ -368,6 +369,16 @@ class MoeContext:
         _call("firewing_hip_moe_step", self._h, _p16(x), T, order, bias_feature, _p16(resid),
               _p16(blocks), ids.ctypes.data, _p16(scores))
         return resid, blocks, ids, scores
+
+    PREFILL_PHASES = ("router", "select", "group", "gemm_gate_up", "gemm_down", "combine")
+
+    def prefill_block_profile(self, layer: int, hidden, tokens: int, out, stream=None) -> dict:
+        """The device-pointer prefill block timed by phase (microseconds, HIP
+        events on the launch stream); waits for it."""
+        us = (ctypes.c_double * 6)()
+        _call("firewing_hip_prefill_block_profile", self._h, layer, _addr(hidden), tokens, _addr(out),
+              _addr(stream), us, 6)
+        return dict(zip(self.PREFILL_PHASES, [float(v) for v in us]))
 
     def moe_step_dev(self, hidden, tokens: int, residual, block_out=None, ids=None, scores=None,
                      order: int = LOGITS_TREE32, bias_feature: bool = True, stream=None) -> None:

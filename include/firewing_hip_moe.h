@@ -194,6 +194,16 @@ bool firewing_hip_prefill_block_dev(firewing_hip_context* ctx, size_t layer, con
                                     size_t tokens, uint16_t* out, int32_t* ids, uint16_t* scores,
                                     void* stream);
 
+/* No counterpart in the reference: a measurement aid. The block of
+ * firewing_hip_prefill_block_dev, queued on `stream` with HIP events between
+ * its phases and waited for; phase_us[0..5] (phases == 6) receive the
+ * microseconds of the router logits, the selection (top-k and scores), the
+ * grouping of (token, expert) pairs, the gate/up GEMM, the down GEMM and the
+ * ordered combine. */
+bool firewing_hip_prefill_block_profile(firewing_hip_context* ctx, size_t layer, const uint16_t* hidden,
+                                        size_t tokens, uint16_t* out, void* stream, double* phase_us,
+                                        size_t phases);
+
 /* All resident layers for T <= 4 tokens in one persistent launch: the
  * 48-layer decode step the overlap benches emulate with 48 execute_exact()
  * calls (src/overlap_bound.rs:732-734). Layers are chained by a pre-norm

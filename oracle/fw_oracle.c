@@ -721,3 +721,140 @@ int fwo_synth_step_timed(const fwo_shape* shape, const fwo_synth_config* config,
     free(hn);
     return ok;
 }
+
+/* ---- CPU baseline timing (the benchmark's reported CPU leg) ------------------ */
+
+/* rows of linear_bf16 (src/expert.rs:554-560) split over threads; each row's
+ * dot is the same sequential tree32 dot. */
+static void linear_rows_mt(const uint16_t* w, const uint16_t* x, size_t rows, size_t cols, uint16_t* out,
+                           int threads) {
+#pragma omp parallel for num_threads(threads) schedule(static)
+    for (long r = 0; r < (long)rows; ++r) out[r] = fwo_to_bf16(fwo_dot_tree32(w + (size_t)r * cols, x, cols));
+}
+
+/* block_core for one token with the matrix rows split over threads (router
+ * rows, each expert's gate_up and down rows, the mixture over hidden
+ * elements): every output is computed by the same operations in the same
+ * order as block_core (TREE32 logits). */
+static int block_rows_mt(const fwo_shape* s, const synth_layer* L, const uint16_t* hidden, uint16_t* out,
+                         int threads) {
+    size_t H = s->hidden, I = s->intermediate, E = s->experts, K = s->top_k, Is = s->shared_intermediate;
+    uint16_t* logits = (uint16_t*)malloc(E * sizeof(uint16_t));
+    uint16_t* scores = (uint16_t*)malloc(K * sizeof(uint16_t));
+    uint16_t* gu = (uint16_t*)malloc(2 * (I > Is ? I : Is) * sizeof(uint16_t));
+    uint16_t* act = (uint16_t*)malloc((I > Is ? I : Is) * sizeof(uint16_t));
+    uint16_t* dn = (uint16_t*)malloc(K * H * sizeof(uint16_t));
+    uint16_t* sd = (uint16_t*)malloc(H * sizeof(uint16_t));
+    int32_t ids[64];
+    int ok = logits && scores && gu && act && dn && sd;
+    if (ok) {
+        linear_rows_mt(L->router, hidden, E, H, logits, threads);
+        for (size_t e = 0; e < E; ++e) {
+            if (isnan(fwo_from_bf16(logits[e]))) ok = 0;
+        }
+        ok = ok && fwo_topk_total_order(logits, E, K, ids);
+        ok = ok && fwo_route_scores(logits, E, ids, K, scores);
+    }
+    size_t order_idx[64];
+    for (size_t r = 0; r < K; ++r) order_idx[r] = r;
+    for (size_t a = 1; a < K; ++a)
+        for (size_t b = a; b > 0 && ids[order_idx[b - 1]] > ids[order_idx[b]]; --b) {
+            size_t t = order_idx[b];
+            order_idx[b] = order_idx[b - 1];
+            order_idx[b - 1] = t;
+        }
+    for (size_t n = 0; ok && n < K; ++n) {
+        size_t r = order_idx[n];
+        linear_rows_mt(L->gate_up[ids[r]], hidden, 2 * I, H, gu, threads);
+        fwo_swiglu_bf16(gu, gu + I, I, act);
+        linear_rows_mt(L->down[ids[r]], act, H, I, dn + n * H, threads);
+        float w = fwo_from_bf16(scores[r]);
+        for (size_t h = 0; h < H; ++h) dn[n * H + h] = fwo_to_bf16(fwo_from_bf16(dn[n * H + h]) * w);
+    }
+    if (ok) {
+        linear_rows_mt(L->shared_gate, hidden, Is, H, gu, threads);
+        linear_rows_mt(L->shared_up, hidden, Is, H, gu + Is, threads);
+        fwo_swiglu_bf16(gu, gu + Is, Is, act);
+        linear_rows_mt(L->shared_down, act, H, Is, sd, threads);
+        uint16_t gate_logit;
+        fwo_linear_bf16(L->shared_expert_gate, hidden, 1, H, &gate_logit);
+        float sigmoid = fwo_from_bf16(fwo_sigmoid_bf16(gate_logit));
+#pragma omp parallel for num_threads(threads) schedule(static)
+        for (long h = 0; h < (long)H; ++h) {
+            uint16_t mix = fwo_to_bf16(0.0f);
+            for (size_t n = 0; n < K; ++n) mix = fwo_add_bf16(mix, dn[n * H + h]);
+            out[h] = fwo_add_bf16(mix, fwo_to_bf16(sigmoid * fwo_from_bf16(sd[h])));
+        }
+    }
+    free(logits);
+    free(scores);
+    free(gu);
+    free(act);
+    free(dn);
+    free(sd);
+    return ok;
+}
+
+/* Times the block of one synthetic layer on `tokens` inputs: the layer's
+ * dense weights and the experts the tokens select are generated first
+ * (untimed); then `warmups` untimed and `runs` timed evaluations of the whole
+ * block for every token (pre-norm when `prenorm`, route, experts, mixture,
+ * shared expert, combine), seconds per run into samples[runs]; the last
+ * run's outputs into out [tokens][H] (NULL to skip). threads > 1: the tokens
+ * in parallel when there are at least as many as threads, else each matrix's
+ * rows (TREE32 logits only). */
+int fwo_bench_block(const fwo_shape* shape, const fwo_synth_config* config, uint32_t layer,
+                    const uint16_t* hidden, size_t tokens, int prenorm, int warmups, int runs,
+                    double* samples, uint16_t* out) {
+    size_t H = shape->hidden, E = shape->experts, K = shape->top_k;
+    if (K == 0 || K > 64 || K > E || tokens == 0) return 0;
+    int threads = config->threads > 0 ? config->threads : 1;
+    synth_layer L;
+    if (!synth_layer_dense(shape, config, layer, &L)) {
+        synth_layer_free(&L);
+        return 0;
+    }
+    uint16_t* hn = (uint16_t*)malloc(tokens * H * sizeof(uint16_t));
+    int32_t* sel = (int32_t*)malloc(tokens * K * sizeof(int32_t));
+    uint16_t* sc = (uint16_t*)malloc(tokens * K * sizeof(uint16_t));
+    uint16_t* lg = (uint16_t*)malloc(tokens * E * sizeof(uint16_t));
+    uint16_t* o = (uint16_t*)malloc(tokens * H * sizeof(uint16_t));
+    int ok = hn && sel && sc && lg && o;
+    for (size_t t = 0; ok && t < tokens; ++t) {
+        if (prenorm)
+            fwo_rms_norm_bf16(hidden + t * H, H, config->bias_feature, hn + t * H);
+        else
+            memcpy(hn + t * H, hidden + t * H, H * sizeof(uint16_t));
+        ok = fwo_route(L.router, hn + t * H, E, H, K, config->order, sel + t * K, lg + t * E, sc + t * K);
+        for (size_t r = 0; ok && r < K; ++r) ok = synth_layer_expert(shape, config, layer, &L, sel[t * K + r]);
+    }
+    const int by_rows = threads > 1 && (long)tokens < threads && config->order == FWO_ORDER_TREE32;
+    for (int run = 0; ok && run < warmups + runs; ++run) {
+        double t0 = now_seconds();
+        if (by_rows) {
+            for (size_t t = 0; ok && t < tokens; ++t) {
+                if (prenorm) fwo_rms_norm_bf16(hidden + t * H, H, config->bias_feature, hn + t * H);
+                ok = block_rows_mt(shape, &L, hn + t * H, o + t * H, threads);
+            }
+        } else {
+#pragma omp parallel for num_threads(threads) schedule(dynamic, 1) reduction(&& : ok)
+            for (long t = 0; t < (long)tokens; ++t) {
+                if (prenorm) fwo_rms_norm_bf16(hidden + (size_t)t * H, H, config->bias_feature, hn + (size_t)t * H);
+                ok = ok && block_core(shape, L.router, (const uint16_t* const*)L.gate_up,
+                                      (const uint16_t* const*)L.down, L.shared_gate, L.shared_up, L.shared_down,
+                                      L.shared_expert_gate, hn + (size_t)t * H, config->order, NULL, NULL,
+                                      o + (size_t)t * H, NULL);
+            }
+        }
+        double dt = now_seconds() - t0;
+        if (run >= warmups && samples) samples[run - warmups] = dt;
+    }
+    if (ok && out) memcpy(out, o, tokens * H * sizeof(uint16_t));
+    free(hn);
+    free(sel);
+    free(sc);
+    free(lg);
+    free(o);
+    synth_layer_free(&L);
+    return ok;
+}

@@ -121,6 +121,9 @@ int fwo_synth_step_timed(const fwo_shape* shape, const fwo_synth_config* config,
 int fwo_synth_route(const fwo_shape* shape, const fwo_synth_config* config, uint32_t layer,
                     const uint16_t* hidden, size_t tokens, int32_t* ids, uint16_t* scores,
                     uint16_t* logits);
+int fwo_bench_block(const fwo_shape* shape, const fwo_synth_config* config, uint32_t layer,
+                    const uint16_t* hidden, size_t tokens, int prenorm, int warmups, int runs,
+                    double* samples, uint16_t* out);
 
 #ifdef __cplusplus
 }

@@ -140,6 +140,10 @@ def lib() -> ctypes.CDLL:
         L.fwo_synth_step_timed.argtypes = [ctypes.POINTER(Shape), ctypes.POINTER(SynthConfig),
                                            ctypes.c_uint32, _u16p, _size, _u16p,
                                            ctypes.POINTER(ctypes.c_double)]
+        L.fwo_bench_block.restype = ctypes.c_int
+        L.fwo_bench_block.argtypes = [ctypes.POINTER(Shape), ctypes.POINTER(SynthConfig), ctypes.c_uint32,
+                                      _u16p, _size, ctypes.c_int, ctypes.c_int, ctypes.c_int,
+                                      ctypes.POINTER(ctypes.c_double), _u16p]
         L.fwo_synth_route.restype = ctypes.c_int
         L.fwo_synth_route.argtypes = [ctypes.POINTER(Shape), ctypes.POINTER(SynthConfig),
                                       ctypes.c_uint32, _u16p, _size, _i32p, _u16p, _u16p]
@@ -445,6 +449,22 @@ def synth_step_timed(shape: dict, seed: int, layers: int, hidden: np.ndarray, bi
                                       _p16(resid), ctypes.byref(secs)):
         raise ValueError("timed synthetic step failed")
     return resid, secs.value
+
+
+def bench_block(shape: dict, seed: int, layer: int, hidden: np.ndarray, prenorm: bool, warmups: int, runs: int,
+                threads: int = 1, bias_feature=True, order=ORDER_TREE32):
+    """CPU baseline timing: (seconds per run [runs], outputs of the last run
+    [T, H]) for the block of one synthetic layer over the tokens of `hidden`
+    (weights generated untimed; see fwo_bench_block)."""
+    h = _u16(hidden).reshape(-1, shape["hidden"])
+    T = h.shape[0]
+    samples = np.zeros(runs, dtype=np.float64)
+    out = np.empty((T, shape["hidden"]), dtype=np.uint16)
+    s, c = _shape(shape), _config(seed, bias_feature, order, threads)
+    if not lib().fwo_bench_block(ctypes.byref(s), ctypes.byref(c), layer, _p16(h), T, int(prenorm), warmups, runs,
+                                 samples.ctypes.data_as(ctypes.POINTER(ctypes.c_double)), _p16(out)):
+        raise ValueError("block timing failed")
+    return samples, out
 
 
 # ---- the reference's own top-k shim (built from native/topk_shim.cpp) ---------------

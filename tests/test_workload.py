@@ -40,3 +40,25 @@ def test_router_bias_realises_zipf_popularity():
         keep = f > 0
         slope = np.polyfit(np.log(r[keep]), np.log(f[keep]), 1)[0]
         assert abs(-slope - 1.1) < 0.08, (layer, slope)
+
+
+def test_cpu_baseline_timing_computes_the_same_block():
+    # The benchmark's CPU leg (fwo_bench_block) must time the oracle's own
+    # block: outputs equal synth_block for one thread, for row-parallel
+    # threads (one token) and for token-parallel threads (several tokens).
+    shape = dict(hidden=256, intermediate=128, experts=64, top_k=6, shared_intermediate=128)
+    x1 = fo.synth_hidden(SEED, 1, shape["hidden"], True, first_token=5)
+    x4 = fo.synth_hidden(SEED, 4, shape["hidden"], True, first_token=9)
+    ref1 = fo.synth_block(shape, SEED, 3, x1)[0]
+    ref4 = fo.synth_block(shape, SEED, 3, x4)[0]
+    for threads in (1, 4):
+        t, out = fo.bench_block(shape, SEED, 3, x1, prenorm=False, warmups=1, runs=3, threads=threads)
+        assert t.shape == (3,) and (t > 0).all()
+        assert np.array_equal(out, ref1), threads
+        t, out = fo.bench_block(shape, SEED, 3, x4, prenorm=False, warmups=0, runs=2, threads=threads)
+        assert np.array_equal(out, ref4), threads
+    # with the pre-norm of the chained step
+    normed = fo.rms_norm_bf16(x1[0], True)
+    ref_n = fo.synth_block(shape, SEED, 3, normed[None])[0]
+    _, out = fo.bench_block(shape, SEED, 3, x1, prenorm=True, warmups=0, runs=1, threads=2)
+    assert np.array_equal(out, ref_n)
