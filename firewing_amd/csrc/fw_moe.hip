@@ -1369,6 +1369,10 @@ bool firewing_hip_prefill_block(firewing_hip_context* c, size_t layer, const uin
         std::string why;
         if (!prefill_args_ok(c, layer, tokens, FIREWING_HIP_LOGITS_TREE32, &why)) return fail("prefill_block: " + why);
         if (!hidden || !out) return fail("prefill_block: null pointer");
+        if (cap && (cap->shared_gate || cap->shared_up || cap->shared_swiglu || cap->shared_down ||
+                    cap->shared_gate_logit || cap->gated_shared || cap->weighted_down))
+            return fail("prefill_block: the shared-expert and weighted-down captures are taken by "
+                        "firewing_hip_sparse_moe_block");
         Ordered ordered(c, nullptr);
         hipStream_t s = ordered.s;
         prefill_reserve(c, tokens, s);
@@ -1435,6 +1439,77 @@ bool firewing_hip_sparse_moe_block_dev(firewing_hip_context* c, size_t layer,
     });
 }
 
+namespace {
+
+bool wants_verifier_captures(const firewing_hip_block_captures* cap) {
+    return cap && (cap->routed_mixture || cap->shared_gate || cap->shared_up || cap->shared_swiglu ||
+                   cap->shared_down || cap->shared_gate_logit || cap->gated_shared || cap->weighted_down);
+}
+
+// The verifier captures of a decode block (src/expert.rs:1154-1199,
+// src/decoder_layer.rs:528-586): the block's intermediate vectors, recomputed
+// with the standalone exact kernels on the resident weights of `layer` for the
+// T inputs at x (device), the selection (ids, scores: host, rank order) and
+// shared-gate sigmoids (host) the fused kernel produced. The fused kernel keeps
+// none of them; the arithmetic is the same, so they are the vectors its output
+// was combined from.
+void take_verifier_captures(firewing_hip_context* c, size_t layer, const uint16_t* x, size_t tokens,
+                            const int32_t* ids, const uint16_t* scores, const uint16_t* sig,
+                            firewing_hip_block_captures* cap, hipStream_t s) {
+    const size_t H = c->shape.hidden, I = c->shape.intermediate, E = c->shape.experts;
+    const size_t K = c->shape.top_k, Is = c->shape.shared_intermediate;
+    const int T = (int)tokens;
+    const dim3 blk(256);
+    auto cover = [](size_t n) { return dim3((unsigned)((n + 255) / 256)); };
+    DeviceBuffer sg(tokens * Is * 2), su(tokens * Is * 2), ss(tokens * Is * 2), sd(tokens * H * 2),
+        gl(tokens * 2), gs(tokens * H * 2);
+    launch_linear(c->shared_gate[layer], x, (int)Is, (int)H, T, sg.as<uint16_t>(), s);
+    launch_linear(c->shared_up[layer], x, (int)Is, (int)H, T, su.as<uint16_t>(), s);
+    hipLaunchKernelGGL(k_swiglu, cover(tokens * Is), blk, 0, s, sg.as<uint16_t>(), su.as<uint16_t>(),
+                       tokens * Is, ss.as<uint16_t>());
+    check(hipGetLastError(), "k_swiglu launch");
+    launch_linear(c->shared_down[layer], ss.as<uint16_t>(), (int)H, (int)Is, T, sd.as<uint16_t>(), s);
+    launch_linear(c->router[layer] + E * H, x, 1, (int)H, T, gl.as<uint16_t>(), s);  // shared_expert_gate
+    for (size_t t = 0; t < tokens; ++t) {
+        hipLaunchKernelGGL(k_scale_bf16, cover(H), blk, 0, s, sd.as<uint16_t>() + t * H, sig[t], H,
+                           gs.as<uint16_t>() + t * H);
+        check(hipGetLastError(), "k_scale_bf16 launch");
+    }
+    // routed experts of each token in execution (ascending id) order, then the mixture
+    DeviceBuffer go(2 * I * 2), act(I * 2), dn(H * 2), wd(tokens * K * H * 2), mix(tokens * H * 2);
+    for (size_t t = 0; t < tokens; ++t) {
+        std::vector<size_t> rank(K);
+        for (size_t r = 0; r < K; ++r) rank[r] = r;
+        std::sort(rank.begin(), rank.end(), [&](size_t a, size_t b) { return ids[t * K + a] < ids[t * K + b]; });
+        for (size_t n = 0; n < K; ++n) {
+            const size_t e = (size_t)ids[t * K + rank[n]];
+            launch_linear(c->gate_up[layer] + e * 2 * I * H, x + t * H, (int)(2 * I), (int)H, 1,
+                          go.as<uint16_t>(), s);
+            hipLaunchKernelGGL(k_swiglu, cover(I), blk, 0, s, go.as<uint16_t>(), go.as<uint16_t>() + I, I,
+                               act.as<uint16_t>());
+            check(hipGetLastError(), "k_swiglu launch");
+            launch_linear(c->down[layer] + e * H * I, act.as<uint16_t>(), (int)H, (int)I, 1, dn.as<uint16_t>(), s);
+            hipLaunchKernelGGL(k_scale_bf16, cover(H), blk, 0, s, dn.as<uint16_t>(), scores[t * K + rank[n]], H,
+                               wd.as<uint16_t>() + (t * K + n) * H);
+            check(hipGetLastError(), "k_scale_bf16 launch");
+        }
+        hipLaunchKernelGGL(k_mixture, cover(H), blk, 0, s, wd.as<uint16_t>() + t * K * H, (int)K, (int)H,
+                           mix.as<uint16_t>() + t * H);
+        check(hipGetLastError(), "k_mixture launch");
+    }
+    if (cap->shared_gate) download(cap->shared_gate, sg.ptr, tokens * Is * 2, s);
+    if (cap->shared_up) download(cap->shared_up, su.ptr, tokens * Is * 2, s);
+    if (cap->shared_swiglu) download(cap->shared_swiglu, ss.ptr, tokens * Is * 2, s);
+    if (cap->shared_down) download(cap->shared_down, sd.ptr, tokens * H * 2, s);
+    if (cap->shared_gate_logit) download(cap->shared_gate_logit, gl.ptr, tokens * 2, s);
+    if (cap->gated_shared) download(cap->gated_shared, gs.ptr, tokens * H * 2, s);
+    if (cap->weighted_down) download(cap->weighted_down, wd.ptr, tokens * K * H * 2, s);
+    if (cap->routed_mixture) download(cap->routed_mixture, mix.ptr, tokens * H * 2, s);
+    check(hipStreamSynchronize(s), "hipStreamSynchronize");
+}
+
+}  // namespace
+
 bool firewing_hip_sparse_moe_block(firewing_hip_context* c, size_t layer,
                                    const uint16_t* hidden, size_t tokens, int order,
                                    uint16_t* out, firewing_hip_block_captures* cap) {
@@ -1464,15 +1539,19 @@ bool firewing_hip_sparse_moe_block(firewing_hip_context* c, size_t layer,
                     }
                 }
             }
+            std::vector<int32_t> ids(tokens * K);
+            std::vector<uint16_t> scores(tokens * K), sig(tokens);
+            download(ids.data(), c->ids, ids.size() * 4, s);
+            download(scores.data(), c->scores, tokens * K * 2, s);
+            download(sig.data(), c->sig, tokens * 2, s);
+            check(hipStreamSynchronize(s), "hipStreamSynchronize");
             if (cap->selected_experts) {
-                std::vector<int32_t> ids(tokens * K);
-                download(ids.data(), c->ids, ids.size() * 4, s);
-                check(hipStreamSynchronize(s), "hipStreamSynchronize");
                 for (size_t i = 0; i < ids.size(); ++i) cap->selected_experts[i] = (size_t)ids[i];
             }
-            if (cap->selected_scores) download(cap->selected_scores, c->scores, tokens * K * 2, s);
-            if (cap->shared_gate_sigmoid) download(cap->shared_gate_sigmoid, c->sig, tokens * 2, s);
-            if (cap->routed_mixture) return fail("sparse_moe_block: routed_mixture capture is not kept by the fused kernel");
+            if (cap->selected_scores) std::copy(scores.begin(), scores.end(), cap->selected_scores);
+            if (cap->shared_gate_sigmoid) std::copy(sig.begin(), sig.end(), cap->shared_gate_sigmoid);
+            if (wants_verifier_captures(cap))
+                take_verifier_captures(c, layer, c->xin, tokens, ids.data(), scores.data(), sig.data(), cap, s);
         }
         check(hipStreamSynchronize(s), "hipStreamSynchronize");
         return true;

@@ -48,10 +48,17 @@ class Shape(ctypes.Structure):
                 ("shared_intermediate", ctypes.c_size_t), ("layers", ctypes.c_size_t)]
 
 
+VERIFIER_CAPTURES = ("routed_mixture", "shared_gate", "shared_up", "shared_swiglu", "shared_down",
+                     "shared_gate_logit", "gated_shared", "weighted_down")
+
+
 class BlockCaptures(ctypes.Structure):
     _fields_ = [("router_logits", ctypes.c_void_p), ("selected_experts", ctypes.c_void_p),
                 ("selected_scores", ctypes.c_void_p), ("routed_mixture", ctypes.c_void_p),
-                ("shared_gate_sigmoid", ctypes.c_void_p)]
+                ("shared_gate_sigmoid", ctypes.c_void_p), ("shared_gate", ctypes.c_void_p),
+                ("shared_up", ctypes.c_void_p), ("shared_swiglu", ctypes.c_void_p),
+                ("shared_down", ctypes.c_void_p), ("shared_gate_logit", ctypes.c_void_p),
+                ("gated_shared", ctypes.c_void_p), ("weighted_down", ctypes.c_void_p)]
 
 
 _u16p = ctypes.POINTER(ctypes.c_uint16)
@@ -315,20 +322,37 @@ class MoeContext:
               _p16(out))
         return out
 
-    def sparse_moe_block(self, layer: int, hidden, order: int = LOGITS_TREE32) -> dict:
+    def sparse_moe_block(self, layer: int, hidden, order: int = LOGITS_TREE32,
+                         captures=()) -> dict:
+        """The block for T <= 4 tokens. `captures` names verifier captures to
+        take as well (any of VERIFIER_CAPTURES; "all" for every one); they are
+        returned under their names, [T, ...] (weighted_down [T, K, H] in
+        ascending expert id)."""
         x = _u16(hidden).reshape(-1, self.H)
         T = x.shape[0]
+        want = VERIFIER_CAPTURES if captures == "all" else tuple(captures)
+        unknown = set(want) - set(VERIFIER_CAPTURES)
+        if unknown:
+            raise ValueError(f"unknown captures {sorted(unknown)}")
         out = np.empty((T, self.H), dtype=np.uint16)
         logits = np.empty((T, self.E), dtype=np.uint16)
         ids = np.empty((T, self.K), dtype=np.uint64)
         scores = np.empty((T, self.K), dtype=np.uint16)
         sig = np.empty(T, dtype=np.uint16)
-        cap = BlockCaptures(logits.ctypes.data, ids.ctypes.data, scores.ctypes.data, None,
-                            sig.ctypes.data)
+        dims = {"routed_mixture": (self.H,), "shared_gate": (self.Is,), "shared_up": (self.Is,),
+                "shared_swiglu": (self.Is,), "shared_down": (self.H,), "shared_gate_logit": (),
+                "gated_shared": (self.H,), "weighted_down": (self.K, self.H)}
+        extra = {k: np.empty((T,) + dims[k], dtype=np.uint16) for k in want}
+        cap = BlockCaptures(logits.ctypes.data, ids.ctypes.data, scores.ctypes.data,
+                            None, sig.ctypes.data)
+        for k, a in extra.items():
+            setattr(cap, k, a.ctypes.data)
         _call("firewing_hip_sparse_moe_block", self._h, layer, _p16(x), T, order, _p16(out),
               ctypes.byref(cap))
-        return {"out": out, "router_logits": logits, "selected_experts": ids.astype(np.int64),
-                "selected_scores": scores, "shared_gate_sigmoid": sig}
+        res = {"out": out, "router_logits": logits, "selected_experts": ids.astype(np.int64),
+               "selected_scores": scores, "shared_gate_sigmoid": sig}
+        res.update(extra)
+        return res
 
     def sparse_moe_block_dev(self, layer: int, hidden, tokens: int, out, order: int = LOGITS_TREE32,
                              stream=None) -> None:

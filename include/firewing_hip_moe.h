@@ -54,13 +54,28 @@ typedef struct firewing_hip_shape {
     size_t layers;              /* L resident layers */
 } firewing_hip_shape;
 
-/* Optional per-call captures of the block (src/expert.rs:1154-1199 names). */
+/* Optional per-call captures of the block, named as the reference's verifiers
+ * name them (src/expert.rs:1154-1199 verify_sparse_moe_fixture,
+ * src/decoder_layer.rs:460-586 require_capture). Every field may be NULL.
+ * The fused decode kernel keeps the first five fields' values itself (except
+ * routed_mixture); routed_mixture and the fields after shared_gate_sigmoid are
+ * recomputed after the block by the standalone exact kernels on the same
+ * resident weights and the same selection, a slower path taken only when one
+ * of them is asked for. */
 typedef struct firewing_hip_block_captures {
-    uint16_t* router_logits;       /* [T, E] or NULL */
-    size_t* selected_experts;      /* [T, K] rank order, or NULL */
-    uint16_t* selected_scores;     /* [T, K] rank order, or NULL */
-    uint16_t* routed_mixture;      /* [T, H] or NULL */
-    uint16_t* shared_gate_sigmoid; /* [T] or NULL */
+    uint16_t* router_logits;       /* [T, E] */
+    size_t* selected_experts;      /* [T, K] rank order */
+    uint16_t* selected_scores;     /* [T, K] rank order */
+    uint16_t* routed_mixture;      /* [T, H] */
+    uint16_t* shared_gate_sigmoid; /* [T] */
+    uint16_t* shared_gate;         /* [T, Is] */
+    uint16_t* shared_up;           /* [T, Is] */
+    uint16_t* shared_swiglu;       /* [T, Is] */
+    uint16_t* shared_down;         /* [T, H] */
+    uint16_t* shared_gate_logit;   /* [T] */
+    uint16_t* gated_shared;        /* [T, H]: bf16(shared_down * sigmoid) */
+    uint16_t* weighted_down;       /* [T, K, H]: bf16(down * score) per selected expert, in
+                                      execution (ascending id) order (src/decoder_layer.rs:532-579) */
 } firewing_hip_block_captures;
 
 typedef struct firewing_hip_context firewing_hip_context;
@@ -184,7 +199,9 @@ bool firewing_hip_sparse_moe_block_dev(firewing_hip_context* ctx, size_t layer,
  * ascending-id bf16 combine (src/expert.rs:906-956). The expert GEMMs
  * accumulate in the matrix units' order, so block outputs match the reference
  * within a bf16 tolerance rather than bit for bit. Host buffers, synchronous;
- * captures as firewing_hip_sparse_moe_block (routed_mixture supported). */
+ * captures: router_logits, selected_experts, selected_scores, routed_mixture
+ * (the MFMA path's, within the same tolerance) and shared_gate_sigmoid; the
+ * other fields must be NULL. */
 bool firewing_hip_prefill_block(firewing_hip_context* ctx, size_t layer, const uint16_t* hidden,
                                 size_t tokens, uint16_t* out, firewing_hip_block_captures* captures);
 

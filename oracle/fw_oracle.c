@@ -390,6 +390,7 @@ static int block_core(const fwo_shape* s, const uint16_t* router, const uint16_t
         int32_t e = ids[r];
         fwo_expert_bf16(gate_up[e], down[e], hidden, H, I, scores[r], NULL, NULL, NULL, weighted);
         for (size_t h = 0; h < H; ++h) routed[h] = fwo_add_bf16(routed[h], weighted[h]);
+        if (cap != NULL && cap->weighted_down) memcpy(cap->weighted_down + n * H, weighted, H * sizeof(uint16_t));
     }
     fwo_linear_bf16(shared_gate, hidden, Is, H, sg);
     fwo_linear_bf16(shared_up, hidden, Is, H, su);
@@ -402,6 +403,7 @@ static int block_core(const fwo_shape* s, const uint16_t* router, const uint16_t
     for (size_t h = 0; h < H; ++h) {
         uint16_t gated = fwo_to_bf16(sigmoid * fwo_from_bf16(sd[h]));
         out[h] = fwo_add_bf16(routed[h], gated);
+        if (cap != NULL && cap->gated_shared) cap->gated_shared[h] = gated;
     }
     if (cap != NULL) {
         if (cap->logits) memcpy(cap->logits, logits, E * sizeof(uint16_t));
@@ -410,6 +412,10 @@ static int block_core(const fwo_shape* s, const uint16_t* router, const uint16_t
         if (cap->routed_mixture) memcpy(cap->routed_mixture, routed, H * sizeof(uint16_t));
         if (cap->shared_down) memcpy(cap->shared_down, sd, H * sizeof(uint16_t));
         if (cap->shared_gate_sigmoid) cap->shared_gate_sigmoid[0] = gate_sigmoid;
+        if (cap->shared_gate) memcpy(cap->shared_gate, sg, Is * sizeof(uint16_t));
+        if (cap->shared_up) memcpy(cap->shared_up, su, Is * sizeof(uint16_t));
+        if (cap->shared_swiglu) memcpy(cap->shared_swiglu, ss, Is * sizeof(uint16_t));
+        if (cap->shared_gate_logit) cap->shared_gate_logit[0] = gate_logit;
     }
 done:
     free(logits);
@@ -578,9 +584,9 @@ int fwo_synth_route(const fwo_shape* shape, const fwo_synth_config* config, uint
     return ok;
 }
 
-int fwo_synth_block(const fwo_shape* shape, const fwo_synth_config* config, uint32_t layer,
-                    const uint16_t* hidden, size_t tokens, uint16_t* out, int32_t* ids,
-                    uint16_t* scores, uint16_t* logits) {
+static int synth_block(const fwo_shape* shape, const fwo_synth_config* config, uint32_t layer,
+                       const uint16_t* hidden, size_t tokens, uint16_t* out, int32_t* ids,
+                       uint16_t* scores, uint16_t* logits, fwo_block_captures* caps) {
     size_t H = shape->hidden, E = shape->experts, K = shape->top_k;
     if (K == 0 || K > 64 || K > E) return 0;
     synth_layer L;
@@ -611,7 +617,7 @@ int fwo_synth_block(const fwo_shape* shape, const fwo_synth_config* config, uint
                                   (const uint16_t* const*)L.down, L.shared_gate, L.shared_up,
                                   L.shared_down, L.shared_expert_gate, hidden + (size_t)t * H,
                                   config->order, sel + (size_t)t * K, lg + (size_t)t * E,
-                                  out + (size_t)t * H, NULL);
+                                  out + (size_t)t * H, caps ? caps + t : NULL);
         }
     }
     if (ok) {
@@ -624,6 +630,18 @@ int fwo_synth_block(const fwo_shape* shape, const fwo_synth_config* config, uint
     free(lg);
     synth_layer_free(&L);
     return ok;
+}
+
+int fwo_synth_block(const fwo_shape* shape, const fwo_synth_config* config, uint32_t layer,
+                    const uint16_t* hidden, size_t tokens, uint16_t* out, int32_t* ids,
+                    uint16_t* scores, uint16_t* logits) {
+    return synth_block(shape, config, layer, hidden, tokens, out, ids, scores, logits, NULL);
+}
+
+int fwo_synth_block_captured(const fwo_shape* shape, const fwo_synth_config* config, uint32_t layer,
+                             const uint16_t* hidden, size_t tokens, uint16_t* out,
+                             fwo_block_captures* captures) {
+    return synth_block(shape, config, layer, hidden, tokens, out, NULL, NULL, NULL, captures);
 }
 
 /* Chained decode step over `layers` synthetic layers. Workload glue, not in the

@@ -89,6 +89,12 @@ typedef struct {
     uint16_t* routed_mixture; /* [H] or NULL */
     uint16_t* shared_down;    /* [H] or NULL */
     uint16_t* shared_gate_sigmoid; /* [1] or NULL */
+    uint16_t* shared_gate;    /* [Is] or NULL */
+    uint16_t* shared_up;      /* [Is] or NULL */
+    uint16_t* shared_swiglu;  /* [Is] or NULL */
+    uint16_t* shared_gate_logit; /* [1] or NULL */
+    uint16_t* gated_shared;   /* [H] or NULL */
+    uint16_t* weighted_down;  /* [K, H] in execution (ascending id) order, or NULL */
 } fwo_block_captures;
 
 int fwo_sparse_moe_block(const fwo_shape* shape, const fwo_layer* layer, const uint16_t* hidden,
@@ -112,6 +118,11 @@ typedef struct {
 int fwo_synth_block(const fwo_shape* shape, const fwo_synth_config* config, uint32_t layer,
                     const uint16_t* hidden, size_t tokens, uint16_t* out, int32_t* ids,
                     uint16_t* scores, uint16_t* logits);
+/* fwo_synth_block with every capture of the block, one captures record per
+ * token (src/expert.rs:1154-1199, src/decoder_layer.rs:528-586 names). */
+int fwo_synth_block_captured(const fwo_shape* shape, const fwo_synth_config* config, uint32_t layer,
+                             const uint16_t* hidden, size_t tokens, uint16_t* out,
+                             fwo_block_captures* captures);
 int fwo_synth_step(const fwo_shape* shape, const fwo_synth_config* config, uint32_t layers,
                    const uint16_t* hidden, size_t tokens, uint16_t* residual_out,
                    uint16_t* block_out, int32_t* ids, uint16_t* scores);

@@ -58,6 +58,12 @@ class BlockCaptures(ctypes.Structure):
         ("routed_mixture", _u16p),
         ("shared_down", _u16p),
         ("shared_gate_sigmoid", _u16p),
+        ("shared_gate", _u16p),
+        ("shared_up", _u16p),
+        ("shared_swiglu", _u16p),
+        ("shared_gate_logit", _u16p),
+        ("gated_shared", _u16p),
+        ("weighted_down", _u16p),
     ]
 
 
@@ -133,6 +139,10 @@ def lib() -> ctypes.CDLL:
         L.fwo_synth_block.restype = ctypes.c_int
         L.fwo_synth_block.argtypes = [ctypes.POINTER(Shape), ctypes.POINTER(SynthConfig),
                                       ctypes.c_uint32, _u16p, _size, _u16p, _i32p, _u16p, _u16p]
+        L.fwo_synth_block_captured.restype = ctypes.c_int
+        L.fwo_synth_block_captured.argtypes = [ctypes.POINTER(Shape), ctypes.POINTER(SynthConfig),
+                                               ctypes.c_uint32, _u16p, _size, _u16p,
+                                               ctypes.POINTER(BlockCaptures)]
         L.fwo_synth_step.restype = ctypes.c_int
         L.fwo_synth_step.argtypes = [ctypes.POINTER(Shape), ctypes.POINTER(SynthConfig),
                                      ctypes.c_uint32, _u16p, _size, _u16p, _u16p, _i32p, _u16p]
@@ -323,6 +333,30 @@ def mixture_bf16(gate_up_weights, down_weights, hidden, hidden_size: int, interm
     return out
 
 
+CAPTURE_NAMES = ("logits", "ids", "scores", "routed_mixture", "shared_down", "shared_gate_sigmoid",
+                 "shared_gate", "shared_up", "shared_swiglu", "shared_gate_logit", "gated_shared",
+                 "weighted_down")
+
+
+def _capture_arrays(shape: dict, lead: tuple) -> dict:
+    H, E, K = shape["hidden"], shape["experts"], shape["top_k"]
+    Is = shape["shared_intermediate"]
+    dims = {"logits": (E,), "ids": (K,), "scores": (K,), "routed_mixture": (H,), "shared_down": (H,),
+            "shared_gate_sigmoid": (1,), "shared_gate": (Is,), "shared_up": (Is,),
+            "shared_swiglu": (Is,), "shared_gate_logit": (1,), "gated_shared": (H,),
+            "weighted_down": (K, H)}
+    return {k: np.empty(lead + dims[k], dtype=np.int32 if k == "ids" else np.uint16)
+            for k in CAPTURE_NAMES}
+
+
+def _captures_of(arrays: dict, index: tuple) -> BlockCaptures:
+    ptrs = []
+    for k in CAPTURE_NAMES:
+        a = arrays[k][index] if index else arrays[k]
+        ptrs.append(_p32(a) if k == "ids" else _p16(a))
+    return BlockCaptures(*ptrs)
+
+
 def sparse_moe_block(shape: dict, weights: dict, hidden, order: int = ORDER_TREE32) -> dict:
     """One token through a dense-weight block; returns out and captures."""
     s = Shape(shape["hidden"], shape["intermediate"], shape["experts"], shape["top_k"],
@@ -330,16 +364,10 @@ def sparse_moe_block(shape: dict, weights: dict, hidden, order: int = ORDER_TREE
     arrs = {k: _u16(v) for k, v in weights.items()}
     layer = Layer(*[_p16(arrs[k]) for k in ("router", "gate_up", "down", "shared_gate",
                                             "shared_up", "shared_down", "shared_expert_gate")])
-    H, E, K = shape["hidden"], shape["experts"], shape["top_k"]
+    H = shape["hidden"]
     out = np.empty(H, dtype=np.uint16)
-    cap_arrays = {
-        "logits": np.empty(E, dtype=np.uint16), "ids": np.empty(K, dtype=np.int32),
-        "scores": np.empty(K, dtype=np.uint16), "routed_mixture": np.empty(H, dtype=np.uint16),
-        "shared_down": np.empty(H, dtype=np.uint16),
-        "shared_gate_sigmoid": np.empty(1, dtype=np.uint16)}
-    cap = BlockCaptures(_p16(cap_arrays["logits"]), _p32(cap_arrays["ids"]),
-                        _p16(cap_arrays["scores"]), _p16(cap_arrays["routed_mixture"]),
-                        _p16(cap_arrays["shared_down"]), _p16(cap_arrays["shared_gate_sigmoid"]))
+    cap_arrays = _capture_arrays(shape, ())
+    cap = _captures_of(cap_arrays, ())
     x = _u16(hidden)
     if not lib().fwo_sparse_moe_block(ctypes.byref(s), ctypes.byref(layer), _p16(x), order,
                                       _p16(out), ctypes.byref(cap)):
@@ -402,6 +430,23 @@ def synth_route(shape: dict, seed: int, layer: int, hidden: np.ndarray, bias_fea
                                  _p16(scores), _p16(logits)):
         raise ValueError("synthetic route failed")
     return ids, scores, logits
+
+
+def synth_block_captures(shape: dict, seed: int, layer: int, hidden: np.ndarray, bias_feature=True,
+                         order=ORDER_TREE32, threads: int | None = None) -> dict:
+    """synth_block with every capture of the block ([T, ...] arrays named as
+    CAPTURE_NAMES; weighted_down [T, K, H] in ascending expert id) and "out"."""
+    h = _u16(hidden)
+    T = h.shape[0]
+    arrays = _capture_arrays(shape, (T,))
+    caps = (BlockCaptures * T)(*[_captures_of(arrays, (t,)) for t in range(T)])
+    out = np.empty((T, shape["hidden"]), dtype=np.uint16)
+    s, c = _shape(shape), _config(seed, bias_feature, order, threads or default_threads())
+    if not lib().fwo_synth_block_captured(ctypes.byref(s), ctypes.byref(c), layer, _p16(h), T,
+                                          _p16(out), caps):
+        raise ValueError("synthetic block failed")
+    arrays["out"] = out
+    return arrays
 
 
 def synth_block(shape: dict, seed: int, layer: int, hidden: np.ndarray, bias_feature=True,

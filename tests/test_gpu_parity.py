@@ -171,6 +171,33 @@ def test_block_tiny_installed(tiny_ctx, tokens, order):
         assert first_diff(got["out"][t], ref["out"]) is None, (t, first_diff(got["out"][t], ref["out"]))
 
 
+def assert_captures_equal(got, ref, t, where):
+    """Every verifier capture of token t bit for bit (src/expert.rs:1154-1199,
+    src/decoder_layer.rs:528-586), and the capture identity the reference's
+    verifier ends with: out = add_bf16(routed_mixture, gated_shared)."""
+    for name in hm.VERIFIER_CAPTURES:
+        g = np.asarray(got[name][t]).ravel()
+        r = np.asarray(ref[name]).ravel()
+        assert g.shape == r.shape and first_diff(g, r) is None, (where, t, name, first_diff(g, r))
+    combined = np.array([fo.add_bf16(int(a), int(b)) for a, b in
+                         zip(got["routed_mixture"][t], got["gated_shared"][t])], dtype=np.uint16)
+    assert first_diff(combined, got["out"][t]) is None, (where, t)
+
+
+@pytest.mark.parametrize("tokens,order", [(1, hm.LOGITS_TREE32), (4, hm.LOGITS_TREE32), (3, hm.LOGITS_FOLD)])
+def test_block_tiny_verifier_captures(tiny_ctx, tokens, order):
+    rng = np.random.default_rng(70 + 10 * tokens + order)
+    w = tiny_weights(rng)
+    install(tiny_ctx, 2, w)
+    x = rand_bf16(rng, tokens * TINY["hidden"]).reshape(tokens, -1)
+    got = tiny_ctx.sparse_moe_block(2, x, order, captures="all")
+    for t in range(tokens):
+        ref = fo.sparse_moe_block(TINY, w, x[t], order)
+        assert first_diff(got["out"][t], ref["out"]) is None
+        assert got["shared_gate_sigmoid"][t] == ref["shared_gate_sigmoid"][0]
+        assert_captures_equal(got, ref, t, "tiny")
+
+
 def test_block_tiny_router_ties(tiny_ctx):
     # A zero router: every logit is +0.0, so selection is experts 0..K-1 by the
     # index rule and the scores are uniform.
@@ -349,6 +376,18 @@ def test_block_workload_shape_fold_order(ctx3):
     assert np.array_equal(got["selected_experts"], ids)
     assert first_diff(got["selected_scores"], scores) is None
     assert first_diff(got["out"], out) is None
+
+
+@pytest.mark.parametrize("tokens,order", [(1, hm.LOGITS_TREE32), (2, hm.LOGITS_FOLD), (4, hm.LOGITS_TREE32)])
+def test_block_verifier_captures_workload_shape(ctx3, tokens, order):
+    x = fo.synth_hidden(SEED, tokens, CFG["hidden"], first_token=900 + tokens)
+    got = ctx3.sparse_moe_block(0, x, order, captures="all")
+    ref = fo.synth_block_captures(CFG, SEED, 0, x, order=order)
+    assert first_diff(got["out"], ref["out"]) is None
+    assert np.array_equal(got["selected_experts"], ref["ids"])
+    assert first_diff(got["shared_gate_sigmoid"], ref["shared_gate_sigmoid"].ravel()) is None
+    for t in range(tokens):
+        assert_captures_equal(got, {k: ref[k][t] for k in hm.VERIFIER_CAPTURES}, t, "workload")
 
 
 def test_mixture_resident_workload_shape(ctx3):

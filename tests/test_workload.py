@@ -62,3 +62,38 @@ def test_cpu_baseline_timing_computes_the_same_block():
     ref_n = fo.synth_block(shape, SEED, 3, normed[None])[0]
     _, out = fo.bench_block(shape, SEED, 3, x1, prenorm=True, warmups=0, runs=1, threads=2)
     assert np.array_equal(out, ref_n)
+
+
+def test_block_captures_compose_to_the_block_output():
+    """The oracle's per-token captures are the block's own intermediate vectors:
+    they recombine, by the reference's formulas (src/expert.rs:1138-1153,
+    src/decoder_layer.rs:532-607), into the block output synth_block gives."""
+    shape = dict(hidden=256, intermediate=64, experts=64, top_k=6, shared_intermediate=96)
+    x = fo.synth_hidden(11, 3, shape["hidden"], first_token=5)
+    cap = fo.synth_block_captures(shape, 11, 0, x)
+    out, ids, scores, logits = fo.synth_block(shape, 11, 0, x)
+    assert np.array_equal(cap["out"], out) and np.array_equal(cap["ids"], ids)
+    assert np.array_equal(cap["scores"], scores) and np.array_equal(cap["logits"], logits)
+    for t in range(3):
+        assert np.array_equal(cap["shared_swiglu"][t], fo.swiglu_bf16(cap["shared_gate"][t], cap["shared_up"][t]))
+        assert cap["shared_gate_sigmoid"][t, 0] == fo.sigmoid_bf16(int(cap["shared_gate_logit"][t, 0]))
+        sig = fo.from_bf16(int(cap["shared_gate_sigmoid"][t, 0]))
+        gated = [fo.to_bf16(np.float32(sig) * np.float32(fo.from_bf16(int(v)))) for v in cap["shared_down"][t]]
+        assert list(cap["gated_shared"][t]) == gated
+        mix = fo.to_bf16(0.0)
+        mixed = []
+        for h in range(shape["hidden"]):
+            m = mix
+            for n in range(shape["top_k"]):
+                m = fo.add_bf16(m, int(cap["weighted_down"][t, n, h]))
+            mixed.append(m)
+        assert list(cap["routed_mixture"][t]) == mixed
+        assert list(out[t]) == [fo.add_bf16(a, b) for a, b in zip(mixed, gated)]
+        # weighted rows in ascending expert id, each bf16(down * score) of its expert
+        order = np.argsort(ids[t], kind="stable")
+        for n, r in enumerate(order):
+            e = int(ids[t, r])
+            gu = fo.synth_tensor(11, 0, 2, e * 2 * 64 * 256, 2 * 64 * 256)
+            dn = fo.synth_tensor(11, 0, 3, e * 256 * 64, 256 * 64)
+            ex = fo.expert_bf16(gu, dn, x[t], 256, 64, int(scores[t, r]))
+            assert np.array_equal(cap["weighted_down"][t, n], ex["weighted_down"]), (t, n, e)
