@@ -5,15 +5,20 @@
 // host buffers in, run exact-order kernels and copy out. The resident context
 // keeps every layer's weights in HBM and runs a whole block, or a whole
 // 48-layer decode step, as one persistent launch (fw_decode.h).
+#include <fcntl.h>
 #include <hip/hip_runtime.h>
+#include <unistd.h>
 
 #include <algorithm>
+#include <atomic>
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
 #include <mutex>
 #include <new>
+#include <stdexcept>
 #include <string>
+#include <thread>
 #include <type_traits>
 #include <vector>
 
@@ -22,6 +27,7 @@
 #include "fw_device.h"
 #include "fw_numerics.h"
 #include "fw_prefill.h"
+#include "fw_safetensors.h"
 #include "fw_synth.h"
 
 using namespace fw;
@@ -978,6 +984,131 @@ bool firewing_hip_install_layer(firewing_hip_context* c, size_t layer, const uin
         upload(c->shared_up[layer], shared_up, Is * H * 2, s);
         upload(c->shared_down[layer], shared_down, H * Is * 2, s);
         check(hipStreamSynchronize(s), "hipStreamSynchronize");
+        return true;
+    });
+}
+
+namespace {
+
+// Copies byte ranges of files into device memory through pinned staging
+// buffers: while one buffer's copy to HBM is in flight on the stream, the next
+// is filled by parallel preads (a page-cached or NVMe file is read faster by
+// several threads than by one).
+class FileStreamer {
+   public:
+    static constexpr size_t kChunk = 32u << 20;
+    static constexpr int kBuffers = 3;
+    static constexpr int kReaders = 4;
+
+    explicit FileStreamer(hipStream_t s) : s_(s) {
+        for (int i = 0; i < kBuffers; ++i) {
+            check(hipHostMalloc(&buf_[i], kChunk, hipHostMallocDefault), "hipHostMalloc staging");
+            check(hipEventCreateWithFlags(&done_[i], hipEventDisableTiming), "hipEventCreate");
+        }
+    }
+    ~FileStreamer() {
+        (void)hipStreamSynchronize(s_);
+        for (int i = 0; i < kBuffers; ++i) {
+            if (done_[i]) (void)hipEventDestroy(done_[i]);
+            if (buf_[i]) (void)hipHostFree(buf_[i]);
+        }
+        if (fd_ >= 0) ::close(fd_);
+    }
+    FileStreamer(const FileStreamer&) = delete;
+    FileStreamer& operator=(const FileStreamer&) = delete;
+
+    void copy(const std::string& file, uint64_t offset, uint64_t bytes, void* dst) {
+        open(file);
+        auto* d = static_cast<char*>(dst);
+        while (bytes) {
+            const size_t n = (size_t)std::min<uint64_t>(bytes, kChunk);
+            const int b = next_++ % kBuffers;
+            if (used_[b]) check(hipEventSynchronize(done_[b]), "hipEventSynchronize staging");
+            fill(static_cast<char*>(buf_[b]), n, offset);
+            check(hipMemcpyAsync(d, buf_[b], n, hipMemcpyHostToDevice, s_), "hipMemcpyAsync staging");
+            check(hipEventRecord(done_[b], s_), "hipEventRecord staging");
+            used_[b] = true;
+            d += n;
+            offset += n;
+            bytes -= n;
+        }
+    }
+
+   private:
+    void open(const std::string& file) {
+        if (file == file_) return;
+        if (fd_ >= 0) ::close(fd_);
+        fd_ = ::open(file.c_str(), O_RDONLY | O_CLOEXEC);
+        if (fd_ < 0) throw std::runtime_error(file + ": cannot open");
+        file_ = file;
+    }
+    void fill(char* dst, size_t n, uint64_t offset) {
+        const size_t part = (n + kReaders - 1) / kReaders;
+        std::atomic<bool> short_read{false};
+        auto read_part = [&](size_t lo, size_t hi) {
+            while (lo < hi) {
+                ssize_t got = ::pread(fd_, dst + lo, hi - lo, (off_t)(offset + lo));
+                if (got <= 0) {
+                    short_read = true;
+                    return;
+                }
+                lo += (size_t)got;
+            }
+        };
+        std::vector<std::thread> readers;
+        for (size_t lo = part; lo < n; lo += part) readers.emplace_back(read_part, lo, std::min(n, lo + part));
+        read_part(0, std::min(n, part));
+        for (auto& t : readers) t.join();
+        if (short_read) throw std::runtime_error(file_ + ": short read");
+    }
+
+    hipStream_t s_;
+    void* buf_[kBuffers] = {};
+    hipEvent_t done_[kBuffers] = {};
+    bool used_[kBuffers] = {};
+    int next_ = 0;
+    int fd_ = -1;
+    std::string file_;
+};
+
+}  // namespace
+
+bool firewing_hip_safetensors_layer_plan(const firewing_hip_shape* shape, const char* path, const char* layer_prefix,
+                                         firewing_hip_tensor_span* spans) {
+    return guarded([&] {
+        if (!shape || !path || !layer_prefix || !spans) return fail("safetensors_layer_plan: null pointer");
+        fw::st::Checkpoint ckpt(path);
+        auto plan = fw::st::layer_plan(ckpt, layer_prefix, shape->hidden, shape->intermediate, shape->experts,
+                                       shape->shared_intermediate);
+        std::vector<std::string> files;
+        for (size_t i = 0; i < plan.size(); ++i) {
+            auto it = std::find(files.begin(), files.end(), plan[i].file);
+            if (it == files.end()) it = files.insert(files.end(), plan[i].file);
+            spans[i].offset = plan[i].offset;
+            spans[i].bytes = plan[i].bytes;
+            spans[i].shard = (uint32_t)(it - files.begin());
+        }
+        return true;
+    });
+}
+
+bool firewing_hip_load_layer_safetensors(firewing_hip_context* c, size_t layer, const char* path,
+                                         const char* layer_prefix) {
+    return guarded([&] {
+        if (!c) return fail("load_layer_safetensors: null context");
+        if (!path || !layer_prefix) return fail("load_layer_safetensors: null path or prefix");
+        if (layer >= c->shape.layers) return fail("load_layer_safetensors: layer out of range");
+        const size_t H = c->shape.hidden, E = c->shape.experts;
+        // every tensor is resolved and validated before the first byte moves
+        fw::st::Checkpoint ckpt(path);
+        auto plan = fw::st::layer_plan(ckpt, layer_prefix, H, c->shape.intermediate, E, c->shape.shared_intermediate);
+        uint16_t* dst[7] = {c->router[layer],      c->gate_up[layer],   c->down[layer],
+                            c->shared_gate[layer], c->shared_up[layer], c->shared_down[layer],
+                            c->router[layer] + E * H};
+        Ordered ordered(c, nullptr);
+        FileStreamer streamer(ordered.s);
+        for (size_t i = 0; i < plan.size(); ++i) streamer.copy(plan[i].file, plan[i].offset, plan[i].bytes, dst[i]);
+        check(hipStreamSynchronize(ordered.s), "hipStreamSynchronize");
         return true;
     });
 }

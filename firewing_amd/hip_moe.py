@@ -23,6 +23,7 @@ there is no CPU fallback.
 from __future__ import annotations
 
 import ctypes
+import os
 from pathlib import Path
 
 import numpy as np
@@ -46,6 +47,21 @@ class Shape(ctypes.Structure):
     _fields_ = [("hidden", ctypes.c_size_t), ("intermediate", ctypes.c_size_t),
                 ("experts", ctypes.c_size_t), ("top_k", ctypes.c_size_t),
                 ("shared_intermediate", ctypes.c_size_t), ("layers", ctypes.c_size_t)]
+
+
+class TensorSpan(ctypes.Structure):
+    _fields_ = [("offset", ctypes.c_uint64), ("bytes", ctypes.c_uint64), ("shard", ctypes.c_uint32)]
+
+
+# the seven tensors of one MoE layer, in resident-bank order (tensor ids 1..7)
+LAYER_TENSORS = ("mlp.gate.weight", "mlp.experts.gate_up_proj", "mlp.experts.down_proj",
+                 "mlp.shared_expert.gate_proj.weight", "mlp.shared_expert.up_proj.weight",
+                 "mlp.shared_expert.down_proj.weight", "mlp.shared_expert_gate.weight")
+
+
+def layer_prefix(layer: int) -> str:
+    """The checkpoint's name prefix of decoder layer `layer`."""
+    return f"model.language_model.layers.{layer}"
 
 
 VERIFIER_CAPTURES = ("routed_mixture", "shared_gate", "shared_up", "shared_swiglu", "shared_down",
@@ -82,6 +98,9 @@ _SIGNATURES = {
     "firewing_hip_device_name": (ctypes.c_char_p, [_vp]),
     "firewing_hip_install_layer": (_b, [_vp, _sz, _u16p, _u16p, _u16p, _u16p, _u16p, _u16p, _u16p]),
     "firewing_hip_generate_layers": (_b, [_vp, _sz, _sz, ctypes.c_uint64, _b]),
+    "firewing_hip_safetensors_layer_plan": (_b, [ctypes.POINTER(Shape), ctypes.c_char_p, ctypes.c_char_p,
+                                                 ctypes.POINTER(TensorSpan)]),
+    "firewing_hip_load_layer_safetensors": (_b, [_vp, _sz, ctypes.c_char_p, ctypes.c_char_p]),
     "firewing_hip_read_tensor": (_b, [_vp, _sz, ctypes.c_int, _sz, _sz, _u16p]),
     "firewing_hip_route": (_b, [_vp, _sz, _u16p, _sz, ctypes.c_int, _szp, _u16p, _u16p]),
     "firewing_hip_mixture_bf16": (_b, [_vp, _sz, _u16p, _szp, _u16p, _sz, _u16p]),
@@ -253,6 +272,18 @@ def copy_bytes(dst_ptr: int, src_ptr: int, nbytes: int, stream: int = 0) -> None
 
 # ---- resident context ------------------------------------------------------------------
 
+def safetensors_layer_plan(path, prefix: str, hidden: int, intermediate: int, experts: int,
+                           shared_intermediate: int, top_k: int = 1) -> list[tuple[int, int, int]]:
+    """Host only: (offset, bytes, shard ordinal) of the layer's seven tensors in
+    LAYER_TENSORS order, validated against the shape; raises FirewingError with
+    the reason otherwise."""
+    shape = Shape(hidden, intermediate, experts, top_k, shared_intermediate, 1)
+    spans = (TensorSpan * 7)()
+    _call("firewing_hip_safetensors_layer_plan", ctypes.byref(shape), os.fsencode(str(path)),
+          prefix.encode(), spans)
+    return [(int(sp.offset), int(sp.bytes), int(sp.shard)) for sp in spans]
+
+
 class MoeContext:
     """Resident banks of `layers` sparse-MoE layers in HBM (metal_moe::Runtime)."""
 
@@ -298,6 +329,13 @@ class MoeContext:
 
     def generate_layers(self, first: int, count: int, seed: int, bias_feature: bool = True) -> None:
         _call("firewing_hip_generate_layers", self._h, first, count, seed, bias_feature)
+
+    def load_layer_safetensors(self, layer: int, path, prefix: str | None = None) -> None:
+        """Install resident layer `layer` from a safetensors checkpoint (a
+        .safetensors file or a model.safetensors.index.json); `prefix` names
+        the checkpoint layer (default: layer_prefix(layer))."""
+        pre = layer_prefix(layer) if prefix is None else prefix
+        _call("firewing_hip_load_layer_safetensors", self._h, layer, os.fsencode(str(path)), pre.encode())
 
     def read_tensor(self, layer: int, tensor: int, first: int, count: int) -> np.ndarray:
         out = np.empty(count, dtype=np.uint16)

@@ -152,6 +152,42 @@ bool firewing_hip_install_layer(firewing_hip_context* ctx, size_t layer, const u
                                 const uint16_t* shared_gate, const uint16_t* shared_up,
                                 const uint16_t* shared_down, const uint16_t* shared_expert_gate);
 
+/* Where one of a layer's tensors lies in a safetensors checkpoint. */
+typedef struct firewing_hip_tensor_span {
+    uint64_t offset; /* absolute byte offset of the payload in its file */
+    uint64_t bytes;  /* payload bytes */
+    uint32_t shard;  /* ordinal of its file among the layer's files, in first-use order */
+} firewing_hip_tensor_span;
+
+/* Host only (no GPU needed): resolve and validate the seven tensors of one MoE
+ * layer in a safetensors checkpoint. `path` is a single .safetensors file or a
+ * model.safetensors.index.json (its weight_map names each tensor's shard, a
+ * plain file name in the index's directory: src/checkpoint_catalog.rs:124-127,
+ * 405-443). The tensors, all BF16 of exactly these shapes, are
+ * "<layer_prefix>.mlp.gate.weight" [E, H], ".mlp.experts.gate_up_proj"
+ * [E, 2I, H], ".mlp.experts.down_proj" [E, H, I],
+ * ".mlp.shared_expert.gate_proj.weight" [Is, H], ".mlp.shared_expert.up_proj.weight"
+ * [Is, H], ".mlp.shared_expert.down_proj.weight" [H, Is] and
+ * ".mlp.shared_expert_gate.weight" [1, H] (src/decoder_layer1.rs:189-213,
+ * src/expert_acquisition.rs:371-375;
+ * layer_prefix e.g. "model.language_model.layers.0"). Each shard's header is
+ * checked as src/checkpoint_catalog.rs:146-245 checks it (header length in
+ * (0, 16 MiB], known dtypes, payload sizes exact and inside the file, no
+ * overlaps). spans[7] receive the tensors in that order; false with the
+ * reason in firewing_hip_last_error() otherwise. */
+bool firewing_hip_safetensors_layer_plan(const firewing_hip_shape* shape, const char* path,
+                                         const char* layer_prefix, firewing_hip_tensor_span* spans);
+
+/* Load one layer's resident banks straight from a safetensors checkpoint (the
+ * plan above against the context's shape, then every payload streamed into
+ * HBM through pinned staging buffers, file reads overlapping the copies).
+ * Replaces the reference's per-call slice readers read_expert_slice /
+ * read_tensor_2d (src/expert.rs:362-512) and the mapped catalog's
+ * expert_bf16 view (src/checkpoint_catalog.rs:416-443) with one copy per layer
+ * at install time. Synchronous; nothing is copied if any tensor fails the plan. */
+bool firewing_hip_load_layer_safetensors(firewing_hip_context* ctx, size_t layer, const char* path,
+                                         const char* layer_prefix);
+
 /* Fill layers [first, first+count) on the device with the seeded synthetic
  * weights (firewing_amd/csrc/fw_synth.h); bias_feature writes the Zipf router
  * bias into router column H-1. */
