@@ -25,6 +25,7 @@
 #include "../../include/firewing_hip_moe.h"
 #include "fw_decode.h"
 #include "fw_device.h"
+#include "fw_hyper.h"
 #include "fw_numerics.h"
 #include "fw_prefill.h"
 #include "fw_safetensors.h"
@@ -352,6 +353,16 @@ struct firewing_hip_context {
         PfGroups g{};
         std::vector<void*> owned;
     } pf;
+    // mlp hyper-connection per layer (installed on demand) and its scratch for T <= 4
+    struct Hyper {
+        int streams = 0, lowrank = 0;
+        std::vector<uint16_t*> norm, down, up, inject;  // [S*H], [R][S*H], [S*H][R], [S][S*H]
+        std::vector<void*> owned;
+        uint16_t *normed = nullptr, *mix_down = nullptr, *scaled = nullptr, *silu = nullptr, *mix_up = nullptr;
+        uint16_t *input_mix = nullptr, *products = nullptr, *mixed = nullptr, *inject_out = nullptr;
+        uint16_t *inject_scaled = nullptr, *inject_sigmoid = nullptr, *weights = nullptr;
+        uint16_t *post = nullptr, *layer_out = nullptr, *inj_products = nullptr;
+    } hc;
 };
 
 namespace {
@@ -952,6 +963,8 @@ void firewing_hip_destroy(firewing_hip_context* c) {
     for (void* b : bufs)
         if (b) (void)hipFree(b);
     for (void* b : c->pf.owned)
+        if (b) (void)hipFree(b);
+    for (void* b : c->hc.owned)
         if (b) (void)hipFree(b);
     if (c->last) (void)hipEventDestroy(c->last);
     if (c->stream) (void)hipStreamDestroy(c->stream);
@@ -1641,6 +1654,44 @@ void take_verifier_captures(firewing_hip_context* c, size_t layer, const uint16_
 
 }  // namespace
 
+namespace {
+
+// The captures of the decode block that just ran on stream s for the T inputs
+// at x (device): what the fused kernel keeps (logits, selection, sigmoid), then
+// the verifier captures when any is asked for. Waits for s.
+void collect_block_captures(firewing_hip_context* c, size_t layer, const uint16_t* x, size_t tokens,
+                            firewing_hip_block_captures* cap, hipStream_t s) {
+    const size_t E = c->shape.experts, K = c->shape.top_k;
+    if (cap->router_logits) {
+        // tagged words: two logits in the low half of each
+        const size_t words = tokens * logit_stride((int)E) / 2;
+        std::vector<uint64_t> lw(words);
+        download(lw.data(), c->logits, words * 8, s);
+        check(hipStreamSynchronize(s), "hipStreamSynchronize");
+        for (size_t t = 0; t < tokens; ++t) {
+            for (size_t e = 0; e < E; ++e) {
+                const uint64_t wd = lw[(t * logit_stride((int)E) + e) / 2];
+                cap->router_logits[t * E + e] = (uint16_t)(wd >> (16 * (e & 1)));
+            }
+        }
+    }
+    std::vector<int32_t> ids(tokens * K);
+    std::vector<uint16_t> scores(tokens * K), sig(tokens);
+    download(ids.data(), c->ids, ids.size() * 4, s);
+    download(scores.data(), c->scores, tokens * K * 2, s);
+    download(sig.data(), c->sig, tokens * 2, s);
+    check(hipStreamSynchronize(s), "hipStreamSynchronize");
+    if (cap->selected_experts) {
+        for (size_t i = 0; i < ids.size(); ++i) cap->selected_experts[i] = (size_t)ids[i];
+    }
+    if (cap->selected_scores) std::copy(scores.begin(), scores.end(), cap->selected_scores);
+    if (cap->shared_gate_sigmoid) std::copy(sig.begin(), sig.end(), cap->shared_gate_sigmoid);
+    if (wants_verifier_captures(cap))
+        take_verifier_captures(c, layer, x, tokens, ids.data(), scores.data(), sig.data(), cap, s);
+}
+
+}  // namespace
+
 bool firewing_hip_sparse_moe_block(firewing_hip_context* c, size_t layer,
                                    const uint16_t* hidden, size_t tokens, int order,
                                    uint16_t* out, firewing_hip_block_captures* cap) {
@@ -1651,39 +1702,12 @@ bool firewing_hip_sparse_moe_block(firewing_hip_context* c, size_t layer,
         if (layer >= c->shape.layers) return fail("sparse_moe_block: layer out of range");
         Ordered ordered(c, nullptr);
         hipStream_t s = ordered.s;
-        const size_t H = c->shape.hidden, E = c->shape.experts, K = c->shape.top_k;
+        const size_t H = c->shape.hidden;
         upload(c->xin, hidden, tokens * H * 2, s);
         launch_decode(c, layer, 1, (int)tokens, order, false, false, c->xin, nullptr, s);
         if (!check_device_error(c, s)) return false;
         download(out, c->out, tokens * H * 2, s);
-        if (cap) {
-            if (cap->router_logits) {
-                // tagged words: two logits in the low half of each
-                const size_t words = tokens * logit_stride((int)E) / 2;
-                std::vector<uint64_t> lw(words);
-                download(lw.data(), c->logits, words * 8, s);
-                check(hipStreamSynchronize(s), "hipStreamSynchronize");
-                for (size_t t = 0; t < tokens; ++t) {
-                    for (size_t e = 0; e < E; ++e) {
-                        const uint64_t wd = lw[(t * logit_stride((int)E) + e) / 2];
-                        cap->router_logits[t * E + e] = (uint16_t)(wd >> (16 * (e & 1)));
-                    }
-                }
-            }
-            std::vector<int32_t> ids(tokens * K);
-            std::vector<uint16_t> scores(tokens * K), sig(tokens);
-            download(ids.data(), c->ids, ids.size() * 4, s);
-            download(scores.data(), c->scores, tokens * K * 2, s);
-            download(sig.data(), c->sig, tokens * 2, s);
-            check(hipStreamSynchronize(s), "hipStreamSynchronize");
-            if (cap->selected_experts) {
-                for (size_t i = 0; i < ids.size(); ++i) cap->selected_experts[i] = (size_t)ids[i];
-            }
-            if (cap->selected_scores) std::copy(scores.begin(), scores.end(), cap->selected_scores);
-            if (cap->shared_gate_sigmoid) std::copy(sig.begin(), sig.end(), cap->shared_gate_sigmoid);
-            if (wants_verifier_captures(cap))
-                take_verifier_captures(c, layer, c->xin, tokens, ids.data(), scores.data(), sig.data(), cap, s);
-        }
+        if (cap) collect_block_captures(c, layer, c->xin, tokens, cap, s);
         check(hipStreamSynchronize(s), "hipStreamSynchronize");
         return true;
     });
@@ -1784,3 +1808,335 @@ bool firewing_hip_set_wait_timeout(firewing_hip_context* c, double seconds) {
 }
 
 }  // extern "C"
+
+// ---- hyper-connection and the in-model MoE sublayer ----
+
+namespace {
+
+struct HyperWeights {
+    const uint16_t *norm, *down, *up, *inject;  // inject may be null (final mixer)
+    int S, W, R;
+};
+
+struct HyperBuffers {
+    uint16_t *normed, *mix_down, *scaled, *silu, *mix_up, *input_mix, *products, *mixed;
+    uint16_t *inject, *inject_scaled, *inject_sigmoid, *weights;
+};
+
+bool hyper_shape_ok(size_t S, size_t W, size_t R, std::string* why) {
+    if (S == 0 || S > 64 || W == 0 || R == 0) {
+        *why = "streams must be in [1, 64], width and lowrank nonzero";
+        return false;
+    }
+    if (S * W > 16384 || (S * W) % 2 || R > 16384 || R % 2) {
+        *why = "streams * width and lowrank must be even and <= 16384";
+        return false;
+    }
+    return true;
+}
+
+// run_hyper_connection (src/hyper_connection.rs:412-490) for T tokens at x
+// ([T][S*W], device) into b, on stream s.
+void queue_hyper_connection(const HyperWeights& w, const uint16_t* x, int T, const HyperBuffers& b, hipStream_t s) {
+    const int SW = w.S * w.W;
+    hipLaunchKernelGGL(k_hc_norm, dim3((unsigned)w.S, (unsigned)T), dim3(256), (size_t)w.W * sizeof(float), s, x,
+                       w.norm, w.S, w.W, b.normed);
+    check(hipGetLastError(), "k_hc_norm launch");
+    for (int t = 0; t < T; ++t) {  // one token per launch: 4 * S * W bytes of LDS
+        launch_linear(w.down, b.normed + (size_t)t * SW, w.R, SW, 1, b.mix_down + (size_t)t * w.R, s);
+        if (w.inject) launch_linear(w.inject, b.normed + (size_t)t * SW, w.S, SW, 1, b.inject + (size_t)t * w.S, s);
+    }
+    hipLaunchKernelGGL(k_hc_scale_silu, dim3((unsigned)((T * w.R + 255) / 256)), dim3(256), 0, s, b.mix_down,
+                       T * w.R, w.S, b.scaled, b.silu);
+    check(hipGetLastError(), "k_hc_scale_silu launch");
+    for (int t0 = 0; t0 < T; t0 += 4) {
+        const int n = std::min(4, T - t0);
+        launch_linear(w.up, b.silu + (size_t)t0 * w.R, SW, w.R, n, b.mix_up + (size_t)t0 * SW, s);
+    }
+    hipLaunchKernelGGL(k_hc_mix, dim3((unsigned)((w.W + 255) / 256), (unsigned)T), dim3(256), 0, s, b.mix_up,
+                       b.normed, w.inject ? b.inject : nullptr, w.S, w.W, b.input_mix, b.products, b.mixed,
+                       b.inject_scaled, b.inject_sigmoid, b.weights);
+    check(hipGetLastError(), "k_hc_mix launch");
+}
+
+void queue_inject_residual(const uint16_t* post, const uint16_t* moe, const uint16_t* weights, int T, int S, int W,
+                           uint16_t* products, uint16_t* out, hipStream_t s) {
+    hipLaunchKernelGGL(k_inject_residual, dim3((unsigned)((S * W + 255) / 256), (unsigned)T), dim3(256), 0, s, post,
+                       moe, weights, S, W, products, out);
+    check(hipGetLastError(), "k_inject_residual launch");
+}
+
+}  // namespace
+
+bool firewing_hip_hyper_connection_bf16(const uint16_t* input, size_t tokens, const uint16_t* hc_norm,
+                                        const uint16_t* mix_down_weight, const uint16_t* mix_up_weight,
+                                        const uint16_t* inject_weight, size_t streams, size_t width, size_t lowrank,
+                                        firewing_hip_hyper_outputs* o) {
+    return guarded([&] {
+        if (!input || !hc_norm || !mix_down_weight || !mix_up_weight || !o)
+            return fail("hyper_connection: null pointer");
+        std::string why;
+        if (!hyper_shape_ok(streams, width, lowrank, &why)) return fail("hyper_connection: " + why);
+        if (tokens == 0 || tokens > 65535) return fail("hyper_connection: tokens must be in [1, 65535]");
+        const size_t S = streams, W = width, R = lowrank, SW = S * W, T = tokens;
+        DeviceBuffer dn(SW * 2), dd(R * SW * 2), du(SW * R * 2), di(inject_weight ? S * SW * 2 : 0), dx(T * SW * 2);
+        upload(dn.ptr, hc_norm, SW * 2, nullptr);
+        upload(dd.ptr, mix_down_weight, R * SW * 2, nullptr);
+        upload(du.ptr, mix_up_weight, SW * R * 2, nullptr);
+        if (inject_weight) upload(di.ptr, inject_weight, S * SW * 2, nullptr);
+        upload(dx.ptr, input, T * SW * 2, nullptr);
+        DeviceBuffer b_normed(T * SW * 2), b_md(T * R * 2), b_sc(T * R * 2), b_si(T * R * 2), b_mu(T * SW * 2),
+            b_im(T * SW * 2), b_pr(T * SW * 2), b_mx(T * W * 2), b_in(T * S * 2), b_is(T * S * 2), b_ig(T * S * 2),
+            b_w(T * S * 2);
+        HyperBuffers b{b_normed.as<uint16_t>(), b_md.as<uint16_t>(), b_sc.as<uint16_t>(), b_si.as<uint16_t>(),
+                       b_mu.as<uint16_t>(),     b_im.as<uint16_t>(), b_pr.as<uint16_t>(), b_mx.as<uint16_t>(),
+                       b_in.as<uint16_t>(),     b_is.as<uint16_t>(), b_ig.as<uint16_t>(), b_w.as<uint16_t>()};
+        HyperWeights w{dn.as<uint16_t>(), dd.as<uint16_t>(), du.as<uint16_t>(),
+                       inject_weight ? di.as<uint16_t>() : nullptr, (int)S, (int)W, (int)R};
+        queue_hyper_connection(w, dx.as<uint16_t>(), (int)T, b, nullptr);
+        auto get = [&](uint16_t* dst, const uint16_t* src, size_t n) {
+            if (dst) download(dst, src, n * 2, nullptr);
+        };
+        get(o->hyper_input_normed, b.normed, T * SW);
+        get(o->mix_down, b.mix_down, T * R);
+        get(o->mix_down_scaled, b.scaled, T * R);
+        get(o->mix_down_silu, b.silu, T * R);
+        get(o->mix_up, b.mix_up, T * SW);
+        get(o->input_mix, b.input_mix, T * SW);
+        get(o->products, b.products, T * SW);
+        get(o->mixed, b.mixed, T * W);
+        if (inject_weight) {
+            get(o->inject, b.inject, T * S);
+            get(o->inject_scaled, b.inject_scaled, T * S);
+            get(o->inject_sigmoid, b.inject_sigmoid, T * S);
+            get(o->injection_weights, b.weights, T * S);
+        }
+        check(hipStreamSynchronize(nullptr), "hipStreamSynchronize");
+        return true;
+    });
+}
+
+bool firewing_hip_inject_residual_bf16(const uint16_t* post_attention, const uint16_t* moe_output,
+                                       const uint16_t* injection_weights, size_t tokens, size_t streams,
+                                       size_t width, uint16_t* products, uint16_t* layer_output) {
+    return guarded([&] {
+        if (!post_attention || !moe_output || !injection_weights || !layer_output)
+            return fail("inject_residual: null pointer");
+        if (streams == 0 || streams > 64 || width == 0 || streams * width > (1u << 24) || tokens == 0 ||
+            tokens > 65535)
+            return fail("inject_residual: invalid shape");
+        const size_t T = tokens, S = streams, W = width;
+        DeviceBuffer dp(T * S * W * 2), dm(T * W * 2), dw(T * S * 2), dpr(T * S * W * 2), dout(T * S * W * 2);
+        upload(dp.ptr, post_attention, T * S * W * 2, nullptr);
+        upload(dm.ptr, moe_output, T * W * 2, nullptr);
+        upload(dw.ptr, injection_weights, T * S * 2, nullptr);
+        queue_inject_residual(dp.as<uint16_t>(), dm.as<uint16_t>(), dw.as<uint16_t>(), (int)T, (int)S, (int)W,
+                              dpr.as<uint16_t>(), dout.as<uint16_t>(), nullptr);
+        if (products) download(products, dpr.ptr, T * S * W * 2, nullptr);
+        download(layer_output, dout.ptr, T * S * W * 2, nullptr);
+        check(hipStreamSynchronize(nullptr), "hipStreamSynchronize");
+        return true;
+    });
+}
+
+namespace {
+
+// Reserve the context's hyper-connection storage: the shape on first use
+// (the same for every layer), the scratch for T <= 4, and `layer`'s weights.
+void hyper_reserve(firewing_hip_context* c, size_t layer, size_t streams, size_t lowrank) {
+    auto& h = c->hc;
+    const size_t L = c->shape.layers, H = c->shape.hidden, S = streams, R = lowrank, SW = S * H, T = kMaxTokens;
+    if (h.streams == 0) {
+        std::string why;
+        if (!hyper_shape_ok(S, H, R, &why)) throw std::runtime_error("hyper-connection: " + why);
+        h.norm.assign(L, nullptr);
+        h.down.assign(L, nullptr);
+        h.up.assign(L, nullptr);
+        h.inject.assign(L, nullptr);
+        auto take = [&](size_t n) {
+            uint16_t* p = dalloc<uint16_t>(n);
+            h.owned.push_back(p);
+            return p;
+        };
+        h.normed = take(T * SW);
+        h.mix_down = take(T * R);
+        h.scaled = take(T * R);
+        h.silu = take(T * R);
+        h.mix_up = take(T * SW);
+        h.input_mix = take(T * SW);
+        h.products = take(T * SW);
+        h.mixed = take(T * H);
+        h.inject_out = take(T * S);
+        h.inject_scaled = take(T * S);
+        h.inject_sigmoid = take(T * S);
+        h.weights = take(T * S);
+        h.post = take(T * SW);
+        h.layer_out = take(T * SW);
+        h.inj_products = take(T * SW);
+        h.streams = (int)S;
+        h.lowrank = (int)R;
+    } else if ((size_t)h.streams != S || (size_t)h.lowrank != R) {
+        throw std::runtime_error("hyper-connection: streams and lowrank must be the same for every layer");
+    }
+    if (!h.norm[layer]) {
+        auto take = [&](size_t n) {
+            uint16_t* p = dalloc<uint16_t>(n);
+            h.owned.push_back(p);
+            return p;
+        };
+        h.norm[layer] = take(SW);
+        h.down[layer] = take(R * SW);
+        h.up[layer] = take(SW * R);
+        h.inject[layer] = take(S * SW);
+    }
+}
+
+HyperBuffers hyper_buffers(firewing_hip_context* c) {
+    auto& h = c->hc;
+    return HyperBuffers{h.normed, h.mix_down,  h.scaled,     h.silu,          h.mix_up,         h.input_mix,
+                        h.products, h.mixed, h.inject_out, h.inject_scaled, h.inject_sigmoid, h.weights};
+}
+
+}  // namespace
+
+bool firewing_hip_install_hyper_connection(firewing_hip_context* c, size_t layer, size_t streams, size_t lowrank,
+                                           const uint16_t* hc_norm, const uint16_t* mix_down_weight,
+                                           const uint16_t* mix_up_weight, const uint16_t* inject_weight) {
+    return guarded([&] {
+        if (!c) return fail("install_hyper_connection: null context");
+        if (layer >= c->shape.layers) return fail("install_hyper_connection: layer out of range");
+        if (!hc_norm || !mix_down_weight || !mix_up_weight || !inject_weight)
+            return fail("install_hyper_connection: null tensor");
+        Ordered ordered(c, nullptr);
+        hyper_reserve(c, layer, streams, lowrank);
+        const size_t SW = streams * c->shape.hidden, R = lowrank;
+        auto& h = c->hc;
+        upload(h.norm[layer], hc_norm, SW * 2, ordered.s);
+        upload(h.down[layer], mix_down_weight, R * SW * 2, ordered.s);
+        upload(h.up[layer], mix_up_weight, SW * R * 2, ordered.s);
+        upload(h.inject[layer], inject_weight, streams * SW * 2, ordered.s);
+        check(hipStreamSynchronize(ordered.s), "hipStreamSynchronize");
+        return true;
+    });
+}
+
+bool firewing_hip_load_hyper_connection_safetensors(firewing_hip_context* c, size_t layer, size_t streams,
+                                                    size_t lowrank, const char* path, const char* layer_prefix) {
+    return guarded([&] {
+        if (!c) return fail("load_hyper_connection_safetensors: null context");
+        if (!path || !layer_prefix) return fail("load_hyper_connection_safetensors: null path or prefix");
+        if (layer >= c->shape.layers) return fail("load_hyper_connection_safetensors: layer out of range");
+        std::string why;
+        if (!hyper_shape_ok(streams, c->shape.hidden, lowrank, &why))
+            return fail("load_hyper_connection_safetensors: " + why);
+        const uint64_t S = streams, SW = streams * c->shape.hidden, R = lowrank;
+        fw::st::Checkpoint ckpt(path);
+        const std::string pre = std::string(layer_prefix) + ".mlp_hyper_connection.";
+        const std::pair<const char*, std::vector<uint64_t>> wanted[4] = {
+            {"hc_norm.weight", {SW}},
+            {"input_mix_weight_down.weight", {R, SW}},
+            {"input_mix_weight_up.weight", {SW, R}},
+            {"block_inject_weight.weight", {S, SW}},
+        };
+        std::vector<fw::st::Span> plan;
+        for (const auto& [suffix, shape] : wanted) {
+            fw::st::Span sp;
+            const auto& t = ckpt.bf16(pre + suffix, shape, &sp.file);
+            sp.offset = t.offset;
+            sp.bytes = t.bytes;
+            plan.push_back(sp);
+        }
+        Ordered ordered(c, nullptr);
+        hyper_reserve(c, layer, streams, lowrank);
+        auto& h = c->hc;
+        uint16_t* dst[4] = {h.norm[layer], h.down[layer], h.up[layer], h.inject[layer]};
+        FileStreamer streamer(ordered.s);
+        for (size_t i = 0; i < 4; ++i) streamer.copy(plan[i].file, plan[i].offset, plan[i].bytes, dst[i]);
+        check(hipStreamSynchronize(ordered.s), "hipStreamSynchronize");
+        return true;
+    });
+}
+
+namespace {
+
+bool sublayer_args_ok(firewing_hip_context* c, size_t layer, size_t tokens, int order, std::string* why) {
+    if (!step_args_ok(c, tokens, order, why)) return false;
+    if (layer >= c->shape.layers) {
+        *why = "layer out of range";
+        return false;
+    }
+    if (c->hc.streams == 0 || !c->hc.norm[layer]) {
+        *why = "the layer's hyper-connection is not installed";
+        return false;
+    }
+    return true;
+}
+
+// hyper-connection -> block on its mixed input -> injection into the streams,
+// all on stream s; post [T][S*H] and out [T][S*H] in device memory.
+void queue_sublayer(firewing_hip_context* c, size_t layer, const uint16_t* post, int T, int order, uint16_t* out,
+                    hipStream_t s) {
+    auto& h = c->hc;
+    const int H = (int)c->shape.hidden;
+    HyperWeights w{h.norm[layer], h.down[layer], h.up[layer], h.inject[layer], h.streams, H, h.lowrank};
+    queue_hyper_connection(w, post, T, hyper_buffers(c), s);
+    launch_decode(c, layer, 1, T, order, false, false, h.mixed, nullptr, s);
+    queue_inject_residual(post, c->out, h.weights, T, h.streams, H, h.inj_products, out, s);
+}
+
+}  // namespace
+
+bool firewing_hip_moe_sublayer_dev(firewing_hip_context* c, size_t layer, const uint16_t* post_attention,
+                                   size_t tokens, int order, uint16_t* layer_output, void* stream) {
+    return guarded([&] {
+        std::string why;
+        if (!sublayer_args_ok(c, layer, tokens, order, &why)) return fail("moe_sublayer: " + why);
+        if (!post_attention || !layer_output) return fail("moe_sublayer: null pointer");
+        if (reinterpret_cast<uintptr_t>(post_attention) % 4 || reinterpret_cast<uintptr_t>(layer_output) % 4)
+            return fail("moe_sublayer: post_attention and layer_output must be 4-byte aligned");
+        Ordered ordered(c, stream);
+        queue_sublayer(c, layer, post_attention, (int)tokens, order, layer_output, ordered.s);
+        return true;
+    });
+}
+
+bool firewing_hip_moe_sublayer(firewing_hip_context* c, size_t layer, const uint16_t* post_attention,
+                               size_t tokens, int order, uint16_t* layer_output,
+                               firewing_hip_sublayer_captures* cap) {
+    return guarded([&] {
+        std::string why;
+        if (!sublayer_args_ok(c, layer, tokens, order, &why)) return fail("moe_sublayer: " + why);
+        if (!post_attention || !layer_output) return fail("moe_sublayer: null pointer");
+        Ordered ordered(c, nullptr);
+        hipStream_t s = ordered.s;
+        auto& h = c->hc;
+        const size_t T = tokens, H = c->shape.hidden, S = h.streams, R = h.lowrank, SW = S * H;
+        upload(h.post, post_attention, T * SW * 2, s);
+        queue_sublayer(c, layer, h.post, (int)T, order, h.layer_out, s);
+        if (!check_device_error(c, s)) return false;
+        download(layer_output, h.layer_out, T * SW * 2, s);
+        if (cap) {
+            auto get = [&](uint16_t* dst, const uint16_t* src, size_t n) {
+                if (dst) download(dst, src, n * 2, s);
+            };
+            firewing_hip_hyper_outputs& o = cap->hyper;
+            get(o.hyper_input_normed, h.normed, T * SW);
+            get(o.mix_down, h.mix_down, T * R);
+            get(o.mix_down_scaled, h.scaled, T * R);
+            get(o.mix_down_silu, h.silu, T * R);
+            get(o.mix_up, h.mix_up, T * SW);
+            get(o.input_mix, h.input_mix, T * SW);
+            get(o.products, h.products, T * SW);
+            get(o.mixed, h.mixed, T * H);
+            get(o.inject, h.inject_out, T * S);
+            get(o.inject_scaled, h.inject_scaled, T * S);
+            get(o.inject_sigmoid, h.inject_sigmoid, T * S);
+            get(o.injection_weights, h.weights, T * S);
+            get(cap->moe_output, c->out, T * H);
+            get(cap->mlp_injection_products, h.inj_products, T * SW);
+            collect_block_captures(c, layer, h.mixed, T, &cap->block, s);
+        }
+        check(hipStreamSynchronize(s), "hipStreamSynchronize");
+        return true;
+    });
+}

@@ -64,6 +64,15 @@ def layer_prefix(layer: int) -> str:
     return f"model.language_model.layers.{layer}"
 
 
+HYPER_OUTPUTS = ("hyper_input_normed", "mix_down", "mix_down_scaled", "mix_down_silu", "mix_up",
+                 "input_mix", "products", "mixed", "inject", "inject_scaled", "inject_sigmoid",
+                 "injection_weights")
+
+
+class HyperOutputs(ctypes.Structure):
+    _fields_ = [(k, ctypes.c_void_p) for k in HYPER_OUTPUTS]
+
+
 VERIFIER_CAPTURES = ("routed_mixture", "shared_gate", "shared_up", "shared_swiglu", "shared_down",
                      "shared_gate_logit", "gated_shared", "weighted_down")
 
@@ -75,6 +84,11 @@ class BlockCaptures(ctypes.Structure):
                 ("shared_up", ctypes.c_void_p), ("shared_swiglu", ctypes.c_void_p),
                 ("shared_down", ctypes.c_void_p), ("shared_gate_logit", ctypes.c_void_p),
                 ("gated_shared", ctypes.c_void_p), ("weighted_down", ctypes.c_void_p)]
+
+
+class SublayerCaptures(ctypes.Structure):
+    _fields_ = [("hyper", HyperOutputs), ("block", BlockCaptures), ("moe_output", ctypes.c_void_p),
+                ("mlp_injection_products", ctypes.c_void_p)]
 
 
 _u16p = ctypes.POINTER(ctypes.c_uint16)
@@ -98,6 +112,15 @@ _SIGNATURES = {
     "firewing_hip_device_name": (ctypes.c_char_p, [_vp]),
     "firewing_hip_install_layer": (_b, [_vp, _sz, _u16p, _u16p, _u16p, _u16p, _u16p, _u16p, _u16p]),
     "firewing_hip_generate_layers": (_b, [_vp, _sz, _sz, ctypes.c_uint64, _b]),
+    "firewing_hip_hyper_connection_bf16": (_b, [_u16p, _sz, _u16p, _u16p, _u16p, _vp, _sz, _sz, _sz,
+                                                ctypes.POINTER(HyperOutputs)]),
+    "firewing_hip_inject_residual_bf16": (_b, [_u16p, _u16p, _u16p, _sz, _sz, _sz, _vp, _u16p]),
+    "firewing_hip_install_hyper_connection": (_b, [_vp, _sz, _sz, _sz, _u16p, _u16p, _u16p, _u16p]),
+    "firewing_hip_load_hyper_connection_safetensors": (_b, [_vp, _sz, _sz, _sz, ctypes.c_char_p,
+                                                            ctypes.c_char_p]),
+    "firewing_hip_moe_sublayer": (_b, [_vp, _sz, _u16p, _sz, ctypes.c_int, _u16p,
+                                       ctypes.POINTER(SublayerCaptures)]),
+    "firewing_hip_moe_sublayer_dev": (_b, [_vp, _sz, _vp, _sz, ctypes.c_int, _vp, _vp]),
     "firewing_hip_safetensors_layer_plan": (_b, [ctypes.POINTER(Shape), ctypes.c_char_p, ctypes.c_char_p,
                                                  ctypes.POINTER(TensorSpan)]),
     "firewing_hip_load_layer_safetensors": (_b, [_vp, _sz, ctypes.c_char_p, ctypes.c_char_p]),
@@ -272,6 +295,50 @@ def copy_bytes(dst_ptr: int, src_ptr: int, nbytes: int, stream: int = 0) -> None
 
 # ---- resident context ------------------------------------------------------------------
 
+def _hyper_arrays(T: int, S: int, W: int, R: int, inject: bool) -> dict:
+    dims = {"hyper_input_normed": S * W, "mix_down": R, "mix_down_scaled": R, "mix_down_silu": R,
+            "mix_up": S * W, "input_mix": S * W, "products": S * W, "mixed": W, "inject": S,
+            "inject_scaled": S, "inject_sigmoid": S, "injection_weights": S}
+    return {k: np.empty((T, dims[k]), dtype=np.uint16) for k in HYPER_OUTPUTS
+            if inject or k not in ("inject", "inject_scaled", "inject_sigmoid", "injection_weights")}
+
+
+def _hyper_struct(arrays: dict) -> HyperOutputs:
+    o = HyperOutputs()
+    for k, a in arrays.items():
+        setattr(o, k, a.ctypes.data)
+    return o
+
+
+def hyper_connection(hidden, hc_norm, mix_down_weight, mix_up_weight, inject_weight, streams: int,
+                     width: int, lowrank: int) -> dict:
+    """run_hyper_connection (src/hyper_connection.rs:412-490) for hidden
+    [T, S*W] on the GPU; every output [T, ...] by name (inject_weight None:
+    the final mixer, without the injection outputs)."""
+    x = _u16(hidden).reshape(-1, streams * width)
+    T = x.shape[0]
+    out = _hyper_arrays(T, streams, width, lowrank, inject_weight is not None)
+    o = _hyper_struct(out)
+    inj = _u16(inject_weight) if inject_weight is not None else None
+    _call("firewing_hip_hyper_connection_bf16", _p16(x), T, _p16(_u16(hc_norm)), _p16(_u16(mix_down_weight)),
+          _p16(_u16(mix_up_weight)), inj.ctypes.data if inj is not None else None, streams, width, lowrank,
+          ctypes.byref(o))
+    return out
+
+
+def inject_residual(post_attention, moe_output, injection_weights, streams: int, width: int):
+    """(products, layer_output), each [T, S*W], of src/decoder_layer.rs:587-607."""
+    post = _u16(post_attention).reshape(-1, streams * width)
+    T = post.shape[0]
+    moe = _u16(moe_output).reshape(T, width)
+    w = _u16(injection_weights).reshape(T, streams)
+    products = np.empty_like(post)
+    out = np.empty_like(post)
+    _call("firewing_hip_inject_residual_bf16", _p16(post), _p16(moe), _p16(w), T, streams, width,
+          products.ctypes.data, _p16(out))
+    return products, out
+
+
 def safetensors_layer_plan(path, prefix: str, hidden: int, intermediate: int, experts: int,
                            shared_intermediate: int, top_k: int = 1) -> list[tuple[int, int, int]]:
     """Host only: (offset, bytes, shard ordinal) of the layer's seven tensors in
@@ -292,6 +359,7 @@ class MoeContext:
         self.shape = Shape(hidden, intermediate, experts, top_k, shared_intermediate, layers)
         self.H, self.I, self.E, self.K = hidden, intermediate, experts, top_k
         self.Is, self.L = shared_intermediate, layers
+        self.hc_streams, self.hc_lowrank = 0, 0
         handle = ctypes.c_void_p()
         _call("firewing_hip_create", ctypes.byref(self.shape), ctypes.byref(handle))
         self._h = handle
@@ -329,6 +397,64 @@ class MoeContext:
 
     def generate_layers(self, first: int, count: int, seed: int, bias_feature: bool = True) -> None:
         _call("firewing_hip_generate_layers", self._h, first, count, seed, bias_feature)
+
+    def install_hyper_connection(self, layer: int, streams: int, lowrank: int, hc_norm, mix_down_weight,
+                                 mix_up_weight, inject_weight) -> None:
+        arrs = [_u16(a) for a in (hc_norm, mix_down_weight, mix_up_weight, inject_weight)]
+        SW = streams * self.H
+        if [a.size for a in arrs] != [SW, lowrank * SW, SW * lowrank, streams * SW]:
+            raise FirewingError("install_hyper_connection: tensor sizes do not match the shape")
+        _call("firewing_hip_install_hyper_connection", self._h, layer, streams, lowrank, *[_p16(a) for a in arrs])
+        self.hc_streams, self.hc_lowrank = streams, lowrank
+
+    def load_hyper_connection_safetensors(self, layer: int, streams: int, lowrank: int, path,
+                                          prefix: str | None = None) -> None:
+        pre = layer_prefix(layer) if prefix is None else prefix
+        _call("firewing_hip_load_hyper_connection_safetensors", self._h, layer, streams, lowrank,
+              os.fsencode(str(path)), pre.encode())
+        self.hc_streams, self.hc_lowrank = streams, lowrank
+
+    def moe_sublayer(self, layer: int, post_attention, order: int = LOGITS_TREE32, captures: bool = False) -> dict:
+        """The in-model MoE sublayer (src/decoder_layer.rs:451-607) on the S
+        residual streams post_attention [T, S*H], T <= 4: {"layer_output"}, and
+        with captures every hyper-connection output, the block's captures on
+        its mixed input ("block": verifier captures included), "moe_output"
+        and "mlp_injection_products"."""
+        S, R = self.hc_streams, self.hc_lowrank
+        post = _u16(post_attention).reshape(-1, S * self.H)
+        T = post.shape[0]
+        out = np.empty_like(post)
+        res = {"layer_output": out}
+        cap = None
+        if captures:
+            hyper = _hyper_arrays(T, S, self.H, R, True)
+            block = {"router_logits": np.empty((T, self.E), dtype=np.uint16),
+                     "selected_experts": np.empty((T, self.K), dtype=np.uint64),
+                     "selected_scores": np.empty((T, self.K), dtype=np.uint16),
+                     "shared_gate_sigmoid": np.empty(T, dtype=np.uint16)}
+            dims = {"routed_mixture": (self.H,), "shared_gate": (self.Is,), "shared_up": (self.Is,),
+                    "shared_swiglu": (self.Is,), "shared_down": (self.H,), "shared_gate_logit": (),
+                    "gated_shared": (self.H,), "weighted_down": (self.K, self.H)}
+            block.update({k: np.empty((T,) + dims[k], dtype=np.uint16) for k in VERIFIER_CAPTURES})
+            moe = np.empty((T, self.H), dtype=np.uint16)
+            products = np.empty_like(post)
+            cap = SublayerCaptures()
+            cap.hyper = _hyper_struct(hyper)
+            for k, a in block.items():
+                setattr(cap.block, k, a.ctypes.data)
+            cap.moe_output = moe.ctypes.data
+            cap.mlp_injection_products = products.ctypes.data
+            res.update(hyper=hyper, block=block, moe_output=moe, mlp_injection_products=products)
+        _call("firewing_hip_moe_sublayer", self._h, layer, _p16(post), T, order, _p16(out),
+              ctypes.byref(cap) if cap is not None else None)
+        if captures:
+            res["block"]["selected_experts"] = res["block"]["selected_experts"].astype(np.int64)
+        return res
+
+    def moe_sublayer_dev(self, layer: int, post_attention, tokens: int, layer_output,
+                         order: int = LOGITS_TREE32, stream=None) -> None:
+        _call("firewing_hip_moe_sublayer_dev", self._h, layer, _addr(post_attention), tokens, order,
+              _addr(layer_output), _addr(stream))
 
     def load_layer_safetensors(self, layer: int, path, prefix: str | None = None) -> None:
         """Install resident layer `layer` from a safetensors checkpoint (a

@@ -288,6 +288,85 @@ bool firewing_hip_synchronize(firewing_hip_context* ctx);
  * command-buffer completion, src/metal_moe.rs:351-358). */
 bool firewing_hip_set_wait_timeout(firewing_hip_context* ctx, double seconds);
 
+/* ---- hyper-connection around the block (src/hyper_connection.rs) ------- */
+
+/* Every output of run_hyper_connection (src/hyper_connection.rs:333-346,
+ * 412-490) for T tokens of S streams of width W with low rank R; each field
+ * may be NULL. */
+typedef struct firewing_hip_hyper_outputs {
+    uint16_t* hyper_input_normed; /* [T, S*W] grouped_rms(input, hc_norm) */
+    uint16_t* mix_down;           /* [T, R] */
+    uint16_t* mix_down_scaled;    /* [T, R] bf16(mix_down / S) */
+    uint16_t* mix_down_silu;      /* [T, R] */
+    uint16_t* mix_up;             /* [T, S*W] */
+    uint16_t* input_mix;          /* [T, S*W] sigmoid(mix_up) */
+    uint16_t* products;           /* [T, S*W] bf16(input_mix * normed) */
+    uint16_t* mixed;              /* [T, W] four-stream mean: the block's input */
+    uint16_t* inject;             /* [T, S] */
+    uint16_t* inject_scaled;      /* [T, S] bf16(inject / S) */
+    uint16_t* inject_sigmoid;     /* [T, S] */
+    uint16_t* injection_weights;  /* [T, S] bf16(2 * inject_sigmoid) */
+} firewing_hip_hyper_outputs;
+
+/* run_hyper_connection (src/hyper_connection.rs:412-490) for T tokens:
+ * input [T, S*W], hc_norm [S*W], mix_down_weight [R, S*W], mix_up_weight
+ * [S*W, R], inject_weight [S, S*W] (NULL: run_final_mixer,
+ * src/hyper_connection.rs:359-410, without the injection outputs). The
+ * grouped RMS norm sums squares in PyTorch's aarch64 cascade
+ * (src/hyper_connection.rs:211-303); the projections are linear_bf16.
+ * S <= 64, S*W and R even and <= 16384. Host pointers, synchronous. */
+bool firewing_hip_hyper_connection_bf16(const uint16_t* input, size_t tokens, const uint16_t* hc_norm,
+                                        const uint16_t* mix_down_weight, const uint16_t* mix_up_weight,
+                                        const uint16_t* inject_weight, size_t streams, size_t width,
+                                        size_t lowrank, firewing_hip_hyper_outputs* outputs);
+
+/* The block output injected into the residual streams
+ * (src/decoder_layer.rs:587-607): products[t][s][h] = bf16(moe[t][h] *
+ * weights[t][s]) (products may be NULL), layer_output[t][s][h] =
+ * add_bf16(post_attention[t][s][h], products[t][s][h]). */
+bool firewing_hip_inject_residual_bf16(const uint16_t* post_attention, const uint16_t* moe_output,
+                                       const uint16_t* injection_weights, size_t tokens, size_t streams,
+                                       size_t width, uint16_t* products, uint16_t* layer_output);
+
+/* Install one layer's mlp hyper-connection on the context (width = H; the
+ * same streams and lowrank for every layer): hc_norm [S*H], mix_down [R, S*H],
+ * mix_up [S*H, R], inject [S, S*H] (the reference's
+ * mlp_hyper_connection.{hc_norm, input_mix_weight_down, input_mix_weight_up,
+ * block_inject_weight}, src/decoder_layer.rs:191-216). */
+bool firewing_hip_install_hyper_connection(firewing_hip_context* ctx, size_t layer, size_t streams,
+                                           size_t lowrank, const uint16_t* hc_norm,
+                                           const uint16_t* mix_down_weight, const uint16_t* mix_up_weight,
+                                           const uint16_t* inject_weight);
+
+/* The same from a safetensors checkpoint ("<layer_prefix>.mlp_hyper_connection.
+ * {hc_norm, input_mix_weight_down, input_mix_weight_up, block_inject_weight}.weight",
+ * BF16, src/decoder_layer1.rs:168-185), validated as
+ * firewing_hip_safetensors_layer_plan validates. */
+bool firewing_hip_load_hyper_connection_safetensors(firewing_hip_context* ctx, size_t layer, size_t streams,
+                                                    size_t lowrank, const char* path,
+                                                    const char* layer_prefix);
+
+/* Captures of the in-model MoE sublayer (src/decoder_layer.rs:451-607). */
+typedef struct firewing_hip_sublayer_captures {
+    firewing_hip_hyper_outputs hyper;   /* mixed = mlp_input, injection_weights = mlp_injection_weights */
+    firewing_hip_block_captures block;  /* of the block on mlp_input */
+    uint16_t* moe_output;               /* [T, H] */
+    uint16_t* mlp_injection_products;   /* [T, S*H] */
+} firewing_hip_sublayer_captures;
+
+/* The in-model MoE sublayer for T <= 4 tokens (src/decoder_layer.rs:451-607):
+ * the layer's mlp hyper-connection on the S residual streams post_attention
+ * [T, S*H], the sparse-MoE block on its mixed input (logit order `order`),
+ * and the block output injected into the streams: layer_output [T, S*H].
+ * Host pointers, synchronous; captures may be NULL. */
+bool firewing_hip_moe_sublayer(firewing_hip_context* ctx, size_t layer, const uint16_t* post_attention,
+                               size_t tokens, int order, uint16_t* layer_output,
+                               firewing_hip_sublayer_captures* captures);
+
+/* Device-pointer variant (4-byte aligned), queued on `stream`. */
+bool firewing_hip_moe_sublayer_dev(firewing_hip_context* ctx, size_t layer, const uint16_t* post_attention,
+                                   size_t tokens, int order, uint16_t* layer_output, void* stream);
+
 /* Seeded synthetic hidden vectors of the benchmark workload (host memory):
  * bf16(N(0,1)) RMS-normalised, x[H-1] = 1.0 when bias_feature (the constant
  * feature that carries the Zipf router bias). No counterpart in the reference,

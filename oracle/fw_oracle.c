@@ -168,6 +168,180 @@ void fwo_build_silu_lut(uint16_t* lut) {
     }
 }
 
+/* src/hyper_connection.rs:211-283 pytorch_inner_square_sum: the sum of
+ * squares in PyTorch's aarch64 contiguous f32 reduction order. The vector
+ * part (n / 4 vectors of 4 lanes, in groups of 4 vectors: `cascade` groups)
+ * runs 16 independent (register, lane) accumulators; group g feeds register r
+ * lane l with element 16g + 4r + l. Each accumulator's terms are summed in a
+ * cascade of LEVELS = 4 levels: level 0 sums `step` = 2^power consecutive
+ * groups, then is added into level 1 and cleared; level 1 is added into level 2
+ * only after `step` level-0 runs (index a multiple of step^2), and so on
+ * (power = max(4, ceil(log2(cascade)) / 4)). Groups past the last full run go
+ * straight into level 0; the levels are then folded into level 0 in order,
+ * vectors past the groups go into register 0, registers 1..3 are folded into
+ * register 0, and the result is the square sum of the scalar tail (n % 4
+ * elements, from 0) plus lanes 0..3 in order. Every multiply and add is a
+ * separately rounded f32 operation. */
+float fwo_inner_square_sum(const float* v, size_t n) {
+    enum { LANES = 4, REGS = 4, LEVELS = 4 };
+    const size_t vectors = n / LANES;
+    const size_t cascade = vectors / REGS;
+    size_t ceil_log2 = 0;
+    if (cascade > 1) {
+        size_t x = cascade - 1;
+        while (x) {
+            ++ceil_log2;
+            x >>= 1;
+        }
+    }
+    const size_t power = ceil_log2 / LEVELS > 4 ? ceil_log2 / LEVELS : 4;
+    const size_t step = (size_t)1 << power;
+    const size_t mask = step - 1;
+    float acc[LEVELS][REGS][LANES];
+    memset(acc, 0, sizeof acc);
+    size_t g = 0;
+    while (g + step <= cascade) {
+        for (size_t k = 0; k < step; ++k, ++g) {
+            for (size_t r = 0; r < REGS; ++r) {
+                for (size_t l = 0; l < LANES; ++l) {
+                    float x = v[(g * REGS + r) * LANES + l];
+                    float sq = x * x;
+                    acc[0][r][l] = acc[0][r][l] + sq;
+                }
+            }
+        }
+        for (size_t lv = 1; lv < LEVELS; ++lv) {
+            for (size_t r = 0; r < REGS; ++r) {
+                for (size_t l = 0; l < LANES; ++l) {
+                    acc[lv][r][l] = acc[lv][r][l] + acc[lv - 1][r][l];
+                    acc[lv - 1][r][l] = 0.0f;
+                }
+            }
+            if (g & (mask << (lv * power))) break;
+        }
+    }
+    for (; g < cascade; ++g) {
+        for (size_t r = 0; r < REGS; ++r) {
+            for (size_t l = 0; l < LANES; ++l) {
+                float x = v[(g * REGS + r) * LANES + l];
+                float sq = x * x;
+                acc[0][r][l] = acc[0][r][l] + sq;
+            }
+        }
+    }
+    for (size_t lv = 1; lv < LEVELS; ++lv)
+        for (size_t r = 0; r < REGS; ++r)
+            for (size_t l = 0; l < LANES; ++l) acc[0][r][l] = acc[0][r][l] + acc[lv][r][l];
+    for (size_t vec = cascade * REGS; vec < vectors; ++vec) {
+        for (size_t l = 0; l < LANES; ++l) {
+            float x = v[vec * LANES + l];
+            float sq = x * x;
+            acc[0][0][l] = acc[0][0][l] + sq;
+        }
+    }
+    for (size_t r = 1; r < REGS; ++r)
+        for (size_t l = 0; l < LANES; ++l) acc[0][0][l] = acc[0][0][l] + acc[0][r][l];
+    float result = 0.0f;
+    for (size_t i = vectors * LANES; i < n; ++i) {
+        float sq = v[i] * v[i];
+        result = result + sq;
+    }
+    for (size_t l = 0; l < LANES; ++l) result = result + acc[0][0][l];
+    return result;
+}
+
+/* src/hyper_connection.rs:285-303 grouped_rms: each of `streams` groups of
+ * `width` values normalised on its own, out = bf16((v * inv) * (1 + w)) with
+ * inv = 1 / sqrt(square_sum / width + eps), each step rounded to f32. */
+void fwo_grouped_rms(const uint16_t* input, const uint16_t* weight, size_t streams, size_t width,
+                     float epsilon, uint16_t* out) {
+    float* f = (float*)malloc(width * sizeof(float));
+    for (size_t s = 0; s < streams; ++s) {
+        const uint16_t* in = input + s * width;
+        for (size_t i = 0; i < width; ++i) f[i] = fwo_from_bf16(in[i]);
+        float mean = fwo_inner_square_sum(f, width) / (float)width;
+        float root = sqrtf(mean + epsilon);
+        float inverse = 1.0f / root;
+        for (size_t i = 0; i < width; ++i) {
+            float scaled = f[i] * inverse;
+            float gain = 1.0f + fwo_from_bf16(weight[s * width + i]);
+            out[s * width + i] = fwo_to_bf16(scaled * gain);
+        }
+    }
+    free(f);
+}
+
+/* src/hyper_connection.rs:305-307 four_stream_mean: a left fold from 0 over
+ * the streams, then divided by their count. */
+static float stream_mean(const float* values, size_t streams) {
+    float sum = 0.0f;
+    for (size_t s = 0; s < streams; ++s) sum = sum + values[s];
+    return sum / (float)streams;
+}
+
+float fwo_stream_mean(const float* values, size_t streams) { return stream_mean(values, streams); }
+
+/* src/hyper_connection.rs:309-317 silu_bf16 (the same formula as the expert's
+ * SiLU, src/expert.rs:565-569). */
+static uint16_t silu_of(uint16_t bits) {
+    float g = fwo_from_bf16(bits);
+    float denominator = 1.0f + expf(-g);
+    return fwo_to_bf16(g / denominator);
+}
+
+/* src/hyper_connection.rs:412-490 run_hyper_connection for one token: the
+ * hyper-connection of `streams` streams of `width` (input [S*W]) with weights
+ * hc_norm [S*W], mix_down [R, S*W], mix_up [S*W, R], inject [S, S*W]
+ * (R = lowrank). inject may be NULL (src/hyper_connection.rs:359-410
+ * run_final_mixer: the same without the injection outputs). */
+int fwo_hyper_connection(const uint16_t* input, const uint16_t* hc_norm, const uint16_t* mix_down_w,
+                         const uint16_t* mix_up_w, const uint16_t* inject_w, size_t streams, size_t width,
+                         size_t lowrank, fwo_hyper_outputs* o) {
+    const size_t SW = streams * width;
+    if (streams == 0 || width == 0 || lowrank == 0 || streams > 64) return 0;
+    fwo_grouped_rms(input, hc_norm, streams, width, 1.0e-6f, o->hyper_input_normed);
+    fwo_linear_bf16(mix_down_w, o->hyper_input_normed, lowrank, SW, o->mix_down);
+    for (size_t i = 0; i < lowrank; ++i) {
+        o->mix_down_scaled[i] = fwo_to_bf16(fwo_from_bf16(o->mix_down[i]) / (float)streams);
+        o->mix_down_silu[i] = silu_of(o->mix_down_scaled[i]);
+    }
+    fwo_linear_bf16(mix_up_w, o->mix_down_silu, SW, lowrank, o->mix_up);
+    for (size_t i = 0; i < SW; ++i) {
+        o->input_mix[i] = fwo_sigmoid_bf16(o->mix_up[i]);
+        o->products[i] = fwo_to_bf16(fwo_from_bf16(o->input_mix[i]) * fwo_from_bf16(o->hyper_input_normed[i]));
+    }
+    float column[64];
+    for (size_t c = 0; c < width; ++c) {
+        for (size_t s = 0; s < streams; ++s) column[s] = fwo_from_bf16(o->products[s * width + c]);
+        o->mixed[c] = fwo_to_bf16(stream_mean(column, streams));
+    }
+    if (inject_w != NULL) {
+        fwo_linear_bf16(inject_w, o->hyper_input_normed, streams, SW, o->inject);
+        for (size_t s = 0; s < streams; ++s) {
+            o->inject_scaled[s] = fwo_to_bf16(fwo_from_bf16(o->inject[s]) / (float)streams);
+            o->inject_sigmoid[s] = fwo_sigmoid_bf16(o->inject_scaled[s]);
+            o->injection_weights[s] = fwo_to_bf16(2.0f * fwo_from_bf16(o->inject_sigmoid[s]));
+        }
+    }
+    return 1;
+}
+
+/* src/decoder_layer.rs:587-607: the block output injected into every stream,
+ * products[s][h] = bf16(moe[h] * weight[s]), and added to the residual
+ * streams, out[s][h] = add_bf16(post_attention[s][h], products[s][h]). */
+void fwo_inject_residual(const uint16_t* post_attention, const uint16_t* moe_output,
+                         const uint16_t* injection_weights, size_t streams, size_t width, uint16_t* products,
+                         uint16_t* layer_output) {
+    for (size_t s = 0; s < streams; ++s) {
+        float w = fwo_from_bf16(injection_weights[s]);
+        for (size_t h = 0; h < width; ++h) {
+            uint16_t p = fwo_to_bf16(fwo_from_bf16(moe_output[h]) * w);
+            if (products) products[s * width + h] = p;
+            layer_output[s * width + h] = fwo_add_bf16(post_attention[s * width + h], p);
+        }
+    }
+}
+
 /* src/expert.rs:341-360 make_hidden (identical in src/router.rs:142-161):
  * ((i*m + a) rem_euclid M - c) / d on every sparse_stride-th index, else 0. */
 int fwo_make_hidden(size_t size, int64_t multiplier, int64_t add, int64_t modulus,

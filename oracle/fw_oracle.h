@@ -44,6 +44,32 @@ uint16_t fwo_sigmoid_bf16(uint16_t value);
 uint16_t fwo_add_bf16(uint16_t left, uint16_t right);
 void fwo_build_silu_lut(uint16_t* lut);
 void fwo_rms_norm_bf16(const uint16_t* r, size_t n, int bias_feature, uint16_t* h);
+/* Hyper-connection (src/hyper_connection.rs) and the block's injection into
+ * the residual streams (src/decoder_layer.rs:587-607). */
+float fwo_inner_square_sum(const float* values, size_t n);
+void fwo_grouped_rms(const uint16_t* input, const uint16_t* weight, size_t streams, size_t width,
+                     float epsilon, uint16_t* out);
+float fwo_stream_mean(const float* values, size_t streams);
+typedef struct {
+    uint16_t* hyper_input_normed; /* [S*W] */
+    uint16_t* mix_down;           /* [R] */
+    uint16_t* mix_down_scaled;    /* [R] */
+    uint16_t* mix_down_silu;      /* [R] */
+    uint16_t* mix_up;             /* [S*W] */
+    uint16_t* input_mix;          /* [S*W] */
+    uint16_t* products;           /* [S*W] */
+    uint16_t* mixed;              /* [W] */
+    uint16_t* inject;             /* [S] */
+    uint16_t* inject_scaled;      /* [S] */
+    uint16_t* inject_sigmoid;     /* [S] */
+    uint16_t* injection_weights;  /* [S] */
+} fwo_hyper_outputs;
+int fwo_hyper_connection(const uint16_t* input, const uint16_t* hc_norm, const uint16_t* mix_down_w,
+                         const uint16_t* mix_up_w, const uint16_t* inject_w, size_t streams, size_t width,
+                         size_t lowrank, fwo_hyper_outputs* outputs);
+void fwo_inject_residual(const uint16_t* post_attention, const uint16_t* moe_output,
+                         const uint16_t* injection_weights, size_t streams, size_t width, uint16_t* products,
+                         uint16_t* layer_output);
 int fwo_make_hidden(size_t size, int64_t multiplier, int64_t add, int64_t modulus,
                     int64_t center, int64_t divisor, size_t sparse_stride, uint16_t* out);
 

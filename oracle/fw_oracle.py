@@ -38,6 +38,15 @@ class Shape(ctypes.Structure):
     ]
 
 
+HYPER_OUTPUTS = ("hyper_input_normed", "mix_down", "mix_down_scaled", "mix_down_silu", "mix_up",
+                 "input_mix", "products", "mixed", "inject", "inject_scaled", "inject_sigmoid",
+                 "injection_weights")
+
+
+class HyperOutputs(ctypes.Structure):
+    _fields_ = [(name, ctypes.POINTER(ctypes.c_uint16)) for name in HYPER_OUTPUTS]
+
+
 class Layer(ctypes.Structure):
     _fields_ = [
         ("router", _u16p),
@@ -112,6 +121,15 @@ def lib() -> ctypes.CDLL:
         L.fwo_add_bf16.argtypes = [ctypes.c_uint16, ctypes.c_uint16]
         L.fwo_build_silu_lut.argtypes = [_u16p]
         L.fwo_rms_norm_bf16.argtypes = [_u16p, _size, ctypes.c_int, _u16p]
+        L.fwo_inner_square_sum.restype = ctypes.c_float
+        L.fwo_inner_square_sum.argtypes = [_f32p, _size]
+        L.fwo_grouped_rms.argtypes = [_u16p, _u16p, _size, _size, ctypes.c_float, _u16p]
+        L.fwo_stream_mean.restype = ctypes.c_float
+        L.fwo_stream_mean.argtypes = [_f32p, _size]
+        L.fwo_hyper_connection.restype = ctypes.c_int
+        L.fwo_hyper_connection.argtypes = [_u16p, _u16p, _u16p, _u16p, _u16p, _size, _size, _size,
+                                           ctypes.POINTER(HyperOutputs)]
+        L.fwo_inject_residual.argtypes = [_u16p, _u16p, _u16p, _size, _size, _u16p, _u16p]
         L.fwo_make_hidden.restype = ctypes.c_int
         L.fwo_make_hidden.argtypes = [_size] + [ctypes.c_int64] * 5 + [_size, _u16p]
         L.fwo_topk_total_order.restype = ctypes.c_int
@@ -256,6 +274,50 @@ def rms_norm_bf16(r, bias_feature: bool = False) -> np.ndarray:
     out = np.empty(a.size, dtype=np.uint16)
     lib().fwo_rms_norm_bf16(_p16(a), a.size, int(bias_feature), _p16(out))
     return out
+
+
+def inner_square_sum(values) -> float:
+    v = np.ascontiguousarray(values, dtype=np.float32)
+    return float(lib().fwo_inner_square_sum(_pf(v), v.size))
+
+
+def grouped_rms(values, weight, streams: int, width: int, epsilon: float = 1e-6) -> np.ndarray:
+    x, w = _u16(values), _u16(weight)
+    out = np.empty(streams * width, dtype=np.uint16)
+    lib().fwo_grouped_rms(_p16(x), _p16(w), streams, width, epsilon, _p16(out))
+    return out
+
+
+def stream_mean(values) -> float:
+    v = np.ascontiguousarray(values, dtype=np.float32)
+    return float(lib().fwo_stream_mean(_pf(v), v.size))
+
+
+def hyper_connection(hidden, hc_norm, mix_down_w, mix_up_w, inject_w, streams: int, width: int,
+                     lowrank: int) -> dict:
+    """One token's hyper-connection: every output of
+    src/hyper_connection.rs:412-490 (inject_w None: run_final_mixer)."""
+    sizes = {"hyper_input_normed": streams * width, "mix_down": lowrank, "mix_down_scaled": lowrank,
+             "mix_down_silu": lowrank, "mix_up": streams * width, "input_mix": streams * width,
+             "products": streams * width, "mixed": width, "inject": streams, "inject_scaled": streams,
+             "inject_sigmoid": streams, "injection_weights": streams}
+    out = {k: np.zeros(sizes[k], dtype=np.uint16) for k in HYPER_OUTPUTS}
+    o = HyperOutputs(*[_p16(out[k]) for k in HYPER_OUTPUTS])
+    x, n, d, u = _u16(hidden), _u16(hc_norm), _u16(mix_down_w), _u16(mix_up_w)
+    inj = _u16(inject_w) if inject_w is not None else None
+    if not lib().fwo_hyper_connection(_p16(x), _p16(n), _p16(d), _p16(u), _p16(inj) if inj is not None else None,
+                                      streams, width, lowrank, ctypes.byref(o)):
+        raise ValueError("invalid hyper-connection shape")
+    return out
+
+
+def inject_residual(post_attention, moe_output, injection_weights, streams: int, width: int):
+    """(products [S*W], layer_output [S*W]) of src/decoder_layer.rs:587-607."""
+    p, m, w = _u16(post_attention), _u16(moe_output), _u16(injection_weights)
+    products = np.empty(streams * width, dtype=np.uint16)
+    out = np.empty(streams * width, dtype=np.uint16)
+    lib().fwo_inject_residual(_p16(p), _p16(m), _p16(w), streams, width, _p16(products), _p16(out))
+    return products, out
 
 
 def make_hidden(size: int, spec: dict) -> np.ndarray:
