@@ -408,6 +408,8 @@ def main() -> int:
                                "step_us": quantiles([1000.0 * v for v in per]),
                                "vs_single_token_steps": round(ms * 1000 / (width * us_per_token), 3),
                                "mean_union_experts_per_layer": round(float(np.mean(u)), 2),
+                               "mode": ("interleaved one-token chains" if ctx.token_chains(width) > 1
+                                        else "multi-token kernel (union experts read once)"),
                                "hbm_gbps": round(gbps, 1),
                                "frac": round(gbps / HBM_PEAK_GBPS, 4)}
             log(f"MTP width {width}: {ms * 1000:.1f} us/step, union {np.mean(u):.1f}, {gbps:.0f} GB/s")

@@ -78,14 +78,14 @@ struct DecodeParams {
     int prenorm;       // block input = rms_norm(residual) (chained step), else the input
     int bias_feature;  // with prenorm: block input [H-1] = 1.0
     int ls, gi;        // logit row stride (even) and shared_expert_gate index (even)
-    const uint16_t* x_in;  // [T][H] input of the first layer
+    const uint16_t* x_in;  // [chains][T][H] input of the first layer of each chain
     // tagged words (payload = two bf16, or one bf16 in the low half)
-    uint64_t* xw;          // [nlayers + 1][T][H / 2] residual stream (index 0 unused)
+    uint64_t* xw;          // [nlayers + chains][T][H / 2] residual stream (indices < chains unused)
     uint64_t* logits;      // [nlayers][T][ls / 2]
     uint64_t* shared_act;  // [nlayers][T][Is / 2]
     uint64_t* act;         // [nlayers][S][T][I / 2]
     // plain outputs, read after the launch
-    uint16_t* x_final;  // [T][H] residual after the last layer, or null
+    uint16_t* x_final;  // [chains][T][H] residual after the last layer of each chain, or null
     uint16_t* out;      // [nlayers][T][H] block outputs
     int32_t* ids;       // [nlayers][T][K] rank order
     uint16_t* scores;   // [nlayers][T][K]
@@ -105,8 +105,21 @@ struct DecodeParams {
                                           // alone (no combine phase flag)
     int rank_slots;                       // one token: slot s is the rank-s expert (B tasks run the
                                           // top-k only up to their own rank), not the s-th smallest id
+    int chains;                           // independent token chains interleaved by layer: layer li
+                                          // continues layer li - chains (1: consecutive layers)
     uint64_t* trace;     // profiling builds only
 };
+
+// A launch runs `chains` independent token chains interleaved by layer: layer
+// li of the launch continues layer li - chains of the same chain, and the
+// first `chains` layers read the caller's input (chain li at row li of x_in).
+// With one chain that is the ordinary sequence of layers.
+__device__ __forceinline__ bool chain_start(const DecodeParams& p, int li) { return li < p.chains; }
+__device__ __forceinline__ int chain_prev(const DecodeParams& p, int li) { return li - p.chains; }
+// this layer's input words ([T][H / 2]) when chain_start
+__device__ __forceinline__ const uint32_t* chain_input(const DecodeParams& p, int li) {
+    return reinterpret_cast<const uint32_t*>(p.x_in) + (size_t)li * p.T * p.H / 2;
+}
 
 // Task timing (wall clock) for profiling builds only (slots: trace_slot).
 #ifdef FW_DECODE_TRACE
@@ -244,8 +257,8 @@ __device__ __forceinline__ bool load_input(const DecodeParams& p, int li, uint32
     const int pairs = p.T * p.H / 2;
     float* xs = sh.xs;
     bool ok = true;
-    if (li == 0) {
-        const auto* x2 = as_global(reinterpret_cast<const uint32_t*>(p.x_in));
+    if (chain_start(p, li)) {
+        const auto* x2 = as_global(chain_input(p, li));
         uint32_t v[NT * kXWords];
 #pragma unroll
         for (int k = 0; k < NT * kXWords; ++k) {
@@ -621,8 +634,8 @@ __device__ __forceinline__ bool router_task(const DecodeParams& p, uint32_t epoc
         line_issue(rs, L.router + (size_t)row0 * H, (uint32_t)(valid ? rin : 0) * (uint32_t)H * 2u, q);
     // one-token steps: the residual words' tags alone say when the block
     // input is complete (a flag hop less on the layer's critical path)
-    if (li > 0 && !p.input_by_tags &&
-        !wait_phase(phase_flags(p, li - 1, kCntC), epoch, p.error, p.limit_ticks, &sh.flag))
+    if (!chain_start(p, li) && !p.input_by_tags &&
+        !wait_phase(phase_flags(p, chain_prev(p, li), kCntC), epoch, p.error, p.limit_ticks, &sh.flag))
         return false;
     FW_TRACE_STAMP(t1);
     if (!stage_layer_input<NT>(p, epoch, sh, st, li, slot)) return false;
@@ -692,7 +705,8 @@ __device__ __forceinline__ bool pairs_task(const DecodeParams& p, uint32_t epoch
         if (st.staged != li) {
             // the block input is ready with the previous layer: stage it while
             // the router runs
-            if (li > 0 && !wait_phase(phase_flags(p, li - 1, kCntC), epoch, p.error, p.limit_ticks, &sh.flag))
+            if (!chain_start(p, li) &&
+                !wait_phase(phase_flags(p, chain_prev(p, li), kCntC), epoch, p.error, p.limit_ticks, &sh.flag))
                 return false;
             if (!stage_layer_input<NT>(p, epoch, sh, st, li)) return false;
         }
@@ -721,7 +735,8 @@ __device__ __forceinline__ bool pairs_task(const DecodeParams& p, uint32_t epoch
     const uint16_t* wrow = wave_row + (size_t)row_rel * H;
     LineShare<MBH> rs;
     if (work) line_issue(rs, wave_row, row_rel * (uint32_t)H * 2u, q);
-    if (shared && li > 0 && !wait_phase(phase_flags(p, li - 1, kCntC), epoch, p.error, p.limit_ticks, &sh.flag))
+    if (shared && !chain_start(p, li) &&
+        !wait_phase(phase_flags(p, chain_prev(p, li), kCntC), epoch, p.error, p.limit_ticks, &sh.flag))
         return false;
     FW_TRACE_STAMP(t1);
     if (work) {
@@ -1097,8 +1112,8 @@ __device__ __forceinline__ bool combine_task(const DecodeParams& p, uint32_t epo
     bool ok = true;
     uint32_t rin = 0;
     if (mixer) {
-        if (li == 0) {
-            rin = reinterpret_cast<const uint32_t*>(p.x_in)[at];
+        if (chain_start(p, li)) {
+            rin = chain_input(p, li)[at];
         } else {
             uint64_t v[1];
             ok = load_tagged<1, 1>(v, p.xw + (size_t)li * T * H / 2 + at, 1, epoch, p.error, p.limit_ticks);
@@ -1169,8 +1184,9 @@ __device__ __forceinline__ bool combine_task(const DecodeParams& p, uint32_t epo
         if ((gg & 1) == 0) {
             const uint32_t o2 = o | (o_odd << 16), x2 = xn | (x_odd << 16);
             reinterpret_cast<uint32_t*>(p.out + (size_t)li * T * H)[at] = o2;
-            coherent_store64(p.xw + (size_t)(li + 1) * T * H / 2 + at, tagged(x2, epoch));
-            if (li + 1 == p.nlayers && p.x_final != nullptr) reinterpret_cast<uint32_t*>(p.x_final)[at] = x2;
+            coherent_store64(p.xw + (size_t)(li + p.chains) * T * H / 2 + at, tagged(x2, epoch));
+            if (li + p.chains >= p.nlayers && p.x_final != nullptr)
+                reinterpret_cast<uint32_t*>(p.x_final)[(size_t)(li + p.chains - p.nlayers) * T * H / 2 + at] = x2;
         }
     }
     if (!wg_all(sh.red, ok)) return false;
@@ -1215,13 +1231,18 @@ __device__ __forceinline__ bool combine_task_fused(const DecodeParams& p, uint32
     // the shared expert's rows need no selection: issue them first
     if (w == 0) line_issue(c[0], L.shared_down + (size_t)r0 * Is, (uint32_t)(g * Is * 2), q);
     // this task's gate/up pairs need the block input (ready with the previous layer)
-    if (li > 0 && !wait_phase(phase_flags(p, li - 1, kCntC), epoch, p.error, p.limit_ticks, &sh.flag)) return false;
+    if (!chain_start(p, li) &&
+        !wait_phase(phase_flags(p, chain_prev(p, li), kCntC), epoch, p.error, p.limit_ticks, &sh.flag))
+        return false;
     // the residual words this task updates (one lane of the lead wave per
     // row), taken from the block input before it is normalised in place
     const int rt = w * kWave + lane;
     const bool mixer = rt < kRowsPerCTask;
     const size_t at = ((size_t)r0 + (rt & ~1)) / 2;
-    if (st.staged != li) {
+    // without pairs of its own (p.cpairs == 0: the rows role runs every B
+    // task) the task needs only its residual words, not the block input
+    const bool own_pairs = p.cpairs > 0;
+    if (own_pairs && st.staged != li) {
         if (st.loaded != li) {
             if (!load_input<NT>(p, li, epoch, sh)) return false;
             st.loaded = li;
@@ -1233,10 +1254,9 @@ __device__ __forceinline__ bool combine_task_fused(const DecodeParams& p, uint32
         normalise_input<NT>(p, sh);
         st.staged = li;
     } else if (mixer) {
-        // (not reached: one C task per workgroup and layer stages its input)
         uint32_t v0;
-        if (li == 0) {
-            v0 = reinterpret_cast<const uint32_t*>(p.x_in)[at];
+        if (chain_start(p, li)) {
+            v0 = chain_input(p, li)[at];
         } else {
             uint64_t v[1];
             if (!load_tagged<1, 1>(v, p.xw + (size_t)li * H / 2 + at, 1, epoch, p.error, p.limit_ticks)) return false;
@@ -1258,7 +1278,7 @@ __device__ __forceinline__ bool combine_task_fused(const DecodeParams& p, uint32
     // the four rows of H bf16, H / 2 + 16 words apart (see kBRowStride)
     uint64_t* brows = reinterpret_cast<uint64_t*>(sh.xs + kBRowsAt);
     const int bstride = (H / 2 + 16) / 2;  // 8-byte words
-    if (w == 0) {
+    if (w == 0 && own_pairs) {
         // 1 KB per wave instruction (16 bytes per lane)
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
@@ -1308,7 +1328,10 @@ __device__ __forceinline__ bool combine_task_fused(const DecodeParams& p, uint32
     // lead wave: as soon as its rows are in LDS (its own loads: no barrier),
     // the two pairs' dots and SwiGLU (src/expert.rs:514-571); lane 0 stores
     // the word of both activations
-    if (w == 0) {
+    if (w == 0 && !own_pairs) {
+        if (lane == 0) __hip_atomic_store(&sh.rows_landed, seq, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+        issue_down();
+    } else if (w == 0) {
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
         FW_TRACE_MARK_IF(lane == 0, slot, 10);
         if (lane == 0) __hip_atomic_store(&sh.rows_landed, seq, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
@@ -1383,8 +1406,9 @@ __device__ __forceinline__ bool combine_task_fused(const DecodeParams& p, uint32
         if ((gg & 1) == 0) {
             const uint32_t o2 = o | (o_odd << 16), x2 = xn | (x_odd << 16);
             reinterpret_cast<uint32_t*>(p.out + (size_t)li * H)[at] = o2;
-            coherent_store64(p.xw + (size_t)(li + 1) * H / 2 + at, tagged(x2, epoch));
-            if (li + 1 == p.nlayers && p.x_final != nullptr) reinterpret_cast<uint32_t*>(p.x_final)[at] = x2;
+            coherent_store64(p.xw + (size_t)(li + p.chains) * H / 2 + at, tagged(x2, epoch));
+            if (li + p.chains >= p.nlayers && p.x_final != nullptr)
+                reinterpret_cast<uint32_t*>(p.x_final)[(size_t)(li + p.chains - p.nlayers) * H / 2 + at] = x2;
         }
     }
     if (!wg_all(sh.red, ok)) return false;

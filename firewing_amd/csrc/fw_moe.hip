@@ -325,6 +325,9 @@ struct firewing_hip_context {
     std::vector<uint16_t*> router;  // [E + 1][H] per layer
     std::vector<uint16_t*> gate_up, down, shared_gate, shared_up, shared_down;
     DecodeLayer* d_layers = nullptr;  // [L]
+    // interleaved token chains: for each chain count c = 2..kMaxTokens, [L * c]
+    // entries, entry v = layer v / c (see vlayers_offset)
+    DecodeLayer* d_vlayers = nullptr;
     uint16_t* d_weight_table = nullptr;
     // decode scratch sized for L layers and T <= 4
     uint16_t* xin = nullptr;     // [T][H] host input staged for the launch
@@ -443,15 +446,50 @@ int decode_grid(const firewing_hip_context* c, int T) {
     return per_cu * c->cu_count;
 }
 
+// First entry of the interleaved layer table for `chains` chains (2..kMaxTokens)
+// over L layers: the tables for 2, 3, ... chains follow one another.
+size_t vlayers_offset(size_t L, int chains) { return L * (size_t)((chains - 2) * (chains + 1) / 2); }
+
+// Whether one-token work at this shape runs the fused C task: every C task of
+// a layer resident at once (one combine workgroup each), the B tasks past the
+// rows role's one per workgroup coming to exactly two gate/up pairs per C task,
+// and the lane layouts of the fused kernel (I, Is multiples of 256, H of 512).
+bool one_token_fused(const firewing_hip_context* c) {
+    const firewing_hip_shape& sh = c->shape;
+    const int n_c = (int)(sh.hidden / kRowsPerCTask);
+    const int n_b = (int)(sh.top_k * (sh.intermediate / kPairsPerTask));
+    const int grid = c->grid[1];
+    const int g_comb = std::min(n_c, grid / 2);
+    const int nb_rows = std::min(n_b, grid - g_comb);
+    const int mbh = sh.hidden > 2048 ? 80 : 64;
+    const int mbi = std::max(sh.intermediate, sh.shared_intermediate) > 512 ? 32 : 16;
+    return fused_combine(1, mbh, mbi) && g_comb == n_c && sh.top_k + 1 <= (size_t)kDirectVectors &&
+           sh.intermediate % 256 == 0 && sh.shared_intermediate % 256 == 0 && sh.hidden % 512 == 0 &&
+           (long)n_b * kPairsPerTask - (long)nb_rows * kPairsPerTask == 2L * n_c;
+}
+
 // Launch the persistent kernel over layers [first, first + n) for T tokens.
 // x_in holds the input of the first layer ([T][H] bf16, 4-byte aligned).
+// Where one-token work runs fused, T >= 2 tokens run as T independent
+// one-token chains interleaved by layer (launch layer l * T + t = layer l of
+// token t; the outputs' [layer][token] order is the same), so the chains'
+// serial steps overlap; otherwise the T-token kernel reads each union expert
+// once for all its tokens.
 void launch_decode(firewing_hip_context* c, size_t first, size_t n, int T, int order,
                    bool prenorm, bool bias_feature, const uint16_t* x_in, uint16_t* x_final,
                    hipStream_t s) {
     const firewing_hip_shape& sh = c->shape;
+    const bool fused = one_token_fused(c);
+    const int chains = (T >= 2 && fused) ? T : 1;
     DecodeParams p{};
     p.layers = c->d_layers + first;
+    if (chains > 1) {
+        T = 1;
+        p.layers = c->d_vlayers + vlayers_offset(c->shape.layers, chains) + first * chains;
+        n *= chains;
+    }
     p.nlayers = (int)n;
+    p.chains = chains;
     p.T = T;
     p.H = (int)sh.hidden;
     p.I = (int)sh.intermediate;
@@ -462,7 +500,7 @@ void launch_decode(firewing_hip_context* c, size_t first, size_t n, int T, int o
     p.prenorm = prenorm ? 1 : 0;
     p.bias_feature = bias_feature ? 1 : 0;
     p.S = p.K * T;
-    const size_t L = n, Tn = (size_t)T, H = sh.hidden, E = sh.experts, K = sh.top_k;
+    const size_t H = sh.hidden, E = sh.experts;
     const size_t S = (size_t)p.S, I = sh.intermediate, Is = sh.shared_intermediate;
     p.x_in = x_in;
     p.xw = c->xw;
@@ -484,9 +522,6 @@ void launch_decode(firewing_hip_context* c, size_t first, size_t n, int T, int o
     p.n_shared = (int)((Is + kPairsPerTask - 1) / kPairsPerTask);
     p.n_b = (int)(S * (I / kPairsPerTask));
     p.n_c = (int)(H / kRowsPerCTask);
-    (void)L;
-    (void)Tn;
-    (void)K;
     // Roles: the combine role gets one workgroup per C task of a layer where
     // the grid allows (so every task's down rows are in flight before the
     // gate/up phase ends), at most half of the grid. The rows role takes one
@@ -516,20 +551,24 @@ void launch_decode(firewing_hip_context* c, size_t first, size_t n, int T, int o
     p.cpairs = 0;
     if (T == 1) {
         roles(1);
-        const int mbh = sh.hidden > 2048 ? 80 : 64;
-        const int mbi = std::max(sh.intermediate, sh.shared_intermediate) > 512 ? 32 : 16;
-        if (fused_combine(1, mbh, mbi) && p.g_comb == p.n_c && K + 1 <= kDirectVectors && I % 256 == 0 &&
-            Is % 256 == 0 && H % 512 == 0 &&
-            (long)S * (long)I - (long)p.nb_rows * kPairsPerTask == 2L * p.n_c)
-            p.cpairs = 2;
-        else
+        if (!fused) {
             kt = 2;
+        } else if (chains == 1) {
+            p.cpairs = 2;
+        } else {
+            // interleaved chains: a combine workgroup runs the chains' C tasks
+            // one after another, so they carry no pairs; the rows role, with
+            // time to spare between a chain's layers, runs every B task
+            p.nb_rows = p.n_b;
+        }
     }
     if (kt != 1) roles(kt);
     p.n_gu = p.n_shared + (p.cpairs > 0 ? p.nb_rows + p.n_c : p.n_b);
     p.cu_count = c->cu_count;
-    p.input_by_tags = p.cpairs > 0 ? 1 : 0;
-    p.rank_slots = p.cpairs > 0 ? 1 : 0;  // the fused one-token C task reads rank-ordered slots
+    // the fused one-token C task reads its activations by their tags and
+    // rank-ordered slots
+    p.input_by_tags = kt == 1 ? 1 : 0;
+    p.rank_slots = kt == 1 ? 1 : 0;
     p.trace = c->trace;
     // The kernel reads its parameters from a device copy; upload only on change
     // (the copy is stream-ordered before the launch; pageable source, staged).
@@ -902,6 +941,12 @@ bool firewing_hip_create(const firewing_hip_shape* shape, firewing_hip_context**
         c->d_layers = dalloc<DecodeLayer>(L);
         check(hipMemcpy(c->d_layers, layers.data(), L * sizeof(DecodeLayer), hipMemcpyHostToDevice),
               "hipMemcpy layers");
+        std::vector<DecodeLayer> vlayers(vlayers_offset(L, kMaxTokens + 1));
+        for (int chains = 2; chains <= kMaxTokens; ++chains)
+            for (size_t v = 0; v < L * chains; ++v) vlayers[vlayers_offset(L, chains) + v] = layers[v / chains];
+        c->d_vlayers = dalloc<DecodeLayer>(vlayers.size());
+        check(hipMemcpy(c->d_vlayers, vlayers.data(), vlayers.size() * sizeof(DecodeLayer), hipMemcpyHostToDevice),
+              "hipMemcpy interleaved layers");
         const size_t T = kMaxTokens, S = K * T;
         c->xin = dalloc<uint16_t>(T * H);
         c->xfinal = dalloc<uint16_t>(T * H);
@@ -918,12 +963,14 @@ bool firewing_hip_create(const firewing_hip_shape* shape, firewing_hip_context**
         check(hipMemset(c->logits, 0, L * T * logit_stride((int)E) / 2 * 8), "hipMemset");
         check(hipMemset(c->shared_act, 0, L * T * Is / 2 * 8), "hipMemset");
         check(hipMemset(c->act, 0, L * S * T * I / 2 * 8), "hipMemset");
-        c->counters = dalloc<uint32_t>((L * kCountersPerLayer + 1) * kCounterGroupWords);
+        // phase counters and flags per launch layer: up to L * kMaxTokens with interleaved chains
+        const size_t LV = L * kMaxTokens;
+        c->counters = dalloc<uint32_t>((LV * kCountersPerLayer + 1) * kCounterGroupWords);
         c->error = dalloc<int32_t>(1);
         c->d_params = dalloc<DecodeParams>(1);
-        check(hipMemset(c->counters, 0, (L * kCountersPerLayer + 1) * kCounterGroupWords * 4), "hipMemset counters");
-        c->flags = dalloc<uint32_t>(L * kCountersPerLayer * kFlagCopies * kFlagStride);
-        check(hipMemset(c->flags, 0, L * kCountersPerLayer * kFlagCopies * kFlagStride * 4), "hipMemset flags");
+        check(hipMemset(c->counters, 0, (LV * kCountersPerLayer + 1) * kCounterGroupWords * 4), "hipMemset counters");
+        c->flags = dalloc<uint32_t>(LV * kCountersPerLayer * kFlagCopies * kFlagStride);
+        check(hipMemset(c->flags, 0, LV * kCountersPerLayer * kFlagCopies * kFlagStride * 4), "hipMemset flags");
         check(hipMemset(c->error, 0, 4), "hipMemset error");
         for (int t = 1; t <= kMaxTokens; ++t) c->grid[t] = decode_grid(c, t);
         // zero the banks so uninstalled layers are defined
@@ -957,7 +1004,7 @@ void firewing_hip_destroy(firewing_hip_context* c) {
     c->shared_up.clear();  // inside the shared_gate allocations
     freev(c->shared_gate);
     freev(c->shared_down);
-    void* bufs[] = {c->d_layers, c->d_weight_table, c->xin, c->xfinal, c->out, c->ids, c->scores,
+    void* bufs[] = {c->d_layers, c->d_vlayers, c->d_weight_table, c->xin, c->xfinal, c->out, c->ids, c->scores,
                     c->sig, c->xw, c->logits, c->shared_act, c->act, c->counters, c->flags,
                     c->error, c->d_params};
     for (void* b : bufs)
@@ -1771,8 +1818,10 @@ extern "C" bool firewing_hip_debug_traced_step(firewing_hip_context* c, const ui
         const size_t L = c->shape.layers, H = c->shape.hidden;
         const size_t E = c->shape.experts, K = c->shape.top_k, I = c->shape.intermediate;
         const size_t Is = c->shape.shared_intermediate;
-        size_t per_layer = (E + 15) / 16 + 1 + (Is + 7) / 8 + K * tokens * (I / 8) + H / 4;
-        size_t n = L * per_layer;
+        // launch layers of one-token work when the tokens run as interleaved chains
+        const size_t chains = tokens >= 2 && one_token_fused(c) ? tokens : 1;
+        size_t per_layer = (E + 15) / 16 + 1 + (Is + 7) / 8 + K * (tokens / chains) * (I / 8) + H / 4;
+        size_t n = L * chains * per_layer;
         if (cap < n * kTraceWords) return fail("trace buffer too small");
         c->trace = dalloc<uint64_t>(n * kTraceWords);
         check(hipMemset(c->trace, 0, n * kTraceWords * 8), "hipMemset trace");
@@ -1789,6 +1838,11 @@ extern "C" bool firewing_hip_debug_traced_step(firewing_hip_context* c, const ui
     });
 }
 #endif
+
+size_t firewing_hip_token_chains(const firewing_hip_context* c, size_t tokens) {
+    if (!c) return 0;
+    return tokens >= 2 && one_token_fused(c) ? tokens : 1;
+}
 
 bool firewing_hip_synchronize(firewing_hip_context* c) {
     return guarded([&] {

@@ -136,6 +136,7 @@ _SIGNATURES = {
     "firewing_hip_moe_step_dev": (_b, [_vp, _vp, _sz, ctypes.c_int, _b, _vp, _vp, _vp, _vp, _vp]),
     "firewing_hip_moe_step": (_b, [_vp, _u16p, _sz, ctypes.c_int, _b, _u16p, _u16p, _vp, _u16p]),
     "firewing_hip_synchronize": (_b, [_vp]),
+    "firewing_hip_token_chains": (_sz, [_vp, _sz]),
     "firewing_hip_set_wait_timeout": (_b, [_vp, ctypes.c_double]),
     "firewing_hip_synth_hidden": (None, [ctypes.c_uint64, ctypes.c_uint32, ctypes.c_uint32,
                                          ctypes.c_uint32, _b, _u16p]),
@@ -455,6 +456,11 @@ class MoeContext:
                          order: int = LOGITS_TREE32, stream=None) -> None:
         _call("firewing_hip_moe_sublayer_dev", self._h, layer, _addr(post_attention), tokens, order,
               _addr(layer_output), _addr(stream))
+
+    def token_chains(self, tokens: int) -> int:
+        """Independent one-token chains a step of `tokens` tokens interleaves
+        (1: the multi-token kernel)."""
+        return int(lib().firewing_hip_token_chains(self._h, tokens))
 
     def load_layer_safetensors(self, layer: int, path, prefix: str | None = None) -> None:
         """Install resident layer `layer` from a safetensors checkpoint (a

@@ -367,6 +367,14 @@ bool firewing_hip_moe_sublayer(firewing_hip_context* ctx, size_t layer, const ui
 bool firewing_hip_moe_sublayer_dev(firewing_hip_context* ctx, size_t layer, const uint16_t* post_attention,
                                    size_t tokens, int order, uint16_t* layer_output, void* stream);
 
+/* No counterpart in the reference: how a step of `tokens` (<= 4) tokens runs
+ * on this context: the number of independent one-token chains it interleaves
+ * by layer (= tokens where the fused one-token path applies at the context's
+ * shape: the chains' serial steps overlap), or 1 for the multi-token kernel
+ * (each union expert's rows read once for all its tokens). Results are the
+ * same either way. 0 for a null context. */
+size_t firewing_hip_token_chains(const firewing_hip_context* ctx, size_t tokens);
+
 /* Seeded synthetic hidden vectors of the benchmark workload (host memory):
  * bf16(N(0,1)) RMS-normalised, x[H-1] = 1.0 when bias_feature (the constant
  * feature that carries the Zipf router bias). No counterpart in the reference,
