@@ -19,6 +19,8 @@ Prints one JSON line (the driver contract) with:
   mtp          the same step with 2 and 4 tokens (MTP verify widths)
   real_shape   the step at the reference model's real block shape (H=2560,
                I=Is=640, 48 layers, ~242 GB resident), beside the headline
+  lm_head      the reference model's LM head (248,320 x 2560, 1.27 GB):
+               exact-order logits and top-20, 1 and 4 tokens per step
   prefill      8192 tokens through one resident block (router, top-10,
                grouped bf16 MFMA expert GEMMs, ordered combine): tokens/s from
                HIP events on the launch stream; the phases (router, GEMMs, ...)
@@ -238,6 +240,50 @@ def bench_real_shape(rt, hm, args) -> dict:
             "resident_gb": round(L * (layer_bytes(REAL_SHAPE, REAL_SHAPE["experts"])) / 1e9, 1)}
 
 
+LM_HEAD = dict(hidden=2560, vocab=248320, k=20)
+
+
+def bench_lm_head(rt, hm, args) -> dict:
+    """The LM head of the reference model (248,320 x 2560 bf16, 1.27 GB,
+    seeded synthetic weights): logits and top-20 per step on one stream, HIP
+    events around each step; T = 1 and 4 tokens."""
+    H, V, k = LM_HEAD["hidden"], LM_HEAD["vocab"], LM_HEAD["k"]
+    ctx = hm.MoeContext(hidden=H, intermediate=32, experts=16, top_k=4, shared_intermediate=32, layers=1)
+    res = {"vocab": V, "hidden": H, "k": k, "head_bytes": V * H * 2}
+    try:
+        ctx.generate_lm_head(V, args.seed)
+        stream = rt.Stream()
+        for T in (1, 4):
+            x_host = hm.synth_hidden(args.seed, T, H, False)
+            x = rt.DeviceArray.from_numpy(x_host)
+            ids = rt.DeviceArray((T, k), np.int32)
+            vals = rt.DeviceArray((T, k), np.uint16)
+            for _ in range(3):
+                ctx.lm_head_dev(x.ptr, T, k, ids.ptr, vals.ptr, stream=stream.handle)
+            stream.synchronize()
+            steps = max(10, args.steps)
+            ev = [rt.Event() for _ in range(steps + 1)]
+            ev[0].record(stream)
+            for i in range(steps):
+                ctx.lm_head_dev(x.ptr, T, k, ids.ptr, vals.ptr, stream=stream.handle)
+                ev[i + 1].record(stream)
+            stream.synchronize()
+            per = [1000.0 * ev[i].elapsed_ms(ev[i + 1]) for i in range(steps)]
+            us = float(np.median(per))
+            gbps = V * H * 2 / (us * 1e-6) / 1e9
+            res[f"t{T}"] = {"us_per_step": round(us, 1), "step_us": quantiles(per), "hbm_gbps": round(gbps, 1),
+                            "frac": round(gbps / HBM_PEAK_GBPS, 4)}
+            log(f"LM head {V} x {H}, {T} token(s): {us:.1f} us/step, {gbps:.0f} GB/s")
+            for e in ev:
+                e.destroy()
+            for a in (x, ids, vals):
+                a.free()
+        stream.destroy()
+    finally:
+        ctx.close()
+    return res
+
+
 def cpu_model() -> str:
     try:
         for line in Path("/proc/cpuinfo").read_text().splitlines():
@@ -297,6 +343,7 @@ def main() -> int:
     ap.add_argument("--no-mtp", action="store_true")
     ap.add_argument("--no-prefill", action="store_true")
     ap.add_argument("--no-real-shape", action="store_true")
+    ap.add_argument("--no-lm-head", action="store_true")
     ap.add_argument("--prefill-only", action="store_true",
                     help="time the 8K-token prefill block alone (for kernel traces)")
     ap.add_argument("--copy-calibration", action="store_true",
@@ -430,6 +477,9 @@ def main() -> int:
         except Exception as e:  # reported, not fatal: the headline stands on its own
             log(f"real-shape step skipped: {e}")
             result["real_shape"] = {"skipped": str(e)}
+
+    if not args.no_lm_head:
+        result["lm_head"] = bench_lm_head(rt, hm, args)
 
     if not args.no_cpu_baseline:
         threads_n = max(1, min(16, os.cpu_count() or 1))

@@ -26,6 +26,7 @@
 #include "fw_decode.h"
 #include "fw_device.h"
 #include "fw_hyper.h"
+#include "fw_lm_head.h"
 #include "fw_numerics.h"
 #include "fw_prefill.h"
 #include "fw_safetensors.h"
@@ -366,6 +367,16 @@ struct firewing_hip_context {
         uint16_t *inject_scaled = nullptr, *inject_sigmoid = nullptr, *weights = nullptr;
         uint16_t *post = nullptr, *layer_out = nullptr, *inj_products = nullptr;
     } hc;
+    // LM head [vocab][H] (installed on demand) and its scratch for T <= 4
+    struct LmHead {
+        size_t vocab = 0;
+        uint16_t* weight = nullptr;   // + kLineSharePad bytes
+        uint16_t* logits = nullptr;   // [T][vocab]
+        uint64_t* cand = nullptr;     // [T][chunks][kMaxLmTopK]
+        int32_t* ids = nullptr;       // [T][kMaxLmTopK]
+        uint16_t* values = nullptr;   // [T][kMaxLmTopK]
+        int grid = 0;                 // workgroups of k_lm_head
+    } lm;
 };
 
 namespace {
@@ -1012,6 +1023,9 @@ void firewing_hip_destroy(firewing_hip_context* c) {
     for (void* b : c->pf.owned)
         if (b) (void)hipFree(b);
     for (void* b : c->hc.owned)
+        if (b) (void)hipFree(b);
+    for (void* b : {(void*)c->lm.weight, (void*)c->lm.logits, (void*)c->lm.cand, (void*)c->lm.ids,
+                    (void*)c->lm.values})
         if (b) (void)hipFree(b);
     if (c->last) (void)hipEventDestroy(c->last);
     if (c->stream) (void)hipStreamDestroy(c->stream);
@@ -2191,6 +2205,174 @@ bool firewing_hip_moe_sublayer(firewing_hip_context* c, size_t layer, const uint
             collect_block_captures(c, layer, h.mixed, T, &cap->block, s);
         }
         check(hipStreamSynchronize(s), "hipStreamSynchronize");
+        return true;
+    });
+}
+
+// ---- LM head ----
+
+namespace {
+
+constexpr int kMaxLmTopK = 64;
+
+// (Re)allocate the head for `vocab` rows; waits for the context's last work
+// before freeing anything.
+void lm_reserve(firewing_hip_context* c, size_t vocab) {
+    auto& m = c->lm;
+    if (m.vocab == vocab && m.weight) return;
+    if (m.weight) check(hipEventSynchronize(c->last), "hipEventSynchronize");
+    for (void* b : {(void*)m.weight, (void*)m.logits, (void*)m.cand, (void*)m.ids, (void*)m.values})
+        if (b) (void)hipFree(b);
+    m = firewing_hip_context::LmHead{};
+    const size_t H = c->shape.hidden, T = kMaxTokens;
+    const size_t chunks = (vocab + kTopkChunk - 1) / kTopkChunk;
+    m.weight = dalloc<uint16_t>(vocab * H + kLineSharePad / 2);
+    m.logits = dalloc<uint16_t>(T * vocab);
+    m.cand = dalloc<uint64_t>(T * chunks * kMaxLmTopK);
+    m.ids = dalloc<int32_t>(T * kMaxLmTopK);
+    m.values = dalloc<uint16_t>(T * kMaxLmTopK);
+    m.vocab = vocab;
+}
+
+bool lm_args_ok(firewing_hip_context* c, size_t vocab, std::string* why) {
+    if (!c) {
+        *why = "null context";
+        return false;
+    }
+    if (vocab == 0 || vocab > (size_t)INT32_MAX / 8 || vocab * c->shape.hidden * 2 > ((size_t)1 << 33)) {
+        *why = "vocab must be in [1, 2^28) with the head below 8 GiB";
+        return false;
+    }
+    return true;
+}
+
+template <int NT>
+const void* lm_kernel(bool wide) {
+    return wide ? reinterpret_cast<const void*>(&k_lm_head<NT, 80>) : reinterpret_cast<const void*>(&k_lm_head<NT, 64>);
+}
+
+const void* lm_kernel_for(int T, bool wide) {
+    switch (T) {
+        case 1: return lm_kernel<1>(wide);
+        case 2: return lm_kernel<2>(wide);
+        case 3: return lm_kernel<3>(wide);
+        default: return lm_kernel<4>(wide);
+    }
+}
+
+// logits [T][V] (scratch when null), then the top-k ids and values, on stream s.
+void queue_lm_head(firewing_hip_context* c, const uint16_t* x, int T, int k, uint16_t* logits, int32_t* ids,
+                   uint16_t* values, hipStream_t s) {
+    auto& m = c->lm;
+    const int V = (int)m.vocab, H = (int)c->shape.hidden;
+    const bool wide = H > 2048;
+    const void* fn = lm_kernel_for(T, wide);
+    if (m.grid == 0) {
+        int per_cu = 0;
+        check(hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, 256, (size_t)kMaxTokens * H * 4),
+              "hipOccupancyMaxActiveBlocksPerMultiprocessor");
+        m.grid = std::max(1, per_cu) * c->cu_count;
+    }
+    uint16_t* out = logits ? logits : m.logits;
+    const uint16_t* w = m.weight;
+    void* args[] = {&w, &x, (void*)&V, (void*)&H, &out};
+    check(hipLaunchKernel(fn, dim3((unsigned)m.grid), dim3(256), args, (size_t)T * H * 4, s), "k_lm_head launch");
+    const int chunks = (V + kTopkChunk - 1) / kTopkChunk;
+    hipLaunchKernelGGL(k_lm_topk_chunks, dim3((unsigned)chunks, (unsigned)T), dim3(256), 0, s, out, V, k, m.cand);
+    check(hipGetLastError(), "k_lm_topk_chunks launch");
+    hipLaunchKernelGGL(k_lm_topk_merge, dim3((unsigned)T), dim3(256), 0, s, m.cand, chunks * k, k, ids, values);
+    check(hipGetLastError(), "k_lm_topk_merge launch");
+}
+
+}  // namespace
+
+bool firewing_hip_install_lm_head(firewing_hip_context* c, const uint16_t* weight, size_t vocab) {
+    return guarded([&] {
+        std::string why;
+        if (!lm_args_ok(c, vocab, &why)) return fail("install_lm_head: " + why);
+        if (!weight) return fail("install_lm_head: null weight");
+        lm_reserve(c, vocab);
+        Ordered ordered(c, nullptr);
+        upload(c->lm.weight, weight, vocab * c->shape.hidden * 2, ordered.s);
+        check(hipStreamSynchronize(ordered.s), "hipStreamSynchronize");
+        return true;
+    });
+}
+
+bool firewing_hip_generate_lm_head(firewing_hip_context* c, size_t vocab, uint64_t seed) {
+    return guarded([&] {
+        std::string why;
+        if (!lm_args_ok(c, vocab, &why)) return fail("generate_lm_head: " + why);
+        lm_reserve(c, vocab);
+        Ordered ordered(c, nullptr);
+        if (!c->d_weight_table) {
+            std::vector<uint16_t> table(65536);
+            fw_synth_normal_table(FW_SYNTH_WEIGHT_SIGMA, table.data());
+            c->d_weight_table = dalloc<uint16_t>(65536);
+            check(hipMemcpy(c->d_weight_table, table.data(), 65536 * 2, hipMemcpyHostToDevice), "hipMemcpy table");
+        }
+        const size_t n = vocab * c->shape.hidden;
+        const uint64_t stream = fw_synth_stream(seed, 0, FW_SYNTH_LM_HEAD);
+        const size_t quads = (n + 3) / 4;
+        hipLaunchKernelGGL(k_generate, dim3((unsigned)((quads + 255) / 256)), dim3(256), 0, ordered.s, c->lm.weight, n,
+                           stream, (uint64_t)0, (const uint16_t*)c->d_weight_table);
+        check(hipGetLastError(), "k_generate launch");
+        check(hipStreamSynchronize(ordered.s), "hipStreamSynchronize");
+        return true;
+    });
+}
+
+bool firewing_hip_load_lm_head_safetensors(firewing_hip_context* c, const char* path, const char* tensor,
+                                           size_t vocab) {
+    return guarded([&] {
+        std::string why;
+        if (!lm_args_ok(c, vocab, &why)) return fail("load_lm_head_safetensors: " + why);
+        if (!path || !tensor) return fail("load_lm_head_safetensors: null path or tensor name");
+        fw::st::Checkpoint ckpt(path);
+        fw::st::Span sp;
+        const auto& t = ckpt.bf16(tensor, {(uint64_t)vocab, (uint64_t)c->shape.hidden}, &sp.file);
+        lm_reserve(c, vocab);
+        Ordered ordered(c, nullptr);
+        FileStreamer streamer(ordered.s);
+        streamer.copy(sp.file, t.offset, t.bytes, c->lm.weight);
+        check(hipStreamSynchronize(ordered.s), "hipStreamSynchronize");
+        return true;
+    });
+}
+
+bool firewing_hip_lm_head_dev(firewing_hip_context* c, const uint16_t* hidden, size_t tokens, size_t k,
+                              uint16_t* logits, int32_t* ids, uint16_t* values, void* stream) {
+    return guarded([&] {
+        if (!c) return fail("lm_head: null context");
+        if (!c->lm.weight) return fail("lm_head: no LM head installed");
+        if (tokens == 0 || tokens > (size_t)kMaxTokens) return fail("lm_head: tokens must be in [1, 4]");
+        if (k == 0 || k > (size_t)kMaxLmTopK || k > c->lm.vocab) return fail("lm_head: k must be in [1, min(64, vocab)]");
+        if (!hidden || !ids || !values) return fail("lm_head: null pointer");
+        Ordered ordered(c, stream);
+        queue_lm_head(c, hidden, (int)tokens, (int)k, logits, ids, values, ordered.s);
+        return true;
+    });
+}
+
+bool firewing_hip_lm_head(firewing_hip_context* c, const uint16_t* hidden, size_t tokens, size_t k,
+                          uint16_t* logits, size_t* ids, uint16_t* values) {
+    return guarded([&] {
+        if (!c) return fail("lm_head: null context");
+        if (!c->lm.weight) return fail("lm_head: no LM head installed");
+        if (tokens == 0 || tokens > (size_t)kMaxTokens) return fail("lm_head: tokens must be in [1, 4]");
+        if (k == 0 || k > (size_t)kMaxLmTopK || k > c->lm.vocab) return fail("lm_head: k must be in [1, min(64, vocab)]");
+        if (!hidden || !ids || !values) return fail("lm_head: null pointer");
+        Ordered ordered(c, nullptr);
+        hipStream_t s = ordered.s;
+        const size_t H = c->shape.hidden, V = c->lm.vocab;
+        upload(c->xin, hidden, tokens * H * 2, s);
+        queue_lm_head(c, c->xin, (int)tokens, (int)k, nullptr, c->lm.ids, c->lm.values, s);
+        if (logits) download(logits, c->lm.logits, tokens * V * 2, s);
+        std::vector<int32_t> hid(tokens * k);
+        download(hid.data(), c->lm.ids, tokens * k * 4, s);
+        download(values, c->lm.values, tokens * k * 2, s);
+        check(hipStreamSynchronize(s), "hipStreamSynchronize");
+        for (size_t i = 0; i < hid.size(); ++i) ids[i] = (size_t)hid[i];
         return true;
     });
 }

@@ -35,7 +35,8 @@ enum fw_synth_tensor {
     FW_SYNTH_SHARED_DOWN = 6,
     FW_SYNTH_SHARED_EXPERT_GATE = 7,
     FW_SYNTH_HIDDEN = 8,
-    FW_SYNTH_PERMUTATION = 9
+    FW_SYNTH_PERMUTATION = 9,
+    FW_SYNTH_LM_HEAD = 10
 };
 
 /* Weight standard deviation for every synthetic weight tensor. */

@@ -137,6 +137,11 @@ _SIGNATURES = {
     "firewing_hip_moe_step": (_b, [_vp, _u16p, _sz, ctypes.c_int, _b, _u16p, _u16p, _vp, _u16p]),
     "firewing_hip_synchronize": (_b, [_vp]),
     "firewing_hip_token_chains": (_sz, [_vp, _sz]),
+    "firewing_hip_install_lm_head": (_b, [_vp, _u16p, _sz]),
+    "firewing_hip_generate_lm_head": (_b, [_vp, _sz, ctypes.c_uint64]),
+    "firewing_hip_load_lm_head_safetensors": (_b, [_vp, ctypes.c_char_p, ctypes.c_char_p, _sz]),
+    "firewing_hip_lm_head": (_b, [_vp, _u16p, _sz, _sz, _vp, _szp, _u16p]),
+    "firewing_hip_lm_head_dev": (_b, [_vp, _vp, _sz, _sz, _vp, _vp, _vp, _vp]),
     "firewing_hip_set_wait_timeout": (_b, [_vp, ctypes.c_double]),
     "firewing_hip_synth_hidden": (None, [ctypes.c_uint64, ctypes.c_uint32, ctypes.c_uint32,
                                          ctypes.c_uint32, _b, _u16p]),
@@ -361,6 +366,7 @@ class MoeContext:
         self.H, self.I, self.E, self.K = hidden, intermediate, experts, top_k
         self.Is, self.L = shared_intermediate, layers
         self.hc_streams, self.hc_lowrank = 0, 0
+        self.vocab = 0
         handle = ctypes.c_void_p()
         _call("firewing_hip_create", ctypes.byref(self.shape), ctypes.byref(handle))
         self._h = handle
@@ -456,6 +462,40 @@ class MoeContext:
                          order: int = LOGITS_TREE32, stream=None) -> None:
         _call("firewing_hip_moe_sublayer_dev", self._h, layer, _addr(post_attention), tokens, order,
               _addr(layer_output), _addr(stream))
+
+    def install_lm_head(self, weight, vocab: int) -> None:
+        w = _u16(weight)
+        if w.size != vocab * self.H:
+            raise FirewingError("install_lm_head: weight size does not match vocab x hidden")
+        _call("firewing_hip_install_lm_head", self._h, _p16(w), vocab)
+        self.vocab = vocab
+
+    def generate_lm_head(self, vocab: int, seed: int) -> None:
+        _call("firewing_hip_generate_lm_head", self._h, vocab, seed)
+        self.vocab = vocab
+
+    def load_lm_head_safetensors(self, path, tensor: str, vocab: int) -> None:
+        _call("firewing_hip_load_lm_head_safetensors", self._h, os.fsencode(str(path)), tensor.encode(), vocab)
+        self.vocab = vocab
+
+    def lm_head(self, hidden, k: int = 20, logits: bool = True) -> dict:
+        """logits [T, vocab] (with logits=True), ids [T, k] and values [T, k]
+        of the LM head for T <= 4 tokens (src/text_output.rs:273-287)."""
+        x = _u16(hidden).reshape(-1, self.H)
+        T = x.shape[0]
+        out = np.empty((T, self.vocab), dtype=np.uint16) if logits else None
+        ids = (ctypes.c_size_t * (T * k))()
+        values = np.empty((T, k), dtype=np.uint16)
+        _call("firewing_hip_lm_head", self._h, _p16(x), T, k, out.ctypes.data if logits else None, ids,
+              _p16(values))
+        res = {"ids": np.array(list(ids), dtype=np.int64).reshape(T, k), "values": values}
+        if logits:
+            res["logits"] = out
+        return res
+
+    def lm_head_dev(self, hidden, tokens: int, k: int, ids, values, logits=None, stream=None) -> None:
+        _call("firewing_hip_lm_head_dev", self._h, _addr(hidden), tokens, k, _addr(logits), _addr(ids),
+              _addr(values), _addr(stream))
 
     def token_chains(self, tokens: int) -> int:
         """Independent one-token chains a step of `tokens` tokens interleaves

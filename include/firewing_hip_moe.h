@@ -367,6 +367,34 @@ bool firewing_hip_moe_sublayer(firewing_hip_context* ctx, size_t layer, const ui
 bool firewing_hip_moe_sublayer_dev(firewing_hip_context* ctx, size_t layer, const uint16_t* post_attention,
                                    size_t tokens, int order, uint16_t* layer_output, void* stream);
 
+/* ---- LM head (src/text_output.rs:204-317) ----------------------------- */
+
+/* Install the LM head [vocab][H] (host pointer) on the context, replacing any
+ * earlier head; the head of the reference model is 248,320 x 2560. */
+bool firewing_hip_install_lm_head(firewing_hip_context* ctx, const uint16_t* weight, size_t vocab);
+
+/* The seeded synthetic head (bf16(N(0, 0.02)), firewing_amd/csrc/fw_synth.h
+ * tensor 10), generated on the device. No counterpart in the reference. */
+bool firewing_hip_generate_lm_head(firewing_hip_context* ctx, size_t vocab, uint64_t seed);
+
+/* The head from a safetensors checkpoint: tensor `tensor` (e.g. "lm_head.weight"),
+ * BF16 [vocab, H], validated as firewing_hip_safetensors_layer_plan validates. */
+bool firewing_hip_load_lm_head_safetensors(firewing_hip_context* ctx, const char* path, const char* tensor,
+                                           size_t vocab);
+
+/* logits = linear_bf16(lm_head, hidden) for T <= 4 tokens (hidden [T, H], the
+ * final mixer's mixed output) and their top-k, k <= 64: ids [T, k] and values
+ * [T, k] in rank order (src/text_output.rs:273-287; the ranking of
+ * pytorch_topk_bf16, src/decoder_layer.rs:28-39, with ties broken by the lower
+ * index). logits [T, vocab] may be NULL. Host pointers, synchronous. */
+bool firewing_hip_lm_head(firewing_hip_context* ctx, const uint16_t* hidden, size_t tokens, size_t k,
+                          uint16_t* logits, size_t* ids, uint16_t* values);
+
+/* Device-pointer variant (hidden 4-byte aligned; ids int32), queued on
+ * `stream`; logits may be NULL. */
+bool firewing_hip_lm_head_dev(firewing_hip_context* ctx, const uint16_t* hidden, size_t tokens, size_t k,
+                              uint16_t* logits, int32_t* ids, uint16_t* values, void* stream);
+
 /* No counterpart in the reference: how a step of `tokens` (<= 4) tokens runs
  * on this context: the number of independent one-token chains it interleaves
  * by layer (= tokens where the fused one-token path applies at the context's

@@ -357,6 +357,25 @@ def test_reference_topk_shim_agrees_up_to_ties():
         assert np.array_equal(f[shim], f[ours])
 
 
+@pytest.mark.skipif(not fo.ref_topk_available(), reason="oracle/_ref not built (no reference mounted)")
+def test_reference_topk_shim_agrees_at_vocabulary_size():
+    # The LM head's top-20 over 248,320 logits (src/text_output.rs:275): the
+    # shim's partial_sort branch (k * 64 <= count). With no tie in the top 21
+    # its list is the value order; with ties the selected values still agree
+    # rank by rank.
+    rng = np.random.default_rng(12)
+    for trial in range(4):
+        vals = rng.standard_normal(248320).astype(np.float32) * (4.0 if trial % 2 else 0.5)
+        logits = bf16(vals)
+        shim = fo.ref_torch_topk_bf16(logits, 20)
+        ours = fo.topk_total_order(logits, 20)
+        f = fo.bf16_to_f32(logits)
+        top = np.sort(f)[::-1][:21]
+        if len(np.unique(top)) == 21:
+            assert list(shim) == list(ours)
+        assert np.array_equal(f[shim], f[ours])
+
+
 def test_route_rejects_nan_logits_in_model_order():
     # src/decoder_layer.rs:279-281
     H, E = 32, 16
