@@ -1,6 +1,7 @@
 // LM head: logits = linear_bf16(lm_head [V][H], x) in the reference's exact
 // order (src/text_output.rs:273-287, src/expert.rs:514-560) and their top-k in
-// the total order (value descending, index ascending). HBM-bound: the head is
+// the total order (value descending, index ascending; keys as fw_numerics.h
+// topk_key). HBM-bound: the head is
 // 1.27 GB at V = 248,320, H = 2560, read once per step.
 #pragma once
 
@@ -61,85 +62,112 @@ __global__ void __launch_bounds__(256, 2) k_lm_head(const uint16_t* __restrict__
     }
 }
 
-// Selection key of (logit, index): larger key = larger logit, then the smaller
-// index (total_order_key16 ranks -0.0 below +0.0 and NaNs outermost).
-__device__ __forceinline__ uint64_t lm_key(uint32_t bf16_bits, uint32_t index) {
-    return ((uint64_t)total_order_key16(bf16_bits) << 32) | (uint64_t)(0xffffffffu - index);
-}
+constexpr int kTopkChunk = 4096;  // logits per workgroup of the first pass (1,024 per wave)
 
-constexpr int kTopkChunk = 4096;         // logits per workgroup of the first pass
-constexpr int kTopkPerThread = kTopkChunk / 256;
-
-// Largest key over the workgroup (256 threads); every thread gets it.
-__device__ __forceinline__ uint64_t wg_max_key(uint64_t v, uint64_t* red) {
+// The k largest of the 32-bit keys a wave holds (MAXPER per lane, distinct,
+// 0 = none), in descending order to out[0..k) (lane 0 writes): each lane sorts
+// its keys, then every round the wave maximum of the lane heads is taken and
+// its lane pops it (the selection of wave_topk).
+template <int MAXPER>
+__device__ __forceinline__ void wave_top_keys(uint32_t (&keys)[MAXPER], int k, uint32_t* out) {
 #pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) {
-        const uint64_t o = (uint64_t)__shfl_xor((long long)v, off, kWave);
-        v = o > v ? o : v;
+    for (int pass = 0; pass < MAXPER; ++pass) {
+#pragma unroll
+        for (int m = pass & 1; m + 1 < MAXPER; m += 2) {
+            const uint32_t a = keys[m], b = keys[m + 1];
+            keys[m] = a > b ? a : b;
+            keys[m + 1] = a > b ? b : a;
+        }
     }
-    const int w = (int)threadIdx.x / kWave;
-    __syncthreads();
-    if (lane_id() == 0) red[w] = v;
-    __syncthreads();
-    uint64_t m = red[0];
+    for (int r = 0; r < k; ++r) {
+        const uint32_t best = wave_max_u32(keys[0]);
+        if (keys[0] == best) {
 #pragma unroll
-    for (int i = 1; i < 4; ++i) m = red[i] > m ? red[i] : m;
-    return m;
+            for (int m = 0; m + 1 < MAXPER; ++m) keys[m] = keys[m + 1];
+            keys[MAXPER - 1] = 0u;
+        }
+        if (lane_id() == 0) out[r] = best;
+    }
 }
 
 // First pass: workgroup c takes logits [c * kTopkChunk, ...) of token t
-// (blockIdx.y) and writes its k largest keys, in order, to
-// cand[t][c][0..k) (0 past the chunk's logits).
+// (blockIdx.y). Keys are topk_key(logit, index within the chunk): larger key =
+// larger logit, then the lower index. Each wave the k largest of its 1,024,
+// then wave 0 the k largest of the four lists, written in descending order as
+// their bf16 order keys (key16[t][c][r]) and chunk positions (pos[t][c][r]).
 __global__ void __launch_bounds__(256) k_lm_topk_chunks(const uint16_t* __restrict__ logits, int V, int k,
-                                                         uint64_t* __restrict__ cand) {
-    __shared__ uint64_t red[4];
+                                                         uint16_t* __restrict__ key16, uint16_t* __restrict__ pos) {
+    __shared__ uint32_t lists[4 * 64];
+    __shared__ uint32_t best[64];
     const int t = (int)blockIdx.y, c = (int)blockIdx.x;
     const int chunks = (int)gridDim.x;
-    uint64_t keys[kTopkPerThread];
+    const int w = (int)threadIdx.x / kWave, lane = lane_id();
+    uint32_t keys[16];
 #pragma unroll
-    for (int i = 0; i < kTopkPerThread; ++i) {
-        const int idx = c * kTopkChunk + i * 256 + (int)threadIdx.x;
-        keys[i] = idx < V ? lm_key(logits[(size_t)t * V + idx], (uint32_t)idx) : 0ull;
+    for (int i = 0; i < 16; ++i) {
+        const int local = w * 1024 + i * kWave + lane;
+        const int idx = c * kTopkChunk + local;
+        keys[i] = idx < V ? topk_key(logits[(size_t)t * V + idx], (uint32_t)local) : 0u;
     }
-    uint64_t* out = cand + ((size_t)t * chunks + c) * k;
-    for (int r = 0; r < k; ++r) {
-        uint64_t best = 0;
+    wave_top_keys<16>(keys, k, lists + w * 64);
+    wg_sync();
+    if (w == 0) {
+        uint32_t m[4];
 #pragma unroll
-        for (int i = 0; i < kTopkPerThread; ++i) best = keys[i] > best ? keys[i] : best;
-        const uint64_t m = wg_max_key(best, red);
-        // keys are distinct (they carry the index): exactly one thread holds m
-#pragma unroll
-        for (int i = 0; i < kTopkPerThread; ++i)
-            if (keys[i] == m) keys[i] = 0;
-        if (threadIdx.x == 0) out[r] = m;
+        for (int i = 0; i < 4; ++i) m[i] = lane < k ? lists[i * 64 + lane] : 0u;
+        wave_top_keys<4>(m, k, best);
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        if (lane < k) {
+            // a chunk with fewer than k logits pads its list with position 0xffff
+            const size_t at = ((size_t)t * chunks + c) * k + lane;
+            key16[at] = (uint16_t)(best[lane] >> 16);
+            pos[at] = best[lane] != 0u ? (uint16_t)topk_key_expert(best[lane]) : (uint16_t)0xffffu;
+        }
     }
 }
 
-// Second pass, one workgroup per token: the k largest of its n chunk
-// candidates, as ids and bf16 values in rank order (round r takes the largest
-// key below round r - 1's: the keys are distinct).
-__global__ void __launch_bounds__(256) k_lm_topk_merge(const uint64_t* __restrict__ cand, int n, int k,
+// Second pass, one workgroup per token: the k largest of the n = chunks * k
+// candidates. Candidate p (= c * k + r) gets the key key16 << 16 | (0xffff - p):
+// among equal values a lower p is a lower chunk, or the same chunk and a lower
+// rank, so a lower vocabulary index. Writes ids (c * kTopkChunk + position)
+// and bf16 values in rank order.
+__global__ void __launch_bounds__(256) k_lm_topk_merge(const uint16_t* __restrict__ key16,
+                                                        const uint16_t* __restrict__ pos, int n, int k,
                                                         int32_t* __restrict__ ids, uint16_t* __restrict__ values) {
-    __shared__ uint64_t red[4];
+    __shared__ uint32_t lists[4 * 64];
+    __shared__ uint32_t best[64];
+    constexpr int kPerLane = 32;  // n <= 4 * 64 * 32 = 8,192
     const int t = (int)blockIdx.x;
-    const uint64_t* c = cand + (size_t)t * n;
-    uint64_t prev = ~0ull;
-    for (int r = 0; r < k; ++r) {
-        uint64_t best = 0;
-        for (int i = (int)threadIdx.x; i < n; i += 256) {
-            const uint64_t v = c[i];
-            best = (v < prev && v > best) ? v : best;
-        }
-        const uint64_t m = wg_max_key(best, red);
-        if (threadIdx.x == 0) {
-            const uint32_t idx = 0xffffffffu - (uint32_t)m;
-            const uint32_t key16 = (uint32_t)(m >> 32);
+    const int w = (int)threadIdx.x / kWave, lane = lane_id();
+    const uint16_t* kk = key16 + (size_t)t * n;
+    uint32_t keys[kPerLane];
+#pragma unroll
+    for (int i = 0; i < kPerLane; ++i) {
+        const int p = (w * kPerLane + i) * kWave + lane;
+        const bool real = p < n && pos[(size_t)t * n + p] != 0xffffu;
+        keys[i] = real ? ((uint32_t)kk[p] << 16) | (0xffffu - (uint32_t)p) : 0u;
+    }
+    wave_top_keys<kPerLane>(keys, k, lists + w * 64);
+    wg_sync();
+    if (w == 0) {
+        uint32_t m[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) m[i] = lane < k ? lists[i * 64 + lane] : 0u;
+        wave_top_keys<4>(m, k, best);
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        if (lane < k) {
+            const uint32_t key = best[lane];
+            const int p = (int)topk_key_expert(key);
+            const uint32_t k16 = key >> 16;
             // the inverse of total_order_key16
-            const uint32_t bits = (key16 & 0x8000u) ? (key16 & 0x7fffu) : ((~key16) & 0xffffu);
-            ids[(size_t)t * k + r] = (int32_t)idx;
-            values[(size_t)t * k + r] = (uint16_t)bits;
+            const uint32_t bits = (k16 & 0x8000u) ? (k16 & 0x7fffu) : ((~k16) & 0xffffu);
+            ids[(size_t)t * k + lane] = (p / k) * kTopkChunk + (int)pos[(size_t)t * n + p];
+            values[(size_t)t * k + lane] = (uint16_t)bits;
         }
-        prev = m;
     }
 }
 

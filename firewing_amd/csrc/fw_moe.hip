@@ -372,7 +372,8 @@ struct firewing_hip_context {
         size_t vocab = 0;
         uint16_t* weight = nullptr;   // + kLineSharePad bytes
         uint16_t* logits = nullptr;   // [T][vocab]
-        uint64_t* cand = nullptr;     // [T][chunks][kMaxLmTopK]
+        uint16_t* cand_key = nullptr;  // [T][chunks][k]: the chunks' top keys (total-order bf16 keys)
+        uint16_t* cand_pos = nullptr;  // [T][chunks][k]: and their positions in the chunk
         int32_t* ids = nullptr;       // [T][kMaxLmTopK]
         uint16_t* values = nullptr;   // [T][kMaxLmTopK]
         int grid = 0;                 // workgroups of k_lm_head
@@ -1024,8 +1025,8 @@ void firewing_hip_destroy(firewing_hip_context* c) {
         if (b) (void)hipFree(b);
     for (void* b : c->hc.owned)
         if (b) (void)hipFree(b);
-    for (void* b : {(void*)c->lm.weight, (void*)c->lm.logits, (void*)c->lm.cand, (void*)c->lm.ids,
-                    (void*)c->lm.values})
+    for (void* b : {(void*)c->lm.weight, (void*)c->lm.logits, (void*)c->lm.cand_key, (void*)c->lm.cand_pos,
+                    (void*)c->lm.ids, (void*)c->lm.values})
         if (b) (void)hipFree(b);
     if (c->last) (void)hipEventDestroy(c->last);
     if (c->stream) (void)hipStreamDestroy(c->stream);
@@ -2221,14 +2222,16 @@ void lm_reserve(firewing_hip_context* c, size_t vocab) {
     auto& m = c->lm;
     if (m.vocab == vocab && m.weight) return;
     if (m.weight) check(hipEventSynchronize(c->last), "hipEventSynchronize");
-    for (void* b : {(void*)m.weight, (void*)m.logits, (void*)m.cand, (void*)m.ids, (void*)m.values})
+    for (void* b : {(void*)m.weight, (void*)m.logits, (void*)m.cand_key, (void*)m.cand_pos, (void*)m.ids,
+                    (void*)m.values})
         if (b) (void)hipFree(b);
     m = firewing_hip_context::LmHead{};
     const size_t H = c->shape.hidden, T = kMaxTokens;
     const size_t chunks = (vocab + kTopkChunk - 1) / kTopkChunk;
     m.weight = dalloc<uint16_t>(vocab * H + kLineSharePad / 2);
     m.logits = dalloc<uint16_t>(T * vocab);
-    m.cand = dalloc<uint64_t>(T * chunks * kMaxLmTopK);
+    m.cand_key = dalloc<uint16_t>(T * chunks * kMaxLmTopK);
+    m.cand_pos = dalloc<uint16_t>(T * chunks * kMaxLmTopK);
     m.ids = dalloc<int32_t>(T * kMaxLmTopK);
     m.values = dalloc<uint16_t>(T * kMaxLmTopK);
     m.vocab = vocab;
@@ -2278,9 +2281,11 @@ void queue_lm_head(firewing_hip_context* c, const uint16_t* x, int T, int k, uin
     void* args[] = {&w, &x, (void*)&V, (void*)&H, &out};
     check(hipLaunchKernel(fn, dim3((unsigned)m.grid), dim3(256), args, (size_t)T * H * 4, s), "k_lm_head launch");
     const int chunks = (V + kTopkChunk - 1) / kTopkChunk;
-    hipLaunchKernelGGL(k_lm_topk_chunks, dim3((unsigned)chunks, (unsigned)T), dim3(256), 0, s, out, V, k, m.cand);
+    hipLaunchKernelGGL(k_lm_topk_chunks, dim3((unsigned)chunks, (unsigned)T), dim3(256), 0, s, out, V, k, m.cand_key,
+                       m.cand_pos);
     check(hipGetLastError(), "k_lm_topk_chunks launch");
-    hipLaunchKernelGGL(k_lm_topk_merge, dim3((unsigned)T), dim3(256), 0, s, m.cand, chunks * k, k, ids, values);
+    hipLaunchKernelGGL(k_lm_topk_merge, dim3((unsigned)T), dim3(256), 0, s, m.cand_key, m.cand_pos, chunks * k, k, ids,
+                       values);
     check(hipGetLastError(), "k_lm_topk_merge launch");
 }
 
@@ -2347,6 +2352,8 @@ bool firewing_hip_lm_head_dev(firewing_hip_context* c, const uint16_t* hidden, s
         if (!c->lm.weight) return fail("lm_head: no LM head installed");
         if (tokens == 0 || tokens > (size_t)kMaxTokens) return fail("lm_head: tokens must be in [1, 4]");
         if (k == 0 || k > (size_t)kMaxLmTopK || k > c->lm.vocab) return fail("lm_head: k must be in [1, min(64, vocab)]");
+        if ((c->lm.vocab + kTopkChunk - 1) / kTopkChunk * k > 8192)
+            return fail("lm_head: ceil(vocab / 4096) * k must be <= 8192");
         if (!hidden || !ids || !values) return fail("lm_head: null pointer");
         Ordered ordered(c, stream);
         queue_lm_head(c, hidden, (int)tokens, (int)k, logits, ids, values, ordered.s);
@@ -2361,6 +2368,8 @@ bool firewing_hip_lm_head(firewing_hip_context* c, const uint16_t* hidden, size_
         if (!c->lm.weight) return fail("lm_head: no LM head installed");
         if (tokens == 0 || tokens > (size_t)kMaxTokens) return fail("lm_head: tokens must be in [1, 4]");
         if (k == 0 || k > (size_t)kMaxLmTopK || k > c->lm.vocab) return fail("lm_head: k must be in [1, min(64, vocab)]");
+        if ((c->lm.vocab + kTopkChunk - 1) / kTopkChunk * k > 8192)
+            return fail("lm_head: ceil(vocab / 4096) * k must be <= 8192");
         if (!hidden || !ids || !values) return fail("lm_head: null pointer");
         Ordered ordered(c, nullptr);
         hipStream_t s = ordered.s;

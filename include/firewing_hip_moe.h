@@ -386,7 +386,8 @@ bool firewing_hip_load_lm_head_safetensors(firewing_hip_context* ctx, const char
  * final mixer's mixed output) and their top-k, k <= 64: ids [T, k] and values
  * [T, k] in rank order (src/text_output.rs:273-287; the ranking of
  * pytorch_topk_bf16, src/decoder_layer.rs:28-39, with ties broken by the lower
- * index). logits [T, vocab] may be NULL. Host pointers, synchronous. */
+ * index; ceil(vocab / 4096) * k <= 8192). logits [T, vocab] may be NULL.
+ * Host pointers, synchronous. */
 bool firewing_hip_lm_head(firewing_hip_context* ctx, const uint16_t* hidden, size_t tokens, size_t k,
                           uint16_t* logits, size_t* ids, uint16_t* values);
 
