@@ -191,7 +191,7 @@ constexpr int kBRowStride = kMaxHidden / 2 + 16;
 constexpr int kFusedWords = kBRowsAt + 4 * kBRowStride > kDirectVectors * 16 * 16 * 2 ? kBRowsAt + 4 * kBRowStride
                                                                                        : kDirectVectors * 16 * 16 * 2;
 __host__ __device__ constexpr int stage_words(int NT, int MBI) {
-    return (NT == 1 && MBI <= 16) ? kFusedWords
+    return (NT == 1 && MBI <= 20) ? kFusedWords
            : NT * kMaxHidden > (kBatchMatrices * NT * MBI * 16 < 8192 ? kBatchMatrices * NT * MBI * 16 : 8192)
                ? NT * kMaxHidden
                : (kBatchMatrices * NT * MBI * 16 < 8192 ? kBatchMatrices * NT * MBI * 16 : 8192);
@@ -974,18 +974,33 @@ __device__ __forceinline__ bool stage_acts_direct(const DecodeParams& p, int li,
     (void)slot;
     const int I = p.I, Is = p.Is;
     const int stride = max(I, Is) / 2;
-    const int parts = stride / 128;  // 1 KB parts: 64 lanes x 16 bytes
     uint64_t* raw = reinterpret_cast<uint64_t*>(sh.xs);
     const int w = wave_id(), lane = lane_id();
     auto source = [&](int m) -> const uint64_t* {
         return m == 0 ? p.shared_act + (size_t)li * (Is / 2) : p.act + ((size_t)li * p.S + m - 1) * (I / 2);
     };
-    for (int c = w; c < (U + 1) * parts; c += kThreads / kWave) {
-        const int m = c / parts, h = c - m * parts;
-        if (h * 128 < (m == 0 ? Is / 2 : I / 2)) {
-            __builtin_amdgcn_global_load_lds(
-                reinterpret_cast<const void*>(source(m) + h * 128 + 2 * lane),
-                (__attribute__((address_space(3))) void*)(raw + (size_t)m * stride + h * 128), 16, 0, 0);
+    if ((I | Is) % 256 == 0) {
+        // whole 1 KB parts (64 lanes x 16 bytes); the staging is on the
+        // layer's critical path, so this loop is kept apart from the general one
+        const int parts = stride / 128;
+        for (int c = w; c < (U + 1) * parts; c += kThreads / kWave) {
+            const int m = c / parts, h = c - m * parts;
+            if (h * 128 < (m == 0 ? Is / 2 : I / 2)) {
+                __builtin_amdgcn_global_load_lds(
+                    reinterpret_cast<const void*>(source(m) + h * 128 + 2 * lane),
+                    (__attribute__((address_space(3))) void*)(raw + (size_t)m * stride + h * 128), 16, 0, 0);
+            }
+        }
+    } else {
+        // a partial last part: lanes past the vector's end stay idle
+        const int parts = (stride + 127) / 128;
+        for (int c = w; c < (U + 1) * parts; c += kThreads / kWave) {
+            const int m = c / parts, h = c - m * parts;
+            if (h * 128 + 2 * lane < (m == 0 ? Is / 2 : I / 2)) {
+                __builtin_amdgcn_global_load_lds(
+                    reinterpret_cast<const void*>(source(m) + h * 128 + 2 * lane),
+                    (__attribute__((address_space(3))) void*)(raw + (size_t)m * stride + h * 128), 16, 0, 0);
+            }
         }
     }
     __builtin_amdgcn_s_waitcnt(0);
@@ -995,39 +1010,46 @@ __device__ __forceinline__ bool stage_acts_direct(const DecodeParams& p, int li,
     FW_TRACE_MARK_IF(lane == 0 && w == 2, slot, 9);
     FW_TRACE_MARK_IF(lane == 0 && w == 3, slot, 3);
     wg_sync();
-    // Thread t's word of vector m is word t (a vector is at most 256 words).
-    // Words without the epoch are read again past the caches, every stale
-    // word of the thread in one pass, until all carry it.
+    // Thread t's words of vector m are words t and t + 256 (a vector is at
+    // most 320 words). Words without the epoch are read again past the caches,
+    // every stale word of the thread (per 256-word half) in one pass, until all
+    // carry it.
     bool ok = true;
     const int tid = threadIdx.x;
-    uint32_t stale = 0;
+    constexpr int kHalves = (MBI * 16 + kThreads - 1) / kThreads;
 #pragma unroll
-    for (int m = 0; m < kDirectVectors; ++m) {
-        if (m <= U && tid < (m == 0 ? Is / 2 : I / 2) && !has_tag(raw[(size_t)m * stride + tid], epoch))
-            stale |= 1u << m;
-    }
-    if (stale != 0) {
-        const uint64_t start = wall_clock64();
-        uint32_t polls = 0;
-        while (stale != 0) {
-            uint64_t v[kDirectVectors];
+    for (int half = 0; half < kHalves; ++half) {
+        if (kHalves > 1 && !ok) break;
+        const int wd = kHalves == 1 ? tid : tid + half * kThreads;
+        uint32_t stale = 0;
 #pragma unroll
-            for (int m = 0; m < kDirectVectors; ++m)
-                if (stale & (1u << m)) v[m] = coherent_load64(source(m) + tid);
+        for (int m = 0; m < kDirectVectors; ++m) {
+            if (m <= U && wd < (m == 0 ? Is / 2 : I / 2) && !has_tag(raw[(size_t)m * stride + wd], epoch))
+                stale |= 1u << m;
+        }
+        if (stale != 0) {
+            const uint64_t start = wall_clock64();
+            uint32_t polls = 0;
+            while (stale != 0) {
+                uint64_t v[kDirectVectors];
 #pragma unroll
-            for (int m = 0; m < kDirectVectors; ++m) {
-                if ((stale & (1u << m)) && has_tag(v[m], epoch)) {
-                    raw[(size_t)m * stride + tid] = v[m];
-                    stale &= ~(1u << m);
+                for (int m = 0; m < kDirectVectors; ++m)
+                    if (stale & (1u << m)) v[m] = coherent_load64(source(m) + wd);
+#pragma unroll
+                for (int m = 0; m < kDirectVectors; ++m) {
+                    if ((stale & (1u << m)) && has_tag(v[m], epoch)) {
+                        raw[(size_t)m * stride + wd] = v[m];
+                        stale &= ~(1u << m);
+                    }
                 }
-            }
-            if (stale == 0) break;
-            if (((++polls & 7) == 0 && coherent_load(p.error) != 0) || wall_clock64() - start > p.limit_ticks) {
-                int32_t expected = 0;
-                __hip_atomic_compare_exchange_strong(p.error, &expected, 1, __ATOMIC_RELAXED, __ATOMIC_RELAXED,
-                                                     __HIP_MEMORY_SCOPE_AGENT);
-                ok = false;
-                break;
+                if (stale == 0) break;
+                if (((++polls & 7) == 0 && coherent_load(p.error) != 0) || wall_clock64() - start > p.limit_ticks) {
+                    int32_t expected = 0;
+                    __hip_atomic_compare_exchange_strong(p.error, &expected, 1, __ATOMIC_RELAXED, __ATOMIC_RELAXED,
+                                                         __HIP_MEMORY_SCOPE_AGENT);
+                    ok = false;
+                    break;
+                }
             }
         }
     }
@@ -1198,10 +1220,10 @@ __device__ __forceinline__ bool combine_task(const DecodeParams& p, uint32_t epo
 }
 
 // Whether a variant carries the fused C task (one token; three down-row slots
-// per wave).
+// per wave of down rows up to 640 columns).
 __host__ __device__ constexpr bool fused_combine(int NT, int MBH, int MBI) {
     (void)MBH;
-    return NT == 1 && MBI <= 16;
+    return NT == 1 && MBI <= 20;
 }
 
 // C task j of layer li for one token when the gate/up pairs past the rows
@@ -1212,13 +1234,13 @@ __host__ __device__ constexpr bool fused_combine(int NT, int MBH, int MBI) {
 // expert for m = 0, slot m - 1 else; on wave m % 4, register slot m / 4). All
 // rows are requested as soon as the selection is known, so no C task waits
 // behind a B task of its workgroup.
-template <int NT, int MBH, int MBI, int TK, class SH>
+template <int NT, int MBH, int MBI, int TK, bool PAIRS, class SH>
 __device__ __forceinline__ bool combine_task_fused(const DecodeParams& p, uint32_t epoch, SH& sh, LdsState& st,
                                                    int li, int j) {
     static_assert(fused_combine(NT, MBH, MBI), "one token");
     static_assert(stage_words(NT, MBI) >= kBRowsAt + 4 * kBRowStride, "gate/up rows above the exponentials");
     static_assert(stage_words(NT, MBI) >= kDirectVectors * MBI * 16 * 2, "tagged words of the staged vectors");
-    static_assert(MBI * 16 <= kThreads, "one staged word per thread and vector");
+    static_assert(MBI * 16 <= 2 * kThreads, "at most two staged words per thread and vector");
     FW_TRACE_STAMP(t0);
     const int slot = trace_slot(p, li, p.n_router + p.n_shared + p.n_b + j);
     (void)slot;
@@ -1239,9 +1261,10 @@ __device__ __forceinline__ bool combine_task_fused(const DecodeParams& p, uint32
     const int rt = w * kWave + lane;
     const bool mixer = rt < kRowsPerCTask;
     const size_t at = ((size_t)r0 + (rt & ~1)) / 2;
-    // without pairs of its own (p.cpairs == 0: the rows role runs every B
-    // task) the task needs only its residual words, not the block input
-    const bool own_pairs = p.cpairs > 0;
+    // without pairs of its own (PAIRS false, p.cpairs == 0: the rows role
+    // runs every B task) the task needs only its residual words, not the
+    // block input
+    constexpr bool own_pairs = PAIRS;
     if (own_pairs && st.staged != li) {
         if (st.loaded != li) {
             if (!load_input<NT>(p, li, epoch, sh)) return false;
@@ -1462,7 +1485,10 @@ __device__ __forceinline__ void combine_role(const DecodeParams* __restrict__ P,
         bool ok;
         if constexpr (fused_combine(NT, MBH, MBI)) {
             // the host runs one-token steps it cannot fuse on the two-token kernel
-            ok = combine_task_fused<NT, MBH, MBI, TK>(p, epoch, sh, st, li, j);
+            // (two instantiations: a runtime flag inside would cost the
+            // common path its scheduling)
+            ok = p.cpairs > 0 ? combine_task_fused<NT, MBH, MBI, TK, true>(p, epoch, sh, st, li, j)
+                              : combine_task_fused<NT, MBH, MBI, TK, false>(p, epoch, sh, st, li, j);
         } else if (j < nb_comb) {
             ok = pairs_task<NT, MBH, TK>(p, epoch, sh, st, li, p.nb_rows + j, false);
         } else {
@@ -1511,6 +1537,13 @@ k_moe_decode(const DecodeParams* __restrict__ P, uint32_t epoch) {
     X(NT, 64, 32, 16)                 \
     X(NT, 80, 16, 16)                 \
     X(NT, 80, 32, 16)
+// One-token variants whose fused C task holds down rows of up to 640 columns
+// (the reference model's I = Is = 640).
+#define FW_DECODE_VARIANTS_ONE_TOKEN(X) \
+    X(1, 64, 20, 8)                     \
+    X(1, 80, 20, 8)                     \
+    X(1, 64, 20, 16)                    \
+    X(1, 80, 20, 16)
 #define FW_DECODE_VARIANTS(X)     \
     FW_DECODE_VARIANTS_FOR(X, 1)  \
     FW_DECODE_VARIANTS_FOR(X, 2)  \

@@ -10,5 +10,8 @@ namespace fw {
 #define FW_INSTANTIATE(NT, MBH, MBI, TK) \
     template __global__ void k_moe_decode<NT, MBH, MBI, TK>(const DecodeParams*, uint32_t);
 FW_DECODE_VARIANTS_FOR(FW_INSTANTIATE, FW_NT)
+#if FW_NT == 1
+FW_DECODE_VARIANTS_ONE_TOKEN(FW_INSTANTIATE)
+#endif
 #undef FW_INSTANTIATE
 }  // namespace fw

@@ -39,6 +39,7 @@ namespace fw {
 #define FW_EXTERN(NT, MBH, MBI, TK) \
     extern template __global__ void k_moe_decode<NT, MBH, MBI, TK>(const DecodeParams*, uint32_t);
 FW_DECODE_VARIANTS(FW_EXTERN)
+FW_DECODE_VARIANTS_ONE_TOKEN(FW_EXTERN)
 #undef FW_EXTERN
 }  // namespace fw
 
@@ -426,11 +427,19 @@ bool validate_shape(const firewing_hip_shape& s, std::string* why) {
 
 // Kernel variant for T tokens and the context's shape: hidden rows of up to
 // 64 blocks (H <= 2048) or 80 (H <= 2560); down rows of up to 16 blocks
-// (I, Is <= 512) or 32 (<= 1024); top-k over up to 512 experts or 1024.
+// (I, Is <= 512), 20 (<= 640, one token: the fused C task) or 32 (<= 1024);
+// top-k over up to 512 experts or 1024.
 const void* decode_kernel(const firewing_hip_context* c, int T) {
     const bool wide_h = c->shape.hidden > 2048;
-    const bool wide_i = std::max(c->shape.intermediate, c->shape.shared_intermediate) > 512;
+    const size_t max_i = std::max(c->shape.intermediate, c->shape.shared_intermediate);
+    const bool wide_i = max_i > 512;
     const bool wide_e = c->shape.experts > 512;
+    if (T == 1 && wide_i && max_i <= 640) {
+        if (wide_e) return wide_h ? reinterpret_cast<const void*>(&k_moe_decode<1, 80, 20, 16>)
+                                  : reinterpret_cast<const void*>(&k_moe_decode<1, 64, 20, 16>);
+        return wide_h ? reinterpret_cast<const void*>(&k_moe_decode<1, 80, 20, 8>)
+                      : reinterpret_cast<const void*>(&k_moe_decode<1, 64, 20, 8>);
+    }
 #define FW_DECODE_VARIANT(NT, TK)                                                                      \
     if (T == NT && wide_e == (TK == 16)) {                                                             \
         if (!wide_h && !wide_i) return reinterpret_cast<const void*>(&k_moe_decode<NT, 64, 16, TK>); \
@@ -462,23 +471,34 @@ int decode_grid(const firewing_hip_context* c, int T) {
 // over L layers: the tables for 2, 3, ... chains follow one another.
 size_t vlayers_offset(size_t L, int chains) { return L * (size_t)((chains - 2) * (chains + 1) / 2); }
 
-// Whether one-token work at this shape runs the fused C task: every C task of
-// a layer resident at once (one combine workgroup each), the B tasks past the
-// rows role's one per workgroup coming to exactly two gate/up pairs per C task,
-// and the lane layouts of the fused kernel (I, Is multiples of 256, H of 512).
-bool one_token_fused(const firewing_hip_context* c) {
+// How one-token work runs at this shape. The fused C task (the one-token
+// kernel variants with down rows of up to 640 columns, at most 11 staged
+// activation vectors) either carries two gate/up pairs itself (kFusedPairs:
+// every C task of a layer resident at once, one combine workgroup each; the
+// B tasks past the rows role's one per workgroup coming to exactly two pairs
+// per C task; I, Is multiples of 256 and H of 512 for its row copies) or
+// none (kFusedNoPairs: the rows role runs every B task; combine workgroups may
+// take several C tasks per layer). kUnfused: the multi-token kernel.
+enum OneTokenMode { kUnfused = 0, kFusedNoPairs = 1, kFusedPairs = 2 };
+
+OneTokenMode one_token_mode(const firewing_hip_context* c) {
     const firewing_hip_shape& sh = c->shape;
+    const size_t max_i = std::max(sh.intermediate, sh.shared_intermediate);
+    const int mbh = sh.hidden > 2048 ? 80 : 64;
+    const int mbi = max_i <= 512 ? 16 : (max_i <= 640 ? 20 : 32);
+    if (!fused_combine(1, mbh, mbi) || sh.top_k + 1 > (size_t)kDirectVectors) return kUnfused;
     const int n_c = (int)(sh.hidden / kRowsPerCTask);
     const int n_b = (int)(sh.top_k * (sh.intermediate / kPairsPerTask));
     const int grid = c->grid[1];
     const int g_comb = std::min(n_c, grid / 2);
     const int nb_rows = std::min(n_b, grid - g_comb);
-    const int mbh = sh.hidden > 2048 ? 80 : 64;
-    const int mbi = std::max(sh.intermediate, sh.shared_intermediate) > 512 ? 32 : 16;
-    return fused_combine(1, mbh, mbi) && g_comb == n_c && sh.top_k + 1 <= (size_t)kDirectVectors &&
-           sh.intermediate % 256 == 0 && sh.shared_intermediate % 256 == 0 && sh.hidden % 512 == 0 &&
-           (long)n_b * kPairsPerTask - (long)nb_rows * kPairsPerTask == 2L * n_c;
+    const bool pairs = g_comb == n_c && sh.intermediate % 256 == 0 && sh.shared_intermediate % 256 == 0 &&
+                       sh.hidden % 512 == 0 &&
+                       (long)n_b * kPairsPerTask - (long)nb_rows * kPairsPerTask == 2L * n_c;
+    return pairs ? kFusedPairs : kFusedNoPairs;
 }
+
+bool one_token_fused(const firewing_hip_context* c) { return one_token_mode(c) != kUnfused; }
 
 // Launch the persistent kernel over layers [first, first + n) for T tokens.
 // x_in holds the input of the first layer ([T][H] bf16, 4-byte aligned).
@@ -491,7 +511,8 @@ void launch_decode(firewing_hip_context* c, size_t first, size_t n, int T, int o
                    bool prenorm, bool bias_feature, const uint16_t* x_in, uint16_t* x_final,
                    hipStream_t s) {
     const firewing_hip_shape& sh = c->shape;
-    const bool fused = one_token_fused(c);
+    const OneTokenMode mode = one_token_mode(c);
+    const bool fused = mode != kUnfused;
     const int chains = (T >= 2 && fused) ? T : 1;
     DecodeParams p{};
     p.layers = c->d_layers + first;
@@ -565,12 +586,13 @@ void launch_decode(firewing_hip_context* c, size_t first, size_t n, int T, int o
         roles(1);
         if (!fused) {
             kt = 2;
-        } else if (chains == 1) {
+        } else if (chains == 1 && mode == kFusedPairs) {
             p.cpairs = 2;
         } else {
-            // interleaved chains: a combine workgroup runs the chains' C tasks
-            // one after another, so they carry no pairs; the rows role, with
-            // time to spare between a chain's layers, runs every B task
+            // no pairs on the C tasks: with interleaved chains a combine
+            // workgroup runs the chains' C tasks one after another (pairs
+            // there would lengthen every chain), and without the exact split
+            // there are none to carry; the rows role runs every B task
             p.nb_rows = p.n_b;
         }
     }
