@@ -982,13 +982,24 @@ __device__ __forceinline__ bool stage_acts_direct(const DecodeParams& p, int li,
     if ((I | Is) % 256 == 0) {
         // whole 1 KB parts (64 lanes x 16 bytes); the staging is on the
         // layer's critical path, so this loop is kept apart from the general one
+        // part c = m * parts + h of the vectors' parts, walked by the waves in
+        // turn with (m, h) stepped by subtraction (no division on the path)
         const int parts = stride / 128;
-        for (int c = w; c < (U + 1) * parts; c += kThreads / kWave) {
-            const int m = c / parts, h = c - m * parts;
+        int m = 0, h = w;
+        while (h >= parts) {
+            h -= parts;
+            ++m;
+        }
+        for (; m <= U;) {
             if (h * 128 < (m == 0 ? Is / 2 : I / 2)) {
                 __builtin_amdgcn_global_load_lds(
                     reinterpret_cast<const void*>(source(m) + h * 128 + 2 * lane),
                     (__attribute__((address_space(3))) void*)(raw + (size_t)m * stride + h * 128), 16, 0, 0);
+            }
+            h += kThreads / kWave;
+            while (h >= parts) {
+                h -= parts;
+                ++m;
             }
         }
     } else {
