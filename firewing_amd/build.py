@@ -57,7 +57,8 @@ def build(verbose: bool = False) -> Path:
     include = ["-I", str(ROOT / "include"), "-I", str(CSRC)]
     compile_flags = [f for f in HIPCC_FLAGS if f != "-shared"]
     units = [(CSRC / "fw_moe.hip", [], out_dir / "fw_moe.o"),
-             (CSRC / "fw_safetensors.cpp", [], out_dir / "fw_safetensors.o")]
+             (CSRC / "fw_safetensors.cpp", [], out_dir / "fw_safetensors.o"),
+             (CSRC / "fw_zstd.hip", [], out_dir / "fw_zstd.o")]
     for nt in (1, 2, 3, 4):
         units.append((CSRC / "fw_decode_kernels.hip", [f"-DFW_NT={nt}"], out_dir / f"fw_decode_t{nt}.o"))
     jobs = [[hipcc(), *compile_flags, *include, *defs, "-c", str(src), "-o", str(obj)] for src, defs, obj in units]

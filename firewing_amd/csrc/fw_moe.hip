@@ -27,6 +27,7 @@
 #include "fw_device.h"
 #include "fw_hyper.h"
 #include "fw_lm_head.h"
+#include "fw_zstd_host.h"
 #include "fw_numerics.h"
 #include "fw_prefill.h"
 #include "fw_safetensors.h"
@@ -2405,5 +2406,150 @@ bool firewing_hip_lm_head(firewing_hip_context* c, const uint16_t* hidden, size_
         check(hipStreamSynchronize(s), "hipStreamSynchronize");
         for (size_t i = 0; i < hid.size(); ++i) ids[i] = (size_t)hid[i];
         return true;
+    });
+}
+
+// ---- compressed expert container: GPU zstd decoding ----
+
+struct firewing_hip_zstd_decoder {
+    fw::zs::Decoder dec;
+    firewing_hip_zstd_decoder(int device, size_t frames, size_t content) : dec(device, frames, content) {}
+};
+
+namespace {
+
+const char* zstd_status_name(uint32_t s) {
+    static const char* names[] = {"ok",
+                                  "not a zstd frame",
+                                  "unsupported or malformed frame header",
+                                  "truncated frame",
+                                  "malformed block",
+                                  "too many blocks",
+                                  "malformed literals section",
+                                  "malformed Huffman table or stream",
+                                  "malformed FSE table",
+                                  "malformed sequences",
+                                  "offset beyond the decoded bytes",
+                                  "decoded size differs from the expected size",
+                                  "scratch exceeded",
+                                  "bytes after the frame"};
+    return s < sizeof(names) / sizeof(names[0]) ? names[s] : "unknown failure";
+}
+
+// the first failed frame of a finished call, as an error; true if none failed
+bool zstd_report(fw::zs::Decoder& d, uint32_t* status, size_t n) {
+    std::vector<uint32_t> st, blk;
+    d.statuses(&st, &blk);
+    if (status) std::copy(st.begin(), st.begin() + std::min(n, st.size()), status);
+    for (size_t i = 0; i < st.size(); ++i)
+        if (st[i] != 0)
+            return fail("zstd frame " + std::to_string(i) + ": " + zstd_status_name(st[i]) + " (block " +
+                        std::to_string(blk[i]) + ")");
+    return true;
+}
+
+bool zstd_jobs(const uint8_t* src, size_t src_bytes, const firewing_hip_zstd_frame* frames, size_t n,
+               bool unshuffle, std::vector<fw::zs::FrameJob>* jobs) {
+    jobs->resize(n);
+    for (size_t i = 0; i < n; ++i) {
+        const auto& f = frames[i];
+        if (f.src_offset > src_bytes || f.src_bytes > src_bytes - f.src_offset)
+            return fail("zstd_decode: frame " + std::to_string(i) + " lies outside the source buffer");
+        (*jobs)[i] = fw::zs::FrameJob{src + f.src_offset, f.src_bytes, f.content_bytes,
+                                      static_cast<uint8_t*>(f.dst), static_cast<uint8_t*>(f.dst_tail),
+                                      f.split, unshuffle};
+    }
+    return true;
+}
+
+}  // namespace
+
+firewing_hip_zstd_decoder* firewing_hip_zstd_create(int device, size_t max_frames, size_t max_content_bytes) {
+    firewing_hip_zstd_decoder* d = nullptr;
+    guarded([&] {
+        d = new firewing_hip_zstd_decoder(device, max_frames, max_content_bytes);
+        return true;
+    });
+    return d;
+}
+
+void firewing_hip_zstd_destroy(firewing_hip_zstd_decoder* d) { delete d; }
+
+bool firewing_hip_zstd_decode_dev(firewing_hip_zstd_decoder* d, const uint8_t* src, size_t src_bytes,
+                                  const firewing_hip_zstd_frame* frames, size_t n, bool bf16_unshuffle,
+                                  void* stream) {
+    return guarded([&] {
+        if (!d) return fail("zstd_decode: null decoder");
+        if (n && (!src || !frames)) return fail("zstd_decode: null pointer");
+        std::vector<fw::zs::FrameJob> jobs;
+        if (!zstd_jobs(src, src_bytes, frames, n, bf16_unshuffle, &jobs)) return false;
+        std::string why;
+        if (!d->dec.queue(jobs, static_cast<hipStream_t>(stream), &why)) return fail(why);
+        return true;
+    });
+}
+
+bool firewing_hip_zstd_decode(firewing_hip_zstd_decoder* d, const uint8_t* src, size_t src_bytes,
+                              const firewing_hip_zstd_frame* frames, size_t n, bool bf16_unshuffle,
+                              uint32_t* status) {
+    return guarded([&] {
+        if (!d) return fail("zstd_decode: null decoder");
+        if (n && (!src || !frames)) return fail("zstd_decode: null pointer");
+        check(hipSetDevice(d->dec.device()), "hipSetDevice");
+        uint8_t* pin = d->dec.pinned(std::max<size_t>(src_bytes, 1));
+        uint8_t* dev = d->dec.device_source(std::max<size_t>(src_bytes, 1));
+        std::vector<fw::zs::FrameJob> jobs;
+        if (!zstd_jobs(dev, src_bytes, frames, n, bf16_unshuffle, &jobs)) return false;
+        check(hipEventSynchronize(d->dec.last()), "hipEventSynchronize");  // the staging is free
+        std::memcpy(pin, src, src_bytes);
+        hipStream_t s = nullptr;
+        check(hipMemcpyAsync(dev, pin, src_bytes, hipMemcpyHostToDevice, s), "hipMemcpyAsync");
+        std::string why;
+        if (!d->dec.queue(jobs, s, &why)) return fail(why);
+        return zstd_report(d->dec, status, n);
+    });
+}
+
+bool firewing_hip_zstd_status(firewing_hip_zstd_decoder* d, uint32_t* status, size_t n) {
+    return guarded([&] {
+        if (!d) return fail("zstd_status: null decoder");
+        return zstd_report(d->dec, status, n);
+    });
+}
+
+bool firewing_hip_install_experts_zstd(firewing_hip_context* c, firewing_hip_zstd_decoder* d, size_t layer,
+                                       const uint32_t* experts, size_t n, const uint8_t* src, size_t src_bytes,
+                                       const uint64_t* offsets, const uint64_t* sizes) {
+    return guarded([&] {
+        if (!c || !d) return fail("install_experts_zstd: null context or decoder");
+        if (layer >= c->shape.layers) return fail("install_experts_zstd: layer out of range");
+        if (n && (!experts || !src || !offsets || !sizes)) return fail("install_experts_zstd: null pointer");
+        const size_t H = c->shape.hidden, I = c->shape.intermediate, E = c->shape.experts;
+        const uint64_t content = 6ull * I * H;
+        if (content > d->dec.max_content()) return fail("install_experts_zstd: the decoder's max_content is below 6*I*H");
+        std::vector<firewing_hip_zstd_frame> frames(n);
+        for (size_t i = 0; i < n; ++i) {
+            if (experts[i] >= E) return fail("install_experts_zstd: expert id out of range");
+            for (size_t j = 0; j < i; ++j)
+                if (experts[j] == experts[i]) return fail("install_experts_zstd: repeated expert id");
+            frames[i] = firewing_hip_zstd_frame{offsets[i], sizes[i], content,
+                                                c->gate_up[layer] + (size_t)experts[i] * 2 * I * H,
+                                                c->down[layer] + (size_t)experts[i] * H * I, 4ull * I * H};
+        }
+        check(hipSetDevice(d->dec.device()), "hipSetDevice");
+        if (d->dec.device() != c->device) return fail("install_experts_zstd: decoder and context on different GPUs");
+        uint8_t* pin = d->dec.pinned(std::max<size_t>(src_bytes, 1));
+        uint8_t* dev = d->dec.device_source(std::max<size_t>(src_bytes, 1));
+        std::vector<fw::zs::FrameJob> jobs;
+        if (!zstd_jobs(dev, src_bytes, frames.data(), n, true, &jobs)) return false;
+        check(hipEventSynchronize(d->dec.last()), "hipEventSynchronize");
+        std::memcpy(pin, src, src_bytes);
+        {
+            Ordered ordered(c, nullptr);
+            check(hipMemcpyAsync(dev, pin, src_bytes, hipMemcpyHostToDevice, ordered.s), "hipMemcpyAsync");
+            std::string why;
+            if (!d->dec.queue(jobs, ordered.s, &why)) return fail(why);
+        }
+        return zstd_report(d->dec, nullptr, n);
     });
 }

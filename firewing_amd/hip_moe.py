@@ -91,6 +91,16 @@ class SublayerCaptures(ctypes.Structure):
                 ("mlp_injection_products", ctypes.c_void_p)]
 
 
+class ZstdFrame(ctypes.Structure):
+    _fields_ = [("src_offset", ctypes.c_uint64), ("src_bytes", ctypes.c_uint64), ("content_bytes", ctypes.c_uint64),
+                ("dst", ctypes.c_void_p), ("dst_tail", ctypes.c_void_p), ("split", ctypes.c_uint64)]
+
+
+ZSTD_STATUS = ["ok", "bad magic", "bad frame header", "truncated", "bad block", "too many blocks",
+               "bad literals", "bad huffman", "bad fse", "bad sequences", "bad offset", "content size",
+               "scratch", "trailing bytes"]
+
+
 _u16p = ctypes.POINTER(ctypes.c_uint16)
 _szp = ctypes.POINTER(ctypes.c_size_t)
 _vp = ctypes.c_void_p
@@ -148,6 +158,14 @@ _SIGNATURES = {
     "firewing_hip_expf_host": (None, [ctypes.POINTER(ctypes.c_float), ctypes.POINTER(ctypes.c_float), _sz]),
     "firewing_hip_expf_device": (_b, [ctypes.POINTER(ctypes.c_float), ctypes.POINTER(ctypes.c_float), _sz]),
     "firewing_hip_copy_bytes": (_b, [_vp, _vp, _sz, _vp]),
+    "firewing_hip_zstd_create": (_vp, [ctypes.c_int, _sz, _sz]),
+    "firewing_hip_zstd_destroy": (None, [_vp]),
+    "firewing_hip_zstd_decode": (_b, [_vp, _vp, _sz, ctypes.POINTER(ZstdFrame), _sz, _b,
+                                      ctypes.POINTER(ctypes.c_uint32)]),
+    "firewing_hip_zstd_decode_dev": (_b, [_vp, _vp, _sz, ctypes.POINTER(ZstdFrame), _sz, _b, _vp]),
+    "firewing_hip_zstd_status": (_b, [_vp, ctypes.POINTER(ctypes.c_uint32), _sz]),
+    "firewing_hip_install_experts_zstd": (_b, [_vp, _vp, _sz, ctypes.POINTER(ctypes.c_uint32), _sz, _vp, _sz,
+                                               ctypes.POINTER(ctypes.c_uint64), ctypes.POINTER(ctypes.c_uint64)]),
 }
 
 _lib = None
@@ -622,9 +640,89 @@ class MoeContext:
     def synchronize(self) -> None:
         _call("firewing_hip_synchronize", self._h)
 
+    def install_experts_zstd(self, decoder: "ZstdDecoder", layer: int, experts, container: bytes,
+                             offsets, sizes) -> None:
+        """Decode container frames (host bytes) into experts' resident rows
+        (src/compressed_overlap.rs:1541-1553 decode + unshuffle + install)."""
+        ex = np.ascontiguousarray(experts, dtype=np.uint32)
+        off = np.ascontiguousarray(offsets, dtype=np.uint64)
+        sz = np.ascontiguousarray(sizes, dtype=np.uint64)
+        src = np.frombuffer(container, dtype=np.uint8) if len(container) else np.zeros(1, np.uint8)
+        _call("firewing_hip_install_experts_zstd", self._h, decoder._h, layer,
+              ex.ctypes.data_as(ctypes.POINTER(ctypes.c_uint32)), len(ex), src.ctypes.data, len(container),
+              off.ctypes.data_as(ctypes.POINTER(ctypes.c_uint64)), sz.ctypes.data_as(ctypes.POINTER(ctypes.c_uint64)))
+
     def set_wait_timeout(self, seconds: float) -> None:
         """Time limit of each dependency wait inside the persistent kernel."""
         _call("firewing_hip_set_wait_timeout", self._h, float(seconds))
+
+
+class ZstdDecoder:
+    """GPU decoder of independent zstd frames (the compressed expert container,
+    src/compressed_overlap.rs), with scratch for `max_frames` frames in flight
+    of at most `max_content` decoded bytes each."""
+
+    def __init__(self, max_frames: int, max_content: int, device: int = 0):
+        h = lib().firewing_hip_zstd_create(device, max_frames, max_content)
+        if not h:
+            raise _err()
+        self._h = ctypes.c_void_p(h)
+        self.max_frames, self.max_content = max_frames, max_content
+
+    def close(self) -> None:
+        if self._h:
+            lib().firewing_hip_zstd_destroy(self._h)
+            self._h = ctypes.c_void_p()
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    @staticmethod
+    def _frames(specs) -> ctypes.Array:
+        arr = (ZstdFrame * max(1, len(specs)))()
+        for i, (off, size, content, dst, dst_tail, split) in enumerate(specs):
+            arr[i] = ZstdFrame(off, size, content, dst, dst_tail, split)
+        return arr
+
+    def decode(self, src: bytes, specs, unshuffle: bool) -> np.ndarray:
+        """Host-source decode; specs = [(src_offset, src_bytes, content_bytes,
+        dst_ptr, dst_tail_ptr, split)]. Returns per-frame statuses; raises if
+        any frame failed (statuses are in the exception's `statuses`)."""
+        frames = self._frames(specs)
+        st = np.zeros(max(1, len(specs)), dtype=np.uint32)
+        buf = np.frombuffer(src, dtype=np.uint8) if len(src) else np.zeros(1, np.uint8)
+        ok = lib().firewing_hip_zstd_decode(self._h, buf.ctypes.data, len(src), frames, len(specs), unshuffle,
+                                            st.ctypes.data_as(ctypes.POINTER(ctypes.c_uint32)))
+        if not ok:
+            e = _err()
+            e.statuses = st[:len(specs)]
+            raise e
+        return st[:len(specs)]
+
+    def decode_dev(self, src_ptr: int, src_bytes: int, specs, unshuffle: bool, stream=None) -> None:
+        """Device-source decode queued on `stream` (asynchronous)."""
+        frames = self._frames(specs)
+        _call("firewing_hip_zstd_decode_dev", self._h, src_ptr, src_bytes, frames, len(specs), unshuffle,
+              _addr(stream))
+
+    def status(self, n: int) -> np.ndarray:
+        """Wait for the last call; its per-frame statuses (raises if any failed)."""
+        st = np.zeros(max(1, n), dtype=np.uint32)
+        ok = lib().firewing_hip_zstd_status(self._h, st.ctypes.data_as(ctypes.POINTER(ctypes.c_uint32)), n)
+        if not ok:
+            e = _err()
+            e.statuses = st[:n]
+            raise e
+        return st[:n]
 
 
 def header_symbols() -> list[str]:

@@ -42,7 +42,8 @@ def build(verbose: bool = False) -> Path:
     include = ["-I", str(hip_build.ROOT / "include"), "-I", str(hip_build.CSRC)]
     flags = [f for f in hip_build.HIPCC_FLAGS if f != "-shared"] + ["-DFW_DECODE_TRACE"]
     units = [(hip_build.CSRC / "fw_moe.hip", [], TRACE_DIR / "fw_moe.o"),
-             (hip_build.CSRC / "fw_safetensors.cpp", [], TRACE_DIR / "fw_safetensors.o")]
+             (hip_build.CSRC / "fw_safetensors.cpp", [], TRACE_DIR / "fw_safetensors.o"),
+             (hip_build.CSRC / "fw_zstd.hip", [], TRACE_DIR / "fw_zstd.o")]
     for nt in (1, 2, 3, 4):
         units.append((hip_build.CSRC / "fw_decode_kernels.hip", [f"-DFW_NT={nt}"], TRACE_DIR / f"t{nt}.o"))
     jobs = [[hip_build.hipcc(), *flags, *include, *d, "-c", str(src), "-o", str(obj)] for src, d, obj in units]

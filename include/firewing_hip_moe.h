@@ -404,6 +404,102 @@ bool firewing_hip_lm_head_dev(firewing_hip_context* ctx, const uint16_t* hidden,
  * same either way. 0 for a null context. */
 size_t firewing_hip_token_chains(const firewing_hip_context* ctx, size_t tokens);
 
+/* ---- compressed expert container (src/compressed_overlap.rs) ----
+ *
+ * The container holds one independent zstd frame (RFC 8878; the reference
+ * decodes with the zstd crate 0.13.3 = libzstd 1.5.7) per expert: the
+ * expert's source bytes, gate_up [2I, H] then down [H, I] (bf16, 6*I*H bytes;
+ * tools/build_sequential_shuffle_container.py), BF16 byte-shuffled (every low
+ * byte, then every high byte). The reference reads a frame, decompresses it
+ * into a buffer, checks the decoded size against EXPERT_BYTES, undoes the
+ * shuffle and copies it into the install buffer
+ * (src/compressed_overlap.rs:1426-1560 run_executable_trial,
+ * src/compressed_overlap.rs:1385-1395 unshuffle_bf16). Here the frames are
+ * decoded on the GPU straight into their destinations with the shuffle
+ * undone on the way.
+ *
+ * Supported: frames of at most 2^27 - 1 decoded bytes with or without a
+ * content-size field, raw / RLE / compressed blocks, every literal and
+ * sequence table mode. Not supported (the frame fails): dictionaries,
+ * skippable frames, bytes after the frame, more than content/1024 + 64
+ * blocks. A content checksum is skipped, not verified (the container's
+ * frames carry none). */
+typedef struct firewing_hip_zstd_decoder firewing_hip_zstd_decoder;
+
+/* One frame of a decode call. Decoded bytes [0, split) go to dst and
+ * [split, content_bytes) to dst_tail (device pointers; dst_tail may be NULL
+ * when split == content_bytes). With the BF16 unshuffle the bytes are those
+ * after the shuffle is undone. */
+typedef struct firewing_hip_zstd_frame {
+    uint64_t src_offset;    /* the frame's first byte in the call's source buffer */
+    uint64_t src_bytes;     /* its compressed size: exactly one frame */
+    uint64_t content_bytes; /* the decoded size the caller expects (the reference's EXPERT_BYTES check) */
+    void* dst;
+    void* dst_tail;
+    uint64_t split;
+} firewing_hip_zstd_frame;
+
+/* Per-frame status codes (firewing_hip_zstd_decode's status array). */
+enum firewing_hip_zstd_status {
+    FIREWING_HIP_ZSTD_OK = 0,
+    FIREWING_HIP_ZSTD_BAD_MAGIC = 1,
+    FIREWING_HIP_ZSTD_BAD_FRAME_HEADER = 2,
+    FIREWING_HIP_ZSTD_TRUNCATED = 3,
+    FIREWING_HIP_ZSTD_BAD_BLOCK = 4,
+    FIREWING_HIP_ZSTD_TOO_MANY_BLOCKS = 5,
+    FIREWING_HIP_ZSTD_BAD_LITERALS = 6,
+    FIREWING_HIP_ZSTD_BAD_HUFFMAN = 7,
+    FIREWING_HIP_ZSTD_BAD_FSE = 8,
+    FIREWING_HIP_ZSTD_BAD_SEQUENCES = 9,
+    FIREWING_HIP_ZSTD_BAD_OFFSET = 10,
+    FIREWING_HIP_ZSTD_CONTENT_SIZE = 11,
+    FIREWING_HIP_ZSTD_SCRATCH = 12,
+    FIREWING_HIP_ZSTD_TRAILING = 13
+};
+
+/* A decoder on GPU `device` with scratch for `max_frames` frames in flight of
+ * at most `max_content_bytes` decoded bytes each (about 4 bytes of scratch
+ * per decoded byte: 9.8 MB experts take ~40 MB a frame). Calls with more
+ * frames run in chunks of max_frames. Decoders are independent of
+ * contexts: one can decode on its own stream while a context's step runs on
+ * another. NULL on failure (see firewing_hip_last_error). No counterpart in
+ * the reference, whose workers each own a zstd::bulk::Decompressor
+ * (src/compressed_overlap.rs:1494-1505). */
+firewing_hip_zstd_decoder* firewing_hip_zstd_create(int device, size_t max_frames, size_t max_content_bytes);
+void firewing_hip_zstd_destroy(firewing_hip_zstd_decoder* dec);
+
+/* Decode `n` frames whose bytes are in host memory `src` [src_bytes] (staged
+ * through pinned memory) into device destinations; synchronous. status [n]
+ * (may be NULL) receives each frame's firewing_hip_zstd_status. Returns false
+ * if any frame failed (the message names the first) or on a usage error.
+ * Replaces decompress_to_buffer + the decoded-size check + unshuffle_bf16
+ * (src/compressed_overlap.rs:1541-1553) for a batch of frames. */
+bool firewing_hip_zstd_decode(firewing_hip_zstd_decoder* dec, const uint8_t* src, size_t src_bytes,
+                              const firewing_hip_zstd_frame* frames, size_t n, bool bf16_unshuffle,
+                              uint32_t* status);
+
+/* Device-source variant: `src` is a device buffer; queued on `stream` (NULL =
+ * the null stream) after the decoder's previous call, asynchronous. Per-frame
+ * statuses are read with firewing_hip_zstd_status. The decoder reads no byte
+ * outside the frames. */
+bool firewing_hip_zstd_decode_dev(firewing_hip_zstd_decoder* dec, const uint8_t* src, size_t src_bytes,
+                                  const firewing_hip_zstd_frame* frames, size_t n, bool bf16_unshuffle,
+                                  void* stream);
+
+/* Wait for the decoder's last call and copy its per-frame statuses (status
+ * [n], n = that call's frame count; may be NULL). False if any frame failed. */
+bool firewing_hip_zstd_status(firewing_hip_zstd_decoder* dec, uint32_t* status, size_t n);
+
+/* Install `n` experts of `layer` from their container frames: frame i (host
+ * bytes src[offsets[i], offsets[i] + sizes[i])) decodes, unshuffled, into
+ * expert experts[i]'s resident gate_up and down rows. Synchronous, ordered
+ * with the context's other work. The install step of the overlap benches
+ * (src/compressed_overlap.rs:1547-1553 unshuffle_bf16 + install copy) into
+ * the banks a step reads (ExactResidentTop10Runner, src/metal_moe.rs:404-470). */
+bool firewing_hip_install_experts_zstd(firewing_hip_context* ctx, firewing_hip_zstd_decoder* dec, size_t layer,
+                                       const uint32_t* experts, size_t n, const uint8_t* src, size_t src_bytes,
+                                       const uint64_t* offsets, const uint64_t* sizes);
+
 /* Seeded synthetic hidden vectors of the benchmark workload (host memory):
  * bf16(N(0,1)) RMS-normalised, x[H-1] = 1.0 when bias_feature (the constant
  * feature that carries the Zipf router bias). No counterpart in the reference,
