@@ -35,6 +35,7 @@ Progress goes to stderr.
 from __future__ import annotations
 
 import argparse
+import ctypes
 import json
 import os
 import sys
@@ -240,6 +241,145 @@ def bench_real_shape(rt, hm, args) -> dict:
             "resident_gb": round(L * (layer_bytes(REAL_SHAPE, REAL_SHAPE["experts"])) / 1e9, 1)}
 
 
+ZSTD_BATCH = dict(frames=256, distinct=16, level=1)
+
+
+def zstd_frames(seed: int, distinct: int):
+    """Real-shape expert frames as the reference's container builder writes
+    them (source = gate_up [1280, 2560] + down [2560, 640] bf16 N(0, 0.02),
+    BF16-shuffled, zstd level 1); returns (sources, frames)."""
+    from firewing_amd import container as fc
+    H, I = REAL_SHAPE["hidden"], REAL_SHAPE["intermediate"]
+    rng = np.random.default_rng(seed)
+    sources, frames = [], []
+    for _ in range(distinct):
+        w = (rng.standard_normal(3 * I * H) * 0.02).astype(np.float32)
+        b = (w.view(np.uint32) >> 16).astype(np.uint16)
+        src = fc.expert_source(b[:2 * I * H], b[2 * I * H:])
+        sources.append(src)
+        frames.append(fc.compress_frame(fc.shuffle_bf16(src), ZSTD_BATCH["level"]))
+    return sources, frames
+
+
+def bench_zstd(rt, hm, args, step=None) -> dict:
+    """GPU decoding of the compressed expert container: a batch of 256
+    real-shape expert frames (9,830,400 source bytes each; 16 distinct frames,
+    each used 16 times), device-resident, decoded and unshuffled into 256
+    expert slots per call, HIP events around each call. With `step` = (ctx, x,
+    resid), the decode also runs beside the 48-layer step on a second stream,
+    the shape of the overlap benches (storage decode beside execute_exact,
+    src/compressed_overlap.rs:1866-1880)."""
+    H, I = REAL_SHAPE["hidden"], REAL_SHAPE["intermediate"]
+    EB = 6 * I * H
+    n, distinct = ZSTD_BATCH["frames"], ZSTD_BATCH["distinct"]
+    sources, frames = zstd_frames(args.seed, distinct)
+    batch = [frames[i % distinct] for i in range(n)]
+    offs = np.cumsum([0] + [len(f) for f in batch])[:-1]
+    blob = np.frombuffer(b"".join(batch), dtype=np.uint8).copy()
+    comp = int(blob.size)
+    src = rt.DeviceArray.from_numpy(blob)
+    dst = rt.DeviceArray((n * EB,), np.uint8)
+    specs = [(int(o), len(f), EB, dst.ptr + i * EB, None, EB) for i, (o, f) in enumerate(zip(offs, batch))]
+    dec = hm.ZstdDecoder(n, EB)
+    stream = rt.Stream()
+    res = {"frames": n, "distinct_frames": distinct, "source_bytes_per_frame": EB, "level": ZSTD_BATCH["level"],
+           "compressed_bytes": comp, "ratio": round(comp / (n * EB), 4)}
+    try:
+        for _ in range(2):
+            dec.decode_dev(src.ptr, comp, specs, True, stream.handle)
+        dec.status(n)
+        out = dst.numpy()
+        for i in (0, n // 2 + 1, n - 1):
+            assert out[i * EB:(i + 1) * EB].tobytes() == sources[i % distinct], f"frame {i} decoded wrong"
+        steps = max(5, args.steps // 5)
+        ev = [rt.Event() for _ in range(steps + 1)]
+        ev[0].record(stream)
+        for i in range(steps):
+            dec.decode_dev(src.ptr, comp, specs, True, stream.handle)
+            ev[i + 1].record(stream)
+        stream.synchronize()
+        dec.status(n)
+        per = [1000.0 * ev[i].elapsed_ms(ev[i + 1]) for i in range(steps)]
+        for e in ev:
+            e.destroy()
+        us = float(np.median(per))
+        res.update({"us_per_batch": round(us, 1), "batch_us": quantiles(per),
+                    "decoded_gbps": round(n * EB / (us * 1e-6) / 1e9, 1),
+                    "compressed_gbps": round(comp / (us * 1e-6) / 1e9, 1),
+                    "us_per_frame": round(us / n, 2)})
+        log(f"zstd container: {n} expert frames ({comp / 1e6:.0f} MB -> {n * EB / 1e6:.0f} MB) in {us:.0f} us, "
+            f"{res['decoded_gbps']:.0f} GB/s decoded")
+        if step is not None:
+            ctx, x, resid = step
+            sA = rt.Stream()
+            reps = 5
+            pairs = []
+            for _ in range(reps):
+                e0, ea, eb = rt.Event(), rt.Event(), rt.Event()
+                e0.record(sA)
+                rt.check(rt.hip().hipStreamWaitEvent(ctypes.c_void_p(stream.handle), ctypes.c_void_p(e0.handle), 0),
+                         "hipStreamWaitEvent")
+                ctx.moe_step_dev(x.ptr, 1, resid.ptr, stream=sA.handle)
+                ea.record(sA)
+                dec.decode_dev(src.ptr, comp, specs, True, stream.handle)
+                eb.record(stream)
+                sA.synchronize()
+                stream.synchronize()
+                pairs.append((1000.0 * e0.elapsed_ms(ea), 1000.0 * e0.elapsed_ms(eb)))
+                for e in (e0, ea, eb):
+                    e.destroy()
+            dec.status(n)
+            ctx.synchronize()
+            step_alone_tot, step_per = time_steps(rt, ctx, x, resid, 1, 10, 2)
+            step_alone = float(np.median([1000.0 * v for v in step_per]))
+            step_with = float(np.median([p[0] for p in pairs]))
+            wall = float(np.median([max(p) for p in pairs]))
+            res["beside_step"] = {"step_us_alone": round(step_alone, 1), "decode_us_alone": round(us, 1),
+                                  "step_us_beside_decode": round(step_with, 1), "wall_us": round(wall, 1),
+                                  "serial_us": round(step_alone + us, 1)}
+            log(f"zstd beside the step: wall {wall:.0f} us vs serial {step_alone + us:.0f} us "
+                f"(step {step_alone:.0f} alone, {step_with:.0f} beside the decode)")
+            sA.destroy()
+    finally:
+        stream.destroy()
+        dec.close()
+        src.free()
+        dst.free()
+    return res
+
+
+def cpu_zstd_baseline(threads_n: int, seed: int) -> dict:
+    """The reference's CPU work per expert frame on the host cores: libzstd
+    decompress + unshuffle (src/compressed_overlap.rs:1541-1553), 1 thread
+    over 4 frames and threads_n threads over 4 frames each, 1 warm-up."""
+    from concurrent.futures import ThreadPoolExecutor
+    from oracle import fw_zstd as fz
+    sources, frames = zstd_frames(seed, 4)
+    EB = len(sources[0])
+
+    def one(i):
+        out = fz.unshuffle_bf16(fz.decompress(frames[i % 4], EB))
+        return len(out)
+
+    one(0)
+    res = {"sample": "4 distinct real-shape expert frames (9,830,400 source bytes, level 1), "
+                     "libzstd decompress + numpy unshuffle per frame", "libzstd": fz.version()}
+    for threads in (1, threads_n):
+        count = 4 * threads
+        t0 = time.perf_counter()
+        if threads == 1:
+            for i in range(count):
+                one(i)
+        else:
+            with ThreadPoolExecutor(threads) as pool:
+                list(pool.map(one, range(count)))
+        dt = time.perf_counter() - t0
+        res[f"{threads}_thread"] = {"frames": count, "decoded_gbps": round(count * EB / dt / 1e9, 2),
+                                    "us_per_frame": round(dt * 1e6 / count, 1)}
+        log(f"CPU zstd decode + unshuffle, {threads} thread(s): {count * EB / dt / 1e9:.2f} GB/s")
+    return res
+
+
 LM_HEAD = dict(hidden=2560, vocab=248320, k=20)
 
 
@@ -344,6 +484,9 @@ def main() -> int:
     ap.add_argument("--no-prefill", action="store_true")
     ap.add_argument("--no-real-shape", action="store_true")
     ap.add_argument("--no-lm-head", action="store_true")
+    ap.add_argument("--no-zstd", action="store_true")
+    ap.add_argument("--zstd-only", action="store_true",
+                    help="time the compressed-container decode alone (for kernel traces)")
     ap.add_argument("--prefill-only", action="store_true",
                     help="time the 8K-token prefill block alone (for kernel traces)")
     ap.add_argument("--copy-calibration", action="store_true",
@@ -357,6 +500,10 @@ def main() -> int:
 
     from firewing_amd import hip_moe as hm
     from firewing_amd import hip_runtime as rt
+
+    if args.zstd_only:
+        print(json.dumps({"compressed_container": bench_zstd(rt, hm, args)}), flush=True)
+        return 0
 
     if args.prefill_only:
         ctx = hm.MoeContext(layers=1, **SHAPE)
@@ -467,6 +614,9 @@ def main() -> int:
     if not args.no_prefill:
         result["prefill"] = bench_prefill(rt, hm, ctx, args)
 
+    if not args.no_zstd:
+        result["compressed_container"] = bench_zstd(rt, hm, args, step=(ctx, x, resid))
+
     ctx.close()
     x.free()
     resid.free()
@@ -485,6 +635,8 @@ def main() -> int:
         threads_n = max(1, min(16, os.cpu_count() or 1))
         log(f"CPU baseline: the oracle's block, 1 and {threads_n} threads")
         result["cpu_baseline"] = cpu_baseline(args, x_host, threads_n)
+        if not args.no_zstd:
+            result["cpu_baseline"]["compressed_container"] = cpu_zstd_baseline(threads_n, args.seed)
         # the oracle's chained step for the same token: bit-identical residual
         from oracle import fw_oracle as fo
         cpu_resid = fo.synth_step(SHAPE, args.seed, L, x_host, threads=threads_n)[0]

@@ -5,17 +5,23 @@
 //   k_zs_reset      clears the chunk's work-list counters (a kernel, not a
 //                   memset, so a captured graph replays it correctly);
 //   k_zs_index      one thread per frame: headers, block list, work lists;
-//   k_zs_literals   one wave per Huffman literal section;
-//   k_zs_sequences  one wave per block with sequences;
-//   k_zs_execute    one 512-thread workgroup per frame, blocks in order, each
-//                   block's output built in LDS (a block regenerates at most
-//                   128 KB) and then written to the frame's output scratch;
+//   k_zs_literals   one workgroup per Huffman literal section, a wave per
+//                   stream, every lane decoding a segment of it;
+//   k_zs_sequences  eight blocks with sequences per wave, a lane each;
+//   k_zs_layout     one thread per frame: block output positions and starting
+//                   repeat-offset histories;
+//   k_zs_raw        one workgroup per raw or RLE block: its bytes in place;
+//   k_zs_execute    one 512-thread workgroup per frame, its compressed blocks
+//                   in order, each block's output built in LDS (a block
+//                   regenerates at most 128 KB) and then written to the
+//                   frame's output scratch;
 //   k_zs_finish     output scratch -> destination, undoing the BF16 byte
 //                   shuffle and splitting at `split`.
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
 #include <stdexcept>
+#include <type_traits>
 
 #include "fw_zstd.h"
 #include "fw_zstd_host.h"
@@ -53,16 +59,35 @@ struct Launch {
     uint64_t seq_cap;
     uint8_t* out;  // [count][out_cap]
     uint64_t out_cap;
-    Work* huf_work;  // [count * max_blocks]
+    Work* huf_work;  // [count * max_blocks] each
     Work* seq_work;
-    uint32_t* counters;  // [0] Huffman work, [1] sequence work
+    Work* raw_work;      // raw and RLE blocks
+    uint32_t* counters;  // [0] Huffman work, [1] sequence work, [2] raw/RLE work
 };
 
 constexpr int kExecThreads = 512;
 constexpr int kChunk = 1024;  // sequences per execute round set (2 per thread)
 
 __global__ void k_zs_reset(uint32_t* counters) {
-    if (threadIdx.x < 2) counters[threadIdx.x] = 0;
+    if (threadIdx.x < 3) counters[threadIdx.x] = 0;
+}
+
+// A byte of global memory (a global, not flat, load).
+__device__ __forceinline__ uint8_t load_byte(const uint8_t* a) {
+    return *(const __attribute__((address_space(1))) uint8_t*)(a);
+}
+
+// The 4 bytes at q (any alignment) as a little-endian word: two aligned words
+// when those lie inside [ok_lo, ok_hi), else byte by byte.
+__device__ __forceinline__ uint32_t load4(const uint8_t* q, const uint8_t* ok_lo, const uint8_t* ok_hi) {
+    const uint8_t* a = reinterpret_cast<const uint8_t*>(reinterpret_cast<uintptr_t>(q) & ~uintptr_t(3));
+    const int sh = 8 * (int)(q - a);
+    if (a >= ok_lo && a + 8 <= ok_hi) {
+        const uint64_t x = (uint64_t)load_word(a) | ((uint64_t)load_word(a + 4) << 32);
+        return (uint32_t)(x >> sh);
+    }
+    return (uint32_t)load_byte(q) | ((uint32_t)load_byte(q + 1) << 8) | ((uint32_t)load_byte(q + 2) << 16) |
+           ((uint32_t)load_byte(q + 3) << 24);
 }
 
 __global__ void __launch_bounds__(64) k_zs_index(Launch L) {
@@ -78,13 +103,16 @@ __global__ void __launch_bounds__(64) k_zs_index(Launch L) {
     F.err_block = info.err_block;
     F.nblocks = st == kOk ? info.nblocks : 0;
     if (st != kOk) return;
-    uint32_t nh = 0, ns = 0;
+    uint32_t nh = 0, ns = 0, nr = 0;
     for (uint32_t b = 0; b < info.nblocks; ++b) {
         Block& B = bl[b];
         B.rep_end[0] = rep_entry(0);
         B.rep_end[1] = rep_entry(1);
         B.rep_end[2] = rep_entry(2);
-        if (B.type != 2) continue;
+        if (B.type != 2) {
+            nr += B.regen > 0;
+            continue;
+        }
         nh += B.lit_type == 2;
         if (B.nseq) {
             ++ns;
@@ -94,41 +122,224 @@ __global__ void __launch_bounds__(64) k_zs_index(Launch L) {
         }
     }
     uint32_t hb = nh ? atomicAdd(&L.counters[0], nh) : 0, sb = ns ? atomicAdd(&L.counters[1], ns) : 0;
+    uint32_t rb = nr ? atomicAdd(&L.counters[2], nr) : 0;
     for (uint32_t b = 0; b < info.nblocks; ++b) {
         const Block& B = bl[b];
-        if (B.type != 2) continue;
+        if (B.type != 2) {
+            if (B.regen) L.raw_work[rb++] = Work{f, b};
+            continue;
+        }
         if (B.lit_type == 2) L.huf_work[hb++] = Work{f, b};
         if (B.nseq) L.seq_work[sb++] = Work{f, b};
     }
 }
 
-// One wave per Huffman literal section: lane 0 builds the decoding table in
-// LDS, lanes 0..streams-1 decode one stream each into the literal scratch.
-__global__ void __launch_bounds__(64) k_zs_literals(Launch L) {
+constexpr uint32_t kLitStage = 32 * 1024;  // LDS copy of a block's Huffman streams (larger: read in place)
+
+// Copy bytes [g, g + n) of the frame into LDS at lds + phase (phase = g's
+// address mod 4, so words stay aligned): aligned words inside the frame
+// [ok_lo, ok_hi) as words, the frame's edge words byte by byte. Returns the
+// bytes' LDS address. All `threads` threads of the workgroup take part.
+__device__ const uint8_t* stage_bytes(uint8_t* lds, const uint8_t* g, uint32_t n, const uint8_t* ok_lo,
+                                      const uint8_t* ok_hi, int threads) {
+    const uint8_t* a0 = reinterpret_cast<const uint8_t*>(reinterpret_cast<uintptr_t>(g) & ~uintptr_t(3));
+    const uint32_t phase = (uint32_t)(g - a0);
+    const uint32_t words = (phase + n + 3) / 4;
+    uint32_t* dst = reinterpret_cast<uint32_t*>(lds);
+    for (uint32_t w = threadIdx.x; w < words; w += threads) {
+        const uint8_t* a = a0 + 4 * w;
+        uint32_t v;
+        if (a >= ok_lo && a + 4 <= ok_hi) {
+            v = load_word(a);
+        } else {
+            v = 0;
+            for (int k = 0; k < 4; ++k)
+                if (a + k >= ok_lo && a + k < ok_hi) v |= (uint32_t)load_byte(a + k) << (8 * k);
+        }
+        dst[w] = v;
+    }
+    return lds + phase;
+}
+
+// 8 bytes of an LDS buffer at q as a little-endian word (three aligned word
+// reads; the buffer is padded so they stay inside it).
+__device__ __forceinline__ uint64_t lds_load8(const uint8_t* q) {
+    typedef const __attribute__((address_space(3))) uint32_t* lp;
+    const uint8_t* a = reinterpret_cast<const uint8_t*>(reinterpret_cast<uintptr_t>(q) & ~uintptr_t(3));
+    const uint32_t w0 = *(lp)(a), w1 = *(lp)(a + 4), w2 = *(lp)(a + 8);
+    const uint32_t sh = 8u * (uint32_t)(q - a);
+    const uint64_t x = (uint64_t)w0 | ((uint64_t)w1 << 32);
+    return sh ? (x >> sh) | ((uint64_t)w2 << (64 - sh)) : x;
+}
+
+// Backward bit reader over a stream staged in LDS (at most 128 KB, so bit
+// positions fit 32 bits). refill() leaves at least 57 bits in the word (or
+// the stream's start), and reads between refills take no checks; a read past
+// the stream's start (a malformed stream) returns garbage, never touches
+// memory outside the buffer, and drives pos negative.
+struct LdsBits {
+    const uint8_t* p;
+    int32_t pos, lo;
+    uint64_t c;
+    __device__ __forceinline__ void load() {
+        int32_t b = ((pos + 7) >> 3) - 8;
+        b = b < 0 ? 0 : b;
+        lo = 8 * b;
+        c = lds_load8(p + b);
+    }
+    __device__ __forceinline__ void seek(int32_t at) {
+        pos = at;
+        load();
+    }
+    __device__ __forceinline__ void refill() {
+        if (pos - lo < 57 && lo > 0) load();
+    }
+    // nb <= 32 bits below pos (zeros below the stream's start)
+    __device__ __forceinline__ uint32_t peek(int nb) const {
+        const int32_t sh = pos - lo - nb;
+        const uint64_t v = sh >= 0 ? (c >> (sh & 63)) : (c << ((-sh) & 63));
+        return (uint32_t)v & (uint32_t)((1ull << nb) - 1);
+    }
+    __device__ __forceinline__ uint32_t read(int nb) {
+        const uint32_t v = peek(nb);
+        pos -= nb;
+        return v;
+    }
+};
+
+// One stream of `count` Huffman symbols decoded by a whole wave: lane l
+// starts at bit pos0 - l*S (S = pos0/64 rounded up) as if a codeword began
+// there and decodes until it passes its segment's end. A prefix code
+// resynchronises within a few codewords, so once lane l-1's true end is
+// known, lane l redoes its segment from there only if its guess differed,
+// and the fix travels up the lanes until nothing changes. Counts then give
+// each lane's output offset and a last pass writes the symbols.
+template <class Mem>
+__device__ bool huf_stream_wave(const uint8_t* s, uint32_t size, const uint8_t* ok_lo, const uint8_t* ok_hi,
+                                const uint16_t* dt, int log, uint32_t count, uint8_t* out) {
+    const int lane = (int)(threadIdx.x & 63);
+    if (size == 0) return false;
+    const uint32_t lastb = s[size - 1];
+    if (lastb == 0) return false;
+    const int64_t pos0 = 8 * (int64_t)(size - 1) + highbit32(lastb);
+    const int64_t S = (pos0 + 63) / 64;
+    int64_t stop = pos0 - (int64_t)(lane + 1) * S;
+    if (stop < 0) stop = 0;
+    int64_t p = pos0 - (int64_t)lane * S;
+    if (p < 0) p = 0;
+    BackBitsT<Mem> r;
+    r.p = s;
+    r.n = size;
+    r.ok_lo = ok_lo;
+    r.ok_hi = ok_hi;
+    auto run = [&](int64_t from, uint8_t* dst, uint32_t& cnt, int64_t& end) -> bool {
+        cnt = 0;
+        end = from;
+        if (from <= stop) return true;
+        if constexpr (std::is_same<Mem, LdsMem>::value) {
+            // up to 4 codewords (4 x 12 bits) per refill
+            LdsBits q{s, (int32_t)from, 0, 0};
+            q.load();
+            const int32_t st = (int32_t)stop;
+            while (q.pos > st) {
+                q.refill();
+#pragma unroll
+                for (int u = 0; u < 4; ++u) {
+                    if (q.pos <= st) break;
+                    if (cnt >= count) return false;
+                    const uint16_t e = dt[q.peek(log)];
+                    if (dst) dst[cnt] = (uint8_t)e;
+                    q.pos -= e >> 8;
+                    ++cnt;
+                }
+            }
+            end = q.pos;
+            return true;
+        } else {
+            r.seek(from);
+            while (r.pos > stop) {
+                if (cnt >= count) return false;
+                const uint16_t e = dt[r.peek(log)];
+                if (dst) dst[cnt] = (uint8_t)e;
+                r.skip(e >> 8);
+                ++cnt;
+            }
+            end = r.pos;
+            return true;
+        }
+    };
+    uint32_t c = 0;
+    int64_t e = 0;
+    bool ok = run(p, nullptr, c, e);
+    bool synced = false;
+    for (int it = 0; it <= 64; ++it) {
+        const uint32_t lo = __shfl_up((uint32_t)e, 1), hi = __shfl_up((uint32_t)((uint64_t)e >> 32), 1);
+        const int64_t t = lane == 0 ? pos0 : (int64_t)(((uint64_t)hi << 32) | lo);
+        const bool redo = t != p;
+        if (!__any(redo)) {
+            synced = true;
+            break;
+        }
+        if (redo) {
+            p = t;
+            ok = run(p, nullptr, c, e);
+        }
+    }
+    // exclusive prefix of the counts
+    uint32_t x = c;
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) {
+        const uint32_t y = __shfl_up(x, d);
+        if (lane >= d) x += y;
+    }
+    const uint32_t total = __shfl(x, 63);
+    const uint32_t base = x - c;
+    const int64_t last_end_lo = (int64_t)__shfl((uint32_t)e, 63);
+    const bool good = synced && total == count && last_end_lo == 0 && !__any(!ok);
+    if (!good) return false;
+    uint32_t c2;
+    int64_t e2;
+    run(p, out + base, c2, e2);
+    return true;
+}
+
+// One workgroup per Huffman literal section: thread 0 builds the decoding
+// table in LDS, the streams are copied into LDS when they fit, and wave k
+// decodes stream k.
+__global__ void __launch_bounds__(256) k_zs_literals(Launch L) {
     __shared__ uint16_t dt[1 << kMaxHufBits];
     __shared__ uint8_t wt[256];
     __shared__ FseEntry ft[64];
     __shared__ int16_t norm[256];
     __shared__ uint16_t next[256];
+    __shared__ __attribute__((aligned(16))) uint8_t stage[kLitStage + 16];
     __shared__ int s_log;
-    const int lane = (int)threadIdx.x;
+    __shared__ uint32_t s_bad;
+    const int wave = (int)(threadIdx.x >> 6);
     const uint32_t total = L.counters[0];
     for (uint32_t w = blockIdx.x; w < total; w += gridDim.x) {
         const Work wk = L.huf_work[w];
         const DevFrame& F = L.frames[wk.frame];
         Block& B = L.blocks[(size_t)wk.frame * L.max_blocks + wk.block];
-        if (lane == 0) {
+        const uint8_t* ok_lo = F.src;
+        const uint8_t* ok_hi = F.src + F.size;
+        const uint32_t s0 = B.stream_off[0];
+        const uint32_t span = B.stream_off[B.nstreams - 1] + B.stream_size[B.nstreams - 1] - s0;
+        const bool staged = span + 8 <= kLitStage;
+        const uint8_t* sbase = staged ? stage_bytes(stage, F.src + s0, span, ok_lo, ok_hi, 256) : F.src + s0;
+        if (threadIdx.x == 0) {
+            s_bad = 0;
             int log = 0;
             const int nsym = huf_weights(F.src + B.huf_desc, (uint32_t)(F.size - B.huf_desc), wt, &log, ft, norm,
-                                         next);
+                                         next, ok_lo, ok_hi);
             if (nsym) {
                 uint32_t start[kMaxHufBits + 2];
                 huf_rank_starts(wt, nsym, start);
-                for (int s = 0; s < nsym; ++s) {
-                    const int wgt = wt[s];
+                for (int sy = 0; sy < nsym; ++sy) {
+                    const int wgt = wt[sy];
                     if (!wgt) continue;
                     const uint32_t len = (1u << wgt) >> 1;
-                    const uint16_t e = huf_entry(s, wgt, log);
+                    const uint16_t e = huf_entry(sy, wgt, log);
                     for (uint32_t i = 0; i < len; ++i) dt[start[wgt] + i] = e;
                     start[wgt] += len;
                 }
@@ -138,48 +349,293 @@ __global__ void __launch_bounds__(64) k_zs_literals(Launch L) {
         __syncthreads();
         const int log = s_log;
         if (log < 0) {
-            if (lane == 0) B.status = kErrHuffman;
-        } else if (lane < (int)B.nstreams) {
+            if (threadIdx.x == 0) B.status = kErrHuffman;
+        } else if (wave < (int)B.nstreams) {
             const uint32_t seg = B.nstreams == 1 ? B.lit_size : (B.lit_size + 3) / 4;
-            const uint32_t cnt = lane == 3 ? B.lit_size - 3 * seg : seg;
-            uint8_t* o = L.lit + (size_t)wk.frame * L.lit_cap + B.lit_out + (size_t)lane * seg;
-            const bool ok = huf_stream(F.src + B.stream_off[lane], B.stream_size[lane], dt, log, cnt,
-                                       [&](uint32_t i, uint8_t v) { o[i] = v; });
-            if (!ok) B.status = kErrHuffman;
+            const uint32_t cnt = wave == 3 ? B.lit_size - 3 * seg : seg;
+            uint8_t* o = L.lit + (size_t)wk.frame * L.lit_cap + B.lit_out + (size_t)wave * seg;
+            const uint32_t off = B.stream_off[wave] - s0;
+            bool ok;
+            if (staged)
+                ok = huf_stream_wave<LdsMem>(sbase + off, B.stream_size[wave], stage, stage + kLitStage + 16, dt,
+                                             log, cnt, o);
+            else
+                ok = huf_stream_wave<GlobalMem>(sbase + off, B.stream_size[wave], ok_lo, ok_hi, dt, log, cnt, o);
+            if (!ok && (threadIdx.x & 63) == 0) s_bad = 1;
+        }
+        __syncthreads();
+        if (threadIdx.x == 0 && s_bad) B.status = kErrHuffman;
+    }
+}
+
+// Backward bit reader over a frame in global memory, the LdsBits contract
+// (refill() leaves at least 57 bits or reaches the stream's start; reads
+// between refills take no checks): three aligned words per refill when they
+// lie inside the frame [ok_lo, ok_hi), else bytes of the stream.
+struct GlobalBits {
+    const uint8_t* p;
+    const uint8_t* ok_lo;
+    const uint8_t* ok_hi;
+    uint32_t n;
+    int32_t pos, lo;
+    uint64_t c;
+    __device__ __forceinline__ void load() {
+        int32_t b = ((pos + 7) >> 3) - 8;
+        b = b < 0 ? 0 : b;
+        lo = 8 * b;
+        c = ::fw::zs::load8(p + b, n - b, ok_lo, ok_hi);
+    }
+    __device__ __forceinline__ void refill() {
+        if (pos - lo < 57 && lo > 0) load();
+    }
+    __device__ __forceinline__ uint32_t peek(int nb) const {
+        const int32_t sh = pos - lo - nb;
+        const uint64_t v = sh >= 0 ? (c >> (sh & 63)) : (c << ((-sh) & 63));
+        return (uint32_t)v & (uint32_t)((1ull << nb) - 1);
+    }
+    __device__ __forceinline__ uint32_t read(int nb) {
+        const uint32_t v = peek(nb);
+        pos -= nb;
+        return v;
+    }
+};
+
+constexpr int kSeqLanes = 8;     // blocks per wave in the sequence pass
+constexpr int kSeqFlush = 64;    // records per lane staged in LDS between flushes
+constexpr int kSeqTable = 1280;  // LL [0, 512), OF [512, 768), ML [768, 1280)
+
+// kSeqLanes blocks per wave, one lane each: the lane builds its block's
+// LL/OF/ML tables in LDS and decodes its sequences from the frame in global
+// memory, two refills per sequence (offset + match-length extra bits <= 47,
+// literal-length extra bits + the three state updates <= 42); every
+// kSeqFlush sequences the whole wave writes the staged records out.
+__global__ void __launch_bounds__(64) k_zs_sequences(Launch L) {
+    __shared__ FseEntry tabs[kSeqLanes][kSeqTable];
+    __shared__ int16_t norms[kSeqLanes][64];
+    __shared__ uint16_t nexts[kSeqLanes][64];
+    __shared__ uint64_t recs[kSeqLanes][kSeqFlush];
+    __shared__ uint32_t llcode[36], mlcode[53];  // value | extra bits << 24
+    __shared__ uint32_t s_n[kSeqLanes], s_i[kSeqLanes];
+    __shared__ uint64_t* s_out[kSeqLanes];
+    __shared__ uint32_t s_active;
+    const int lane = (int)threadIdx.x;
+    if (lane < 36) llcode[lane] = kLLBase[lane] | ((uint32_t)kLLBits[lane] << 24);
+    if (lane < 53) mlcode[lane] = kMLBase[lane] | ((uint32_t)kMLBits[lane] << 24);
+    __syncthreads();
+    const uint32_t total = L.counters[1];
+    for (uint32_t w0 = blockIdx.x * kSeqLanes; w0 < total; w0 += gridDim.x * kSeqLanes) {
+        const uint32_t w = w0 + (uint32_t)lane;
+        const bool mine = lane < kSeqLanes && w < total;
+        Block* Bp = nullptr;
+        const DevFrame* Fp = nullptr;
+        uint64_t* out = nullptr;
+        uint32_t st = kOk, nseq = 0, i = 0;
+        GlobalBits r{};
+        int lg[3] = {0, 0, 0};
+        uint32_t sll = 0, sof = 0, sml = 0, rep[3] = {0, 0, 0};
+        uint64_t tll = 0, tml = 0;
+        FseEntry* tl = tabs[lane < kSeqLanes ? lane : 0];
+        if (mine) {
+            const Work wk = L.seq_work[w];
+            Fp = &L.frames[wk.frame];
+            Bp = &L.blocks[(size_t)wk.frame * L.max_blocks + wk.block];
+            const Block& B = *Bp;
+            const uint8_t* f = Fp->src;
+            out = L.seq + (size_t)wk.frame * L.seq_cap + B.seq_out;
+            nseq = B.nseq;
+            const uint32_t end = B.src + B.size;
+            const int off3[3] = {0, 512, 768};
+            for (int k = 0; k < 3 && st == kOk; ++k) {
+                lg[k] = table_for(f, end, B.table[k], k, tl + off3[k], norms[lane], nexts[lane]);
+                if (lg[k] < 0) st = kErrFse;
+            }
+            rep[0] = rep_entry(0);
+            rep[1] = rep_entry(1);
+            rep[2] = rep_entry(2);
+            if (st == kOk) {
+                r.p = f + B.seq_src;
+                r.n = B.seq_size;
+                r.ok_lo = f;
+                r.ok_hi = f + end;
+                const uint32_t lastb = B.seq_size ? f[B.seq_src + B.seq_size - 1] : 0u;
+                if (lastb == 0) {
+                    st = kErrSequences;
+                } else {
+                    r.pos = 8 * (int32_t)(B.seq_size - 1) + highbit32(lastb);
+                    r.load();
+                    sll = r.read(lg[0]);
+                    sof = r.read(lg[1]);
+                    sml = r.read(lg[2]);
+                }
+            }
+        }
+        for (;;) {
+            uint32_t k = 0;
+            if (mine && st == kOk) {
+                const FseEntry* tll_ = tl;
+                const FseEntry* tof_ = tl + 512;
+                const FseEntry* tml_ = tl + 768;
+                for (; k < (uint32_t)kSeqFlush && i < nseq; ++k) {
+                    const FseEntry ell = tll_[sll], eof = tof_[sof], eml = tml_[sml];
+                    const uint32_t mc = mlcode[eml.sym < 53 ? eml.sym : 0], lc = llcode[ell.sym < 36 ? ell.sym : 0];
+                    if (eof.sym > 31 || eml.sym > 52 || ell.sym > 35) {
+                        st = kErrSequences;
+                        break;
+                    }
+                    r.refill();
+                    const uint64_t ov = (1ull << eof.sym) + r.read(eof.sym);
+                    const uint32_t ml = (mc & 0xffffff) + r.read(mc >> 24);
+                    r.refill();
+                    const uint32_t ll = (lc & 0xffffff) + r.read(lc >> 24);
+                    uint32_t off;
+                    if (ov > 3) {
+                        if (ov - 3 >= (1ull << 27)) {
+                            st = kErrOffset;
+                            break;
+                        }
+                        off = (uint32_t)(ov - 3);
+                        rep[2] = rep[1];
+                        rep[1] = rep[0];
+                        rep[0] = off;
+                    } else {
+                        const int idx = (int)ov - 1 + (ll == 0);
+                        if (idx == 0) {
+                            off = rep[0];
+                        } else if (idx == 1) {
+                            off = rep[1];
+                            rep[1] = rep[0];
+                            rep[0] = off;
+                        } else if (idx == 2) {
+                            off = rep[2];
+                            rep[2] = rep[1];
+                            rep[1] = rep[0];
+                            rep[0] = off;
+                        } else {
+                            if (!rep_minus_one(rep[0], &off)) {
+                                st = kErrOffset;
+                                break;
+                            }
+                            rep[2] = rep[1];
+                            rep[1] = rep[0];
+                            rep[0] = off;
+                        }
+                    }
+                    tll += ll;
+                    tml += ml;
+                    if (tll > Bp->lit_size) {
+                        st = kErrSequences;
+                        break;
+                    }
+                    recs[lane][k] = seq_pack(ll, ml, off);
+                    if (++i < nseq) {
+                        sll = ell.base + r.read(ell.nb);
+                        sml = eml.base + r.read(eml.nb);
+                        sof = eof.base + r.read(eof.nb);
+                    }
+                }
+            }
+            if (lane < kSeqLanes) {
+                s_n[lane] = k;
+                s_i[lane] = i;
+                s_out[lane] = out;
+            }
+            if (lane == 0) s_active = 0;
+            __syncthreads();
+            if (mine && st == kOk && i < nseq) atomicOr(&s_active, 1u);
+            // the staged records of every lane, written by the whole wave
+            for (int q = lane; q < kSeqLanes * kSeqFlush; q += 64) {
+                const int ln = q / kSeqFlush, kk = q % kSeqFlush;
+                const uint32_t nl = s_n[ln];
+                if ((uint32_t)kk < nl) s_out[ln][s_i[ln] - nl + kk] = recs[ln][kk];
+            }
+            __syncthreads();
+            if (!s_active) break;
+        }
+        if (mine) {
+            if (st == kOk && nseq && r.pos > 0) st = kErrSequences;
+            if (st == kOk && Bp->lit_size + tml > kBlockMax) st = kErrBlock;
+            Bp->sum_ll = tll;
+            Bp->regen = Bp->lit_size + tml;
+            if (st == kOk)
+                for (int k = 0; k < 3; ++k) Bp->rep_end[k] = rep[k];
+            else
+                Bp->status = st;
         }
         __syncthreads();
     }
 }
 
-// One wave per block with sequences: lane 0 builds the LL/OF/ML tables in LDS
-// and decodes the block's sequences.
-__global__ void __launch_bounds__(64) k_zs_sequences(Launch L) {
-    __shared__ FseEntry tab[3][512];
-    __shared__ int16_t norm[64];
-    __shared__ uint16_t next[64];
-    const uint32_t total = L.counters[1];
-    for (uint32_t w = blockIdx.x; w < total; w += gridDim.x) {
-        if (threadIdx.x == 0) {
-            const Work wk = L.seq_work[w];
-            const DevFrame& F = L.frames[wk.frame];
-            Block& B = L.blocks[(size_t)wk.frame * L.max_blocks + wk.block];
-            SeqTables T;
-            uint32_t st = kOk;
-            for (int k = 0; k < 3 && st == kOk; ++k) {
-                const int lg = table_for(F.src, B.src + B.size, B.table[k], k, tab[k], norm, next);
-                if (lg < 0) st = kErrFse;
-                T.t[k] = tab[k];
-                T.log[k] = lg;
-            }
-            uint64_t sll = 0, sml = 0;
-            if (st == kOk)
-                st = decode_sequences(F.src, B, T, L.seq + (size_t)wk.frame * L.seq_cap + B.seq_out, &sll, &sml,
-                                      B.rep_end);
-            if (st == kOk && B.lit_size + sml > kBlockMax) st = kErrBlock;
-            B.sum_ll = sll;
-            B.regen = B.lit_size + sml;
-            if (st != kOk) B.status = st;
+// One thread per frame: the blocks' failures, output positions and starting
+// repeat-offset histories (composing the blocks' transfers in order).
+__global__ void __launch_bounds__(64) k_zs_layout(Launch L) {
+    const uint32_t f = blockIdx.x * 64 + threadIdx.x;
+    if (f >= L.count) return;
+    DevFrame& F = L.frames[f];
+    if (F.status != kOk) return;
+    Block* bl = L.blocks + (size_t)f * L.max_blocks;
+    uint32_t st = kOk, eb = 0;
+    uint32_t cur[3] = {1, 4, 8};
+    uint64_t out = 0;
+    for (uint32_t b = 0; b < F.nblocks; ++b) {
+        Block& B = bl[b];
+        if (B.status != kOk) {
+            st = B.status;
+            eb = b;
+            break;
         }
+        B.out = out;
+        out += B.regen;
+        uint32_t nx[3];
+        for (int k = 0; k < 3; ++k) {
+            B.rep_start[k] = cur[k];
+            const uint64_t v = rep_resolve(B.rep_end[k], cur);
+            nx[k] = v < (1ull << 31) ? (uint32_t)v : 0;
+        }
+        for (int k = 0; k < 3; ++k) cur[k] = nx[k];
+    }
+    if (st == kOk && out != F.content) st = kErrContentSize;
+    if (st != kOk) {
+        F.status = st;
+        F.err_block = eb;
+    }
+}
+
+// Raw and RLE blocks, one workgroup each: the block's bytes to the frame's
+// output scratch, whole aligned words (4 per thread in flight) and the ends
+// byte by byte.
+__global__ void __launch_bounds__(256) k_zs_raw(Launch L) {
+    const uint32_t total = L.counters[2];
+    const int t = (int)threadIdx.x;
+    for (uint32_t w = blockIdx.x; w < total; w += gridDim.x) {
+        const Work wk = L.raw_work[w];
+        const DevFrame& F = L.frames[wk.frame];
+        if (F.status != kOk) continue;
+        const Block& B = L.blocks[(size_t)wk.frame * L.max_blocks + wk.block];
+        uint8_t* dst = L.out + (size_t)wk.frame * L.out_cap + B.out;
+        const uint32_t n = (uint32_t)B.regen;
+        const uint8_t* src = F.src + B.src;
+        const uint8_t* ok_lo = F.src;
+        const uint8_t* ok_hi = F.src + F.size;
+        const bool rle = B.type == 1;
+        const uint32_t rv = rle ? load_byte(src) * 0x01010101u : 0;
+        const uint32_t head = std::min<uint32_t>((4 - ((uintptr_t)dst & 3)) & 3, n);
+        if (t < (int)head) dst[t] = rle ? (uint8_t)rv : load_byte(src + t);
+        const uint32_t words = (n - head) / 4;
+        for (uint32_t w0 = t; w0 < words; w0 += 4 * 256) {
+            uint32_t v[4];
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                const uint32_t wi = w0 + 256 * u;
+                v[u] = wi < words ? (rle ? rv : load4(src + head + 4 * wi, ok_lo, ok_hi)) : 0;
+            }
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                const uint32_t wi = w0 + 256 * u;
+                if (wi < words) *reinterpret_cast<uint32_t*>(dst + head + 4 * wi) = v[u];
+            }
+        }
+        const uint32_t rest = head + 4 * words;
+        if (t < (int)(n - rest)) dst[rest + t] = rle ? (uint8_t)rv : load_byte(src + rest + t);
     }
 }
 
@@ -258,31 +714,43 @@ __device__ __forceinline__ void for_bytes(const uint8_t* src, uint64_t b, uint64
 // Literal bytes [j0, j1) of the block (block-relative literal indices) into
 // obuf: with `cnt` sequences, literal j of sequence i lands at
 // mst[i] - (lit[i + 1] - j); with cnt == 0 (the trailing literals) at
-// tail_pos + (j - j0). Each thread takes 16-byte windows of the literal index.
-__device__ void copy_literals(ExecLds& S, const Block& B, const uint8_t* litp, uint32_t j0, uint32_t j1, int cnt,
-                              uint32_t tail_pos) {
+// tail_pos + (j - j0). Each thread takes 16-byte windows of the literal index,
+// loaded whole before they are placed.
+__device__ void copy_literals(ExecLds& S, const Block& B, const uint8_t* litp, const uint8_t* ok_lo,
+                              const uint8_t* ok_hi, uint32_t j0, uint32_t j1, int cnt, uint32_t tail_pos) {
     if (j1 <= j0) return;
     const uint32_t w0 = j0 & ~15u;
-    const uint32_t nwin = ((j1 + 15) & ~15u) - w0;
-    for (uint32_t a = w0 + 16 * threadIdx.x; a < w0 + nwin; a += 16 * kExecThreads) {
+    const uint32_t wend = (j1 + 15) & ~15u;
+    for (uint32_t a = w0 + 16 * threadIdx.x; a < wend; a += 16 * kExecThreads) {
         const uint32_t b = a > j0 ? a : j0, e = a + 16 < j1 ? a + 16 : j1;
-        if (b >= e) continue;
+        uint32_t v[4];
+        if (B.lit_type == 2) {
+            // the Huffman scratch: 16-byte aligned windows inside the allocation
+#pragma unroll
+            for (int u = 0; u < 4; ++u) v[u] = load_word(litp + a + 4 * u);
+        } else if (B.lit_type == 0) {
+            // raw literals in the frame: the window's bytes inside the literals
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                const uint32_t o = a + 4 * u;
+                v[u] = (o >= b && o + 4 <= e) ? load4(litp + o, ok_lo, ok_hi) : 0;
+                if (!(o >= b && o + 4 <= e))
+                    for (int k = 0; k < 4; ++k)
+                        if (o + k >= b && o + k < e) v[u] |= (uint32_t)load_byte(litp + o + k) << (8 * k);
+            }
+        } else {
+            const uint32_t r = load_byte(litp) * 0x01010101u;
+            v[0] = v[1] = v[2] = v[3] = r;
+        }
         int i = cnt ? last_le(S.lit, cnt, b) : 0;
-        auto put = [&](uint64_t j, uint8_t v) {
+        for (uint32_t j = b; j < e; ++j) {
+            const uint8_t x = (uint8_t)(v[(j - a) >> 2] >> (8 * ((j - a) & 3)));
             if (cnt) {
                 while (j >= S.lit[i + 1]) ++i;
-                S.obuf[S.mst[i] - (S.lit[i + 1] - (uint32_t)j)] = v;
+                S.obuf[S.mst[i] - (S.lit[i + 1] - j)] = x;
             } else {
-                S.obuf[tail_pos + ((uint32_t)j - j0)] = v;
+                S.obuf[tail_pos + (j - j0)] = x;
             }
-        };
-        if (B.lit_type == 2) {
-            for_bytes(litp, b, e, put);
-        } else if (B.lit_type == 0) {
-            for_bytes(litp, b, e, put);
-        } else {
-            const uint8_t v = litp[0];
-            for (uint32_t j = b; j < e; ++j) put(j, v);
         }
     }
 }
@@ -304,6 +772,8 @@ __device__ void exec_block(ExecLds& S, const DevFrame& F, const Launch& L, uint3
     const int t = (int)threadIdx.x;
     const uint64_t base = B.out;
     const uint8_t* litp = B.lit_type == 2 ? L.lit + (size_t)f * L.lit_cap + B.lit_out : F.src + B.lit_src;
+    const uint8_t* ok_lo = F.src;
+    const uint8_t* ok_hi = F.src + F.size;
     const uint64_t* sq = L.seq + (size_t)f * L.seq_cap + B.seq_out;
     const uint32_t rs[3] = {B.rep_start[0], B.rep_start[1], B.rep_start[2]};
     uint32_t pos = 0, lp = 0;
@@ -349,67 +819,110 @@ __device__ void exec_block(ExecLds& S, const DevFrame& F, const Launch& L, uint3
         if (t == 0) S.lit[cnt] = lp + (uint32_t)(tot >> 32);
         __syncthreads();
         if (S.err) return;
-        copy_literals(S, B, litp, lp, lp + (uint32_t)(tot >> 32), cnt, 0);
+        copy_literals(S, B, litp, ok_lo, ok_hi, lp, lp + (uint32_t)(tot >> 32), cnt, 0);
         __syncthreads();
         // matches in dependency rounds: a match runs once no pending earlier
-        // match writes any byte of its source
+        // match writes any byte of its source. The earlier matches that could
+        // (those whose output meets the source) are found once per chunk.
+        int clo[2], chi[2];
+        int64_t srcq[2];
+#pragma unroll
+        for (int q = 0; q < 2; ++q) {
+            const int i = 2 * t + q;
+            clo[q] = chi[q] = 0;
+            srcq[q] = 0;
+            if (i < cnt && ml[q]) {
+                const int64_t src = (int64_t)S.mst[i] - S.off[i];
+                const int64_t e = min<int64_t>(src + S.ml[i], S.mst[i]);
+                srcq[q] = src;
+                if (e > 0 && i > 0) {
+                    const uint32_t s0 = src > 0 ? (uint32_t)src : 0;
+                    // first sequence whose match ends past s0, first whose match starts at or past e
+                    int lo = 0, hi = i;
+                    while (lo < hi) {
+                        const int mid = (lo + hi) >> 1;
+                        if (S.mst[mid] + S.ml[mid] > s0)
+                            hi = mid;
+                        else
+                            lo = mid + 1;
+                    }
+                    int lo2 = lo, hi2 = i;
+                    while (lo2 < hi2) {
+                        const int mid = (lo2 + hi2) >> 1;
+                        if (S.mst[mid] >= (uint32_t)e)
+                            hi2 = mid;
+                        else
+                            lo2 = mid + 1;
+                    }
+                    clo[q] = lo;
+                    chi[q] = lo2;
+                }
+            }
+        }
         for (;;) {
-            bool rdy[2];
+            bool rdy[2], coop[2];
 #pragma unroll
             for (int q = 0; q < 2; ++q) {
                 const int i = 2 * t + q;
-                rdy[q] = false;
-                if (i < cnt && (S.pend[i >> 5] >> (i & 31) & 1)) {
-                    const int64_t src = (int64_t)S.mst[i] - S.off[i];
-                    const int64_t e = min<int64_t>(src + S.ml[i], S.mst[i]);
-                    bool clash = false;
-                    if (e > 0 && i > 0) {
-                        const uint32_t s0 = src > 0 ? (uint32_t)src : 0;
-                        // first sequence whose match ends past s0, first whose match starts at or past e
-                        int lo = 0, hi = i;
-                        while (lo < hi) {
-                            const int mid = (lo + hi) >> 1;
-                            if (S.mst[mid] + S.ml[mid] > s0)
-                                hi = mid;
-                            else
-                                lo = mid + 1;
-                        }
-                        int lo2 = lo, hi2 = i;
-                        while (lo2 < hi2) {
-                            const int mid = (lo2 + hi2) >> 1;
-                            if (S.mst[mid] >= (uint32_t)e)
-                                hi2 = mid;
-                            else
-                                lo2 = mid + 1;
-                        }
-                        clash = any_pending(S.pend, lo, lo2);
-                    }
-                    rdy[q] = !clash;
-                }
+                rdy[q] = i < cnt && (S.pend[i >> 5] >> (i & 31) & 1) && !any_pending(S.pend, clo[q], chi[q]);
+                // long matches and matches reaching into earlier blocks are
+                // shared out bytewise; short in-block ones stay with their thread
+                coop[q] = rdy[q] && (ml[q] > 64 || srcq[q] < 0);
             }
-            const uint64_t mlen = (rdy[0] ? ml[0] : 0) + (rdy[1] ? ml[1] : 0);
+            const uint64_t mlen = (coop[0] ? ml[0] : 0) + (coop[1] ? ml[1] : 0);
             uint64_t rtot;
             const uint32_t rpre = (uint32_t)wg_scan(mlen, S.scan, &rtot);
             if (2 * t < cnt) S.rpre[2 * t] = rpre;
-            if (2 * t + 1 < cnt) S.rpre[2 * t + 1] = rpre + (rdy[0] ? ml[0] : 0);
+            if (2 * t + 1 < cnt) S.rpre[2 * t + 1] = rpre + (coop[0] ? ml[0] : 0);
             if (t < kChunk / 32) S.ready[t] = 0;
             __syncthreads();
 #pragma unroll
             for (int q = 0; q < 2; ++q)
-                if (rdy[q]) atomicOr(&S.ready[(2 * t + q) >> 5], 1u << ((2 * t + q) & 31));
+                if (coop[q]) atomicOr(&S.ready[(2 * t + q) >> 5], 1u << ((2 * t + q) & 31));
             __syncthreads();
-            const uint32_t R = (uint32_t)rtot;
-            for (uint32_t b = t; b < R; b += kExecThreads) {
-                int i = last_le(S.rpre, cnt, b);
-                while (i > 0 && !(S.ready[i >> 5] >> (i & 31) & 1)) --i;  // zero-length entries share a prefix
-                const uint32_t k = b - S.rpre[i], o = S.off[i], m = S.mst[i];
-                const uint32_t kk = o < S.ml[i] ? k % o : k;
-                const int64_t si = (int64_t)m - o + kk;
-                S.obuf[m + k] = si >= 0 ? S.obuf[si] : fout[(int64_t)base + si];
+#pragma unroll
+            for (int q = 0; q < 2; ++q) {
+                if (rdy[q] && !coop[q]) {
+                    const uint32_t m = S.mst[2 * t + q], o = off[q], n = ml[q];
+                    if (o >= n) {
+                        for (uint32_t k = 0; k < n; ++k) S.obuf[m + k] = S.obuf[m - o + k];
+                    } else {
+                        uint32_t k2 = 0;
+                        for (uint32_t k = 0; k < n; ++k) {
+                            S.obuf[m + k] = S.obuf[m - o + k2];
+                            if (++k2 == o) k2 = 0;
+                        }
+                    }
+                }
             }
-            __syncthreads();
-            if (t < kChunk / 32) S.pend[t] &= ~S.ready[t];
+            const uint32_t R = (uint32_t)rtot;
+            for (uint32_t b0 = t; b0 < R; b0 += 4 * kExecThreads) {
+                uint32_t dpos[4];
+                uint8_t val[4];
+#pragma unroll
+                for (int u = 0; u < 4; ++u) {
+                    const uint32_t b = b0 + u * kExecThreads;
+                    dpos[u] = 0xffffffffu;
+                    val[u] = 0;
+                    if (b < R) {
+                        int i = last_le(S.rpre, cnt, b);
+                        while (i > 0 && !(S.ready[i >> 5] >> (i & 31) & 1)) --i;  // zero-length entries share a prefix
+                        const uint32_t k = b - S.rpre[i], o = S.off[i], m = S.mst[i];
+                        const uint32_t kk = o < S.ml[i] ? k % o : k;
+                        const int64_t si = (int64_t)m - o + kk;
+                        dpos[u] = m + k;
+                        val[u] = si >= 0 ? S.obuf[si] : load_byte(fout + ((int64_t)base + si));
+                    }
+                }
+#pragma unroll
+                for (int u = 0; u < 4; ++u)
+                    if (dpos[u] != 0xffffffffu) S.obuf[dpos[u]] = val[u];
+            }
             if (t == 0) S.flag = 0;
+            __syncthreads();
+#pragma unroll
+            for (int q = 0; q < 2; ++q)
+                if (rdy[q]) atomicAnd(&S.pend[(2 * t + q) >> 5], ~(1u << ((2 * t + q) & 31)));
             __syncthreads();
             if (t < kChunk / 32 && S.pend[t]) atomicOr(&S.flag, 1u);
             __syncthreads();
@@ -419,7 +932,7 @@ __device__ void exec_block(ExecLds& S, const DevFrame& F, const Launch& L, uint3
         lp += (uint32_t)(tot >> 32);
     }
     // literals after the last sequence
-    copy_literals(S, B, litp, lp, B.lit_size, 0, pos);
+    copy_literals(S, B, litp, ok_lo, ok_hi, lp, B.lit_size, 0, pos);
     __syncthreads();
 }
 
@@ -446,66 +959,24 @@ __global__ void __launch_bounds__(kExecThreads) k_zs_execute(Launch L) {
     const uint32_t f = blockIdx.x;
     DevFrame& F = L.frames[f];
     if (F.status != kOk) return;
-    Block* bl = L.blocks + (size_t)f * L.max_blocks;
+    const Block* bl = L.blocks + (size_t)f * L.max_blocks;
     uint8_t* fout = L.out + (size_t)f * L.out_cap;
     const int t = (int)threadIdx.x;
-    if (t == 0) {
-        // blocks' failures, output positions and starting repeat-offset histories
-        uint32_t st = kOk, eb = 0;
-        uint32_t cur[3] = {1, 4, 8};
-        uint64_t out = 0;
-        for (uint32_t b = 0; b < F.nblocks && st == kOk; ++b) {
-            Block& B = bl[b];
-            if (B.status != kOk) {
-                st = B.status;
-                eb = b;
-                break;
-            }
-            B.out = out;
-            out += B.regen;
-            uint32_t nx[3];
-            for (int k = 0; k < 3; ++k) {
-                B.rep_start[k] = cur[k];
-                const uint64_t v = rep_resolve(B.rep_end[k], cur);
-                nx[k] = v < (1ull << 31) ? (uint32_t)v : 0;
-            }
-            for (int k = 0; k < 3; ++k) cur[k] = nx[k];
-        }
-        if (st == kOk && out != F.content) st = kErrContentSize;
-        S.err = 0;
-        S.flag = st;
-        if (st != kOk) {
-            F.status = st;
-            F.err_block = eb;
-        }
-    }
+    if (t == 0) S.err = 0;
     __syncthreads();
-    if (S.flag != kOk) return;
+    // compressed blocks in order (raw and RLE blocks are already in place)
     for (uint32_t b = 0; b < F.nblocks; ++b) {
         const Block& B = bl[b];
-        const uint32_t n = (uint32_t)B.regen;
-        if (B.type == 0) {
-            // raw: through LDS so the stores are whole words
-            for (uint64_t a = (B.src & ~3ull) + 4 * t; a < (uint64_t)B.src + n; a += 4 * kExecThreads) {
-                const uint64_t lo = a > B.src ? a : B.src, hi = a + 4 < (uint64_t)B.src + n ? a + 4 : B.src + n;
-                for_bytes(F.src, lo, hi, [&](uint64_t i, uint8_t v) { S.obuf[i - B.src] = v; });
+        if (B.type != 2) continue;
+        exec_block(S, F, L, f, B, fout);
+        if (S.err) {
+            if (t == 0) {
+                F.status = kErrOffset;
+                F.err_block = b;
             }
-            __syncthreads();
-        } else if (B.type == 1) {
-            const uint8_t v = F.src[B.src];
-            for (uint32_t i = t; i < n; i += kExecThreads) S.obuf[i] = v;
-            __syncthreads();
-        } else {
-            exec_block(S, F, L, f, B, fout);
-            if (S.err) {
-                if (t == 0) {
-                    F.status = kErrOffset;
-                    F.err_block = b;
-                }
-                return;
-            }
+            return;
         }
-        store_block(S.obuf, fout + B.out, n);
+        store_block(S.obuf, fout + B.out, (uint32_t)B.regen);
         __syncthreads();
     }
 }
@@ -588,8 +1059,8 @@ Decoder::Decoder(int device, size_t max_frames, uint64_t max_content) : device_(
         lit_ = dev_alloc<uint8_t>(max_frames * lit_cap_);
         seq_ = dev_alloc<uint64_t>(max_frames * seq_cap_ * sizeof(uint64_t));
         out_ = dev_alloc<uint8_t>(max_frames * out_cap_);
-        work_ = dev_alloc<void>(2 * max_frames * (size_t)max_blocks_ * sizeof(Work));
-        counters_ = dev_alloc<uint32_t>(2 * sizeof(uint32_t));
+        work_ = dev_alloc<void>(3 * max_frames * (size_t)max_blocks_ * sizeof(Work));
+        counters_ = dev_alloc<uint32_t>(3 * sizeof(uint32_t));
         hcheck(hipEventCreateWithFlags(&last_, hipEventDisableTiming), "hipEventCreate");
         hcheck(hipEventCreateWithFlags(&copied_, hipEventDisableTiming), "hipEventCreate");
         hcheck(hipFuncSetAttribute((const void*)k_zs_execute, hipFuncAttributeMaxDynamicSharedMemorySize,
@@ -701,11 +1172,14 @@ bool Decoder::queue(const std::vector<FrameJob>& jobs, hipStream_t s, std::strin
         L.out_cap = out_cap_;
         L.huf_work = static_cast<Work*>(work_);
         L.seq_work = static_cast<Work*>(work_) + max_frames_ * (size_t)max_blocks_;
+        L.raw_work = static_cast<Work*>(work_) + 2 * max_frames_ * (size_t)max_blocks_;
         L.counters = counters_;
         hipLaunchKernelGGL(k_zs_reset, dim3(1), dim3(64), 0, s, counters_);
         hipLaunchKernelGGL(k_zs_index, dim3((count + 63) / 64), dim3(64), 0, s, L);
-        hipLaunchKernelGGL(k_zs_literals, dim3(grid_), dim3(64), 0, s, L);
-        hipLaunchKernelGGL(k_zs_sequences, dim3(grid_), dim3(64), 0, s, L);
+        hipLaunchKernelGGL(k_zs_literals, dim3(grid_), dim3(256), 0, s, L);
+        hipLaunchKernelGGL(k_zs_sequences, dim3(grid_), dim3(64), 0, s, L);  // kSeqLanes blocks per workgroup
+        hipLaunchKernelGGL(k_zs_layout, dim3((count + 63) / 64), dim3(64), 0, s, L);
+        hipLaunchKernelGGL(k_zs_raw, dim3(grid_), dim3(256), 0, s, L);
         hipLaunchKernelGGL(k_zs_execute, dim3(count), dim3(kExecThreads), sizeof(ExecLds), s, L);
         const uint32_t pieces = (uint32_t)std::min<uint64_t>((max_content_ + 4095) / 4096, 2048);
         hipLaunchKernelGGL(k_zs_finish, dim3(pieces, count), dim3(256), 0, s, L);

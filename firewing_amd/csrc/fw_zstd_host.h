@@ -62,8 +62,8 @@ class Decoder {
     uint8_t* lit_ = nullptr;
     uint64_t* seq_ = nullptr;
     uint8_t* out_ = nullptr;
-    void* work_ = nullptr;         // two work lists of max_frames * max_blocks entries
-    uint32_t* counters_ = nullptr;  // [chunks][2]
+    void* work_ = nullptr;         // three work lists of max_frames * max_blocks entries
+    uint32_t* counters_ = nullptr;  // the work lists' lengths
     void* frames_ = nullptr;        // device frame records of the last call
     void* frames_host_ = nullptr;   // pinned staging of the frame records
     hipEvent_t copied_ = nullptr;   // the last upload of the records has run

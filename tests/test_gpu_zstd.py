@@ -211,3 +211,27 @@ def test_install_real_shape_experts():
         # neighbours untouched
         ref = fo.synth_tensor(3, 0, hm.GATE_UP, 18 * 2 * I * H, 4096)
         assert np.array_equal(ctx.read_tensor(0, hm.GATE_UP, 18 * 2 * I * H, 4096), ref)
+
+
+def test_install_from_container_file(tmp_path):
+    # the reference's miss path: page-aligned preads of the records, then
+    # decode + unshuffle + install (src/compressed_overlap.rs:1426-1560)
+    from firewing_amd import container as fc
+    H, I, E = SMALL["hidden"], SMALL["intermediate"], SMALL["experts"]
+    rng = np.random.default_rng(8)
+    weights = {}
+    recs = []
+    for layer in (0, 1):
+        for e in range(E):
+            gu, dn = bf16_weights(rng, 2 * I * H, 0.2), bf16_weights(rng, H * I, 0.2)
+            weights[(layer, e)] = (gu, dn)
+            recs.append((layer, e, gu, dn))
+    fc.write_container(tmp_path / "experts.fwz", tmp_path / "experts.json", recs)
+    c = fc.Container(tmp_path / "experts.json")
+    with hm.MoeContext(layers=2, **SMALL) as ctx, hm.ZstdDecoder(E, 6 * I * H) as dec:
+        ctx.generate_layers(0, 2, 12, True)
+        for layer in (0, 1):
+            c.install(ctx, dec, layer, list(range(E)), verify=True)
+        for (layer, e), (gu, dn) in weights.items():
+            assert np.array_equal(ctx.read_tensor(layer, hm.GATE_UP, e * 2 * I * H, 2 * I * H), gu)
+            assert np.array_equal(ctx.read_tensor(layer, hm.DOWN, e * H * I, H * I), dn)
