@@ -67,6 +67,8 @@ struct Launch {
 
 constexpr int kExecThreads = 512;
 constexpr int kChunk = 1024;  // sequences per execute round set (2 per thread)
+constexpr int kFar = 7168;    // LDS bytes for a chunk's sources in earlier blocks
+constexpr uint32_t kShort = 64;  // matches up to this long are copied by their own thread
 
 __global__ void k_zs_reset(uint32_t* counters) {
     if (threadIdx.x < 3) counters[threadIdx.x] = 0;
@@ -400,7 +402,10 @@ struct GlobalBits {
     }
 };
 
-constexpr int kSeqLanes = 8;     // blocks per wave in the sequence pass
+#ifndef FW_ZS_SEQ_LANES
+#define FW_ZS_SEQ_LANES 8
+#endif
+constexpr int kSeqLanes = FW_ZS_SEQ_LANES;  // blocks per wave in the sequence pass
 constexpr int kSeqFlush = 64;    // records per lane staged in LDS between flushes
 constexpr int kSeqTable = 1280;  // LL [0, 512), OF [512, 768), ML [768, 1280)
 
@@ -475,57 +480,39 @@ __global__ void __launch_bounds__(64) k_zs_sequences(Launch L) {
                 const FseEntry* tll_ = tl;
                 const FseEntry* tof_ = tl + 512;
                 const FseEntry* tml_ = tl + 768;
+                // symbols are in range by construction (table_for: counts of
+                // at most kMaxSym[kind] symbols, RLE symbols checked)
                 for (; k < (uint32_t)kSeqFlush && i < nseq; ++k) {
                     const FseEntry ell = tll_[sll], eof = tof_[sof], eml = tml_[sml];
-                    const uint32_t mc = mlcode[eml.sym < 53 ? eml.sym : 0], lc = llcode[ell.sym < 36 ? ell.sym : 0];
-                    if (eof.sym > 31 || eml.sym > 52 || ell.sym > 35) {
-                        st = kErrSequences;
-                        break;
-                    }
+                    const uint32_t mc = mlcode[eml.sym], lc = llcode[ell.sym];
                     r.refill();
                     const uint64_t ov = (1ull << eof.sym) + r.read(eof.sym);
                     const uint32_t ml = (mc & 0xffffff) + r.read(mc >> 24);
                     r.refill();
                     const uint32_t ll = (lc & 0xffffff) + r.read(lc >> 24);
-                    uint32_t off;
-                    if (ov > 3) {
-                        if (ov - 3 >= (1ull << 27)) {
-                            st = kErrOffset;
-                            break;
-                        }
-                        off = (uint32_t)(ov - 3);
-                        rep[2] = rep[1];
-                        rep[1] = rep[0];
-                        rep[0] = off;
-                    } else {
-                        const int idx = (int)ov - 1 + (ll == 0);
-                        if (idx == 0) {
-                            off = rep[0];
-                        } else if (idx == 1) {
-                            off = rep[1];
-                            rep[1] = rep[0];
-                            rep[0] = off;
-                        } else if (idx == 2) {
-                            off = rep[2];
-                            rep[2] = rep[1];
-                            rep[1] = rep[0];
-                            rep[0] = off;
-                        } else {
-                            if (!rep_minus_one(rep[0], &off)) {
-                                st = kErrOffset;
-                                break;
-                            }
-                            rep[2] = rep[1];
-                            rep[1] = rep[0];
-                            rep[0] = off;
-                        }
-                    }
-                    tll += ll;
-                    tml += ml;
-                    if (tll > Bp->lit_size) {
-                        st = kErrSequences;
+                    // repeat offsets (RFC 8878 3.1.1.5) without branches: idx 0..2
+                    // take history entry idx (idx from the code and ll == 0),
+                    // 3 = entry 0 minus one, 4 = a new offset
+                    const bool fresh = ov > 3;
+                    const uint32_t idx = fresh ? 4u : (uint32_t)ov - 1u + (ll == 0);
+                    uint32_t m1;
+                    const bool m1ok = rep_minus_one(rep[0], &m1);
+                    const uint32_t off = idx == 0 ? rep[0]
+                                         : idx == 1 ? rep[1]
+                                         : idx == 2 ? rep[2]
+                                         : idx == 3 ? m1
+                                                    : (uint32_t)(ov - 3);
+                    if ((fresh && ov - 3 >= (1ull << 27)) || (idx == 3 && !m1ok)) {
+                        st = kErrOffset;
                         break;
                     }
+                    const uint32_t n1 = idx == 0 ? rep[1] : rep[0];
+                    const uint32_t n2 = idx <= 1 ? rep[2] : rep[1];
+                    rep[0] = off;
+                    rep[1] = n1;
+                    rep[2] = n2;
+                    tll += ll;
+                    tml += ml;
                     recs[lane][k] = seq_pack(ll, ml, off);
                     if (++i < nseq) {
                         sll = ell.base + r.read(ell.nb);
@@ -533,6 +520,8 @@ __global__ void __launch_bounds__(64) k_zs_sequences(Launch L) {
                         sof = eof.base + r.read(eof.nb);
                     }
                 }
+                // the literal lengths only grow: one check per batch
+                if (tll > Bp->lit_size) st = kErrSequences;
             }
             if (lane < kSeqLanes) {
                 s_n[lane] = k;
@@ -648,11 +637,13 @@ struct ExecLds {
     uint32_t ml[kChunk];
     uint32_t off[kChunk];
     uint32_t rpre[kChunk];     // this round's ready match bytes before sequence i
+    uint32_t fpre[kChunk];     // first byte of sequence i's earlier-block source in far
     uint32_t pend[kChunk / 32];
     uint32_t ready[kChunk / 32];
     uint64_t scan[kExecThreads / 64];
     uint32_t flag;
     uint32_t err;
+    uint8_t far[kFar];         // the chunk's match-source bytes from earlier blocks
 };
 
 // exclusive prefix over the workgroup of a 64-bit value; *total = the sum
@@ -821,20 +812,59 @@ __device__ void exec_block(ExecLds& S, const DevFrame& F, const Launch& L, uint3
         if (S.err) return;
         copy_literals(S, B, litp, ok_lo, ok_hi, lp, lp + (uint32_t)(tot >> 32), cnt, 0);
         __syncthreads();
-        // matches in dependency rounds: a match runs once no pending earlier
-        // match writes any byte of its source. The earlier matches that could
-        // (those whose output meets the source) are found once per chunk.
-        int clo[2], chi[2];
+        // the bytes of earlier blocks that this chunk's matches copy: staged
+        // in LDS once (those blocks are final), unless they do not fit
+        uint32_t need[2];
         int64_t srcq[2];
 #pragma unroll
         for (int q = 0; q < 2; ++q) {
             const int i = 2 * t + q;
+            srcq[q] = (i < cnt && ml[q]) ? (int64_t)S.mst[i] - off[q] : 0;
+            // a match reads its first min(off, ml) source bytes (the rest repeat them)
+            const int64_t used = srcq[q] + (int64_t)min(off[q], ml[q]);
+            need[q] = srcq[q] < 0 ? (uint32_t)((used < 0 ? used : 0) - srcq[q]) : 0;
+        }
+        uint64_t ftot;
+        const uint32_t fpre = (uint32_t)wg_scan(need[0] + need[1], S.scan, &ftot);
+        const bool far_ok = ftot <= (uint64_t)kFar;
+        if (2 * t < cnt) S.fpre[2 * t] = fpre;
+        if (2 * t + 1 < cnt) S.fpre[2 * t + 1] = fpre + need[0];
+        __syncthreads();
+        if (far_ok) {
+            const uint32_t F_ = (uint32_t)ftot;
+            for (uint32_t b0 = t; b0 < F_; b0 += 4 * kExecThreads) {
+                uint32_t at[4];
+                uint8_t v[4];
+#pragma unroll
+                for (int u = 0; u < 4; ++u) {
+                    const uint32_t b = b0 + u * kExecThreads;
+                    at[u] = 0xffffffffu;
+                    v[u] = 0;
+                    if (b < F_) {
+                        // the last sequence with fpre <= b owns byte b (sequences that
+                        // stage nothing share their successor's prefix)
+                        const int i = last_le(S.fpre, cnt, b);
+                        const int64_t src = (int64_t)S.mst[i] - S.off[i];
+                        at[u] = b;
+                        v[u] = load_byte(fout + ((int64_t)base + src + (b - S.fpre[i])));
+                    }
+                }
+#pragma unroll
+                for (int u = 0; u < 4; ++u)
+                    if (at[u] != 0xffffffffu) S.far[at[u]] = v[u];
+            }
+        }
+        // matches in dependency rounds: a match runs once no pending earlier
+        // match writes any byte of its source. The earlier matches that could
+        // (those whose output meets the source) are found once per chunk.
+        int clo[2], chi[2];
+#pragma unroll
+        for (int q = 0; q < 2; ++q) {
+            const int i = 2 * t + q;
             clo[q] = chi[q] = 0;
-            srcq[q] = 0;
             if (i < cnt && ml[q]) {
-                const int64_t src = (int64_t)S.mst[i] - S.off[i];
+                const int64_t src = srcq[q];
                 const int64_t e = min<int64_t>(src + S.ml[i], S.mst[i]);
-                srcq[q] = src;
                 if (e > 0 && i > 0) {
                     const uint32_t s0 = src > 0 ? (uint32_t)src : 0;
                     // first sequence whose match ends past s0, first whose match starts at or past e
@@ -859,74 +889,78 @@ __device__ void exec_block(ExecLds& S, const DevFrame& F, const Launch& L, uint3
                 }
             }
         }
+        __syncthreads();  // far bytes staged
+        bool left[2] = {false, false};
+#pragma unroll
+        for (int q = 0; q < 2; ++q) left[q] = (2 * t + q) < cnt && ml[q] > 0;
         for (;;) {
             bool rdy[2], coop[2];
 #pragma unroll
             for (int q = 0; q < 2; ++q) {
-                const int i = 2 * t + q;
-                rdy[q] = i < cnt && (S.pend[i >> 5] >> (i & 31) & 1) && !any_pending(S.pend, clo[q], chi[q]);
-                // long matches and matches reaching into earlier blocks are
-                // shared out bytewise; short in-block ones stay with their thread
-                coop[q] = rdy[q] && (ml[q] > 64 || srcq[q] < 0);
+                rdy[q] = left[q] && !any_pending(S.pend, clo[q], chi[q]);
+                // long matches, and earlier-block sources that did not fit in
+                // far, are shared out bytewise; the rest stay with their thread
+                coop[q] = rdy[q] && (ml[q] > kShort || (srcq[q] < 0 && !far_ok));
             }
-            const uint64_t mlen = (coop[0] ? ml[0] : 0) + (coop[1] ? ml[1] : 0);
-            uint64_t rtot;
-            const uint32_t rpre = (uint32_t)wg_scan(mlen, S.scan, &rtot);
-            if (2 * t < cnt) S.rpre[2 * t] = rpre;
-            if (2 * t + 1 < cnt) S.rpre[2 * t + 1] = rpre + (coop[0] ? ml[0] : 0);
-            if (t < kChunk / 32) S.ready[t] = 0;
-            __syncthreads();
-#pragma unroll
-            for (int q = 0; q < 2; ++q)
-                if (coop[q]) atomicOr(&S.ready[(2 * t + q) >> 5], 1u << ((2 * t + q) & 31));
-            __syncthreads();
 #pragma unroll
             for (int q = 0; q < 2; ++q) {
                 if (rdy[q] && !coop[q]) {
                     const uint32_t m = S.mst[2 * t + q], o = off[q], n = ml[q];
-                    if (o >= n) {
-                        for (uint32_t k = 0; k < n; ++k) S.obuf[m + k] = S.obuf[m - o + k];
-                    } else {
-                        uint32_t k2 = 0;
-                        for (uint32_t k = 0; k < n; ++k) {
-                            S.obuf[m + k] = S.obuf[m - o + k2];
-                            if (++k2 == o) k2 = 0;
+                    const int64_t src = srcq[q];
+                    const uint32_t fb = S.fpre[2 * t + q];
+                    uint32_t k2 = 0;
+                    for (uint32_t k = 0; k < n; ++k) {
+                        // source byte src + k2 (k2 = k mod o): in this block, or staged in far
+                        const int64_t si = src + k2;
+                        S.obuf[m + k] = si >= 0 ? S.obuf[si] : S.far[fb + k2];
+                        if (++k2 == o) k2 = 0;
+                    }
+                }
+            }
+            if (__syncthreads_or(coop[0] || coop[1])) {
+                const uint64_t mlen = (coop[0] ? ml[0] : 0) + (coop[1] ? ml[1] : 0);
+                uint64_t rtot;
+                const uint32_t rpre = (uint32_t)wg_scan(mlen, S.scan, &rtot);
+                if (2 * t < cnt) S.rpre[2 * t] = rpre;
+                if (2 * t + 1 < cnt) S.rpre[2 * t + 1] = rpre + (coop[0] ? ml[0] : 0);
+                if (t < kChunk / 32) S.ready[t] = 0;
+                __syncthreads();
+#pragma unroll
+                for (int q = 0; q < 2; ++q)
+                    if (coop[q]) atomicOr(&S.ready[(2 * t + q) >> 5], 1u << ((2 * t + q) & 31));
+                __syncthreads();
+                const uint32_t R = (uint32_t)rtot;
+                for (uint32_t b0 = t; b0 < R; b0 += 4 * kExecThreads) {
+                    uint32_t dpos[4];
+                    uint8_t val[4];
+#pragma unroll
+                    for (int u = 0; u < 4; ++u) {
+                        const uint32_t b = b0 + u * kExecThreads;
+                        dpos[u] = 0xffffffffu;
+                        val[u] = 0;
+                        if (b < R) {
+                            int i = last_le(S.rpre, cnt, b);
+                            while (i > 0 && !(S.ready[i >> 5] >> (i & 31) & 1)) --i;  // zero-length entries share a prefix
+                            const uint32_t k = b - S.rpre[i], o = S.off[i], m = S.mst[i];
+                            const uint32_t kk = o < S.ml[i] ? k % o : k;
+                            const int64_t si = (int64_t)m - o + kk;
+                            dpos[u] = m + k;
+                            val[u] = si >= 0 ? S.obuf[si] : load_byte(fout + ((int64_t)base + si));
                         }
                     }
-                }
-            }
-            const uint32_t R = (uint32_t)rtot;
-            for (uint32_t b0 = t; b0 < R; b0 += 4 * kExecThreads) {
-                uint32_t dpos[4];
-                uint8_t val[4];
 #pragma unroll
-                for (int u = 0; u < 4; ++u) {
-                    const uint32_t b = b0 + u * kExecThreads;
-                    dpos[u] = 0xffffffffu;
-                    val[u] = 0;
-                    if (b < R) {
-                        int i = last_le(S.rpre, cnt, b);
-                        while (i > 0 && !(S.ready[i >> 5] >> (i & 31) & 1)) --i;  // zero-length entries share a prefix
-                        const uint32_t k = b - S.rpre[i], o = S.off[i], m = S.mst[i];
-                        const uint32_t kk = o < S.ml[i] ? k % o : k;
-                        const int64_t si = (int64_t)m - o + kk;
-                        dpos[u] = m + k;
-                        val[u] = si >= 0 ? S.obuf[si] : load_byte(fout + ((int64_t)base + si));
-                    }
+                    for (int u = 0; u < 4; ++u)
+                        if (dpos[u] != 0xffffffffu) S.obuf[dpos[u]] = val[u];
                 }
-#pragma unroll
-                for (int u = 0; u < 4; ++u)
-                    if (dpos[u] != 0xffffffffu) S.obuf[dpos[u]] = val[u];
+                __syncthreads();
             }
-            if (t == 0) S.flag = 0;
-            __syncthreads();
 #pragma unroll
             for (int q = 0; q < 2; ++q)
-                if (rdy[q]) atomicAnd(&S.pend[(2 * t + q) >> 5], ~(1u << ((2 * t + q) & 31)));
-            __syncthreads();
-            if (t < kChunk / 32 && S.pend[t]) atomicOr(&S.flag, 1u);
-            __syncthreads();
-            if (!S.flag) break;
+                if (rdy[q]) {
+                    atomicAnd(&S.pend[(2 * t + q) >> 5], ~(1u << ((2 * t + q) & 31)));
+                    left[q] = false;
+                }
+            if (!__syncthreads_or(left[0] || left[1])) break;
         }
         pos += (uint32_t)tot;
         lp += (uint32_t)(tot >> 32);
