@@ -370,58 +370,34 @@ __global__ void __launch_bounds__(256) k_zs_literals(Launch L) {
     }
 }
 
-// Backward bit reader over a frame in global memory, the LdsBits contract
-// (refill() leaves at least 57 bits or reaches the stream's start; reads
-// between refills take no checks): three aligned words per refill when they
-// lie inside the frame [ok_lo, ok_hi), else bytes of the stream.
-struct GlobalBits {
-    const uint8_t* p;
-    const uint8_t* ok_lo;
-    const uint8_t* ok_hi;
-    uint32_t n;
-    int32_t pos, lo;
-    uint64_t c;
-    __device__ __forceinline__ void load() {
-        int32_t b = ((pos + 7) >> 3) - 8;
-        b = b < 0 ? 0 : b;
-        lo = 8 * b;
-        c = ::fw::zs::load8(p + b, n - b, ok_lo, ok_hi);
-    }
-    __device__ __forceinline__ void refill() {
-        if (pos - lo < 57 && lo > 0) load();
-    }
-    __device__ __forceinline__ uint32_t peek(int nb) const {
-        const int32_t sh = pos - lo - nb;
-        const uint64_t v = sh >= 0 ? (c >> (sh & 63)) : (c << ((-sh) & 63));
-        return (uint32_t)v & (uint32_t)((1ull << nb) - 1);
-    }
-    __device__ __forceinline__ uint32_t read(int nb) {
-        const uint32_t v = peek(nb);
-        pos -= nb;
-        return v;
-    }
-};
-
-#ifndef FW_ZS_SEQ_LANES
-#define FW_ZS_SEQ_LANES 8
-#endif
-constexpr int kSeqLanes = FW_ZS_SEQ_LANES;  // blocks per wave in the sequence pass
-constexpr int kSeqFlush = 64;    // records per lane staged in LDS between flushes
+constexpr int kSeqLanes = 8;     // blocks per wave in the sequence pass
+constexpr int kSeqFlush = 32;    // sequences per lane between record flushes
 constexpr int kSeqTable = 1280;  // LL [0, 512), OF [512, 768), ML [768, 1280)
+// A sequence reads at most 31 + 16 + 16 extra bits and 9 + 9 + 8 state bits:
+// kSeqFlush sequences consume at most 32 x 89 bits = 356 bytes.
+constexpr int kSeqBack = 360;
+constexpr int kSeqWin = 400;     // a lane's window of its bitstream (>= kSeqBack + 19)
 
 // kSeqLanes blocks per wave, one lane each: the lane builds its block's
-// LL/OF/ML tables in LDS and decodes its sequences from the frame in global
-// memory, two refills per sequence (offset + match-length extra bits <= 47,
-// literal-length extra bits + the three state updates <= 42); every
-// kSeqFlush sequences the whole wave writes the staged records out.
+// LL/OF/ML tables in LDS and decodes its sequences. Its bitstream is read
+// from a window of LDS that the whole wave refills between batches of
+// kSeqFlush sequences, so a sequence step never waits on global memory; two
+// refills of the bit word per sequence (offset + match-length extra bits <=
+// 47, literal-length extra bits + the three state updates <= 42). The wave
+// also writes the staged records out between batches.
 __global__ void __launch_bounds__(64) k_zs_sequences(Launch L) {
     __shared__ FseEntry tabs[kSeqLanes][kSeqTable];
     __shared__ int16_t norms[kSeqLanes][64];
     __shared__ uint16_t nexts[kSeqLanes][64];
     __shared__ uint64_t recs[kSeqLanes][kSeqFlush];
+    __shared__ __attribute__((aligned(16))) uint8_t win[kSeqLanes][kSeqWin + 16];
     __shared__ uint32_t llcode[36], mlcode[53];  // value | extra bits << 24
     __shared__ uint32_t s_n[kSeqLanes], s_i[kSeqLanes];
+    __shared__ int32_t s_wb[kSeqLanes];
     __shared__ uint64_t* s_out[kSeqLanes];
+    __shared__ const uint8_t* s_src[kSeqLanes];
+    __shared__ const uint8_t* s_flo[kSeqLanes];
+    __shared__ const uint8_t* s_fhi[kSeqLanes];
     __shared__ uint32_t s_active;
     const int lane = (int)threadIdx.x;
     if (lane < 36) llcode[lane] = kLLBase[lane] | ((uint32_t)kLLBits[lane] << 24);
@@ -432,20 +408,22 @@ __global__ void __launch_bounds__(64) k_zs_sequences(Launch L) {
         const uint32_t w = w0 + (uint32_t)lane;
         const bool mine = lane < kSeqLanes && w < total;
         Block* Bp = nullptr;
-        const DevFrame* Fp = nullptr;
         uint64_t* out = nullptr;
+        const uint8_t* sp = nullptr;  // the bitstream in global memory
+        const uint8_t* flo = nullptr;
+        const uint8_t* fhi = nullptr;
         uint32_t st = kOk, nseq = 0, i = 0;
-        GlobalBits r{};
+        LdsBits r{};
         int lg[3] = {0, 0, 0};
         uint32_t sll = 0, sof = 0, sml = 0, rep[3] = {0, 0, 0};
         uint64_t tll = 0, tml = 0;
         FseEntry* tl = tabs[lane < kSeqLanes ? lane : 0];
         if (mine) {
             const Work wk = L.seq_work[w];
-            Fp = &L.frames[wk.frame];
+            const DevFrame& F = L.frames[wk.frame];
             Bp = &L.blocks[(size_t)wk.frame * L.max_blocks + wk.block];
             const Block& B = *Bp;
-            const uint8_t* f = Fp->src;
+            const uint8_t* f = F.src;
             out = L.seq + (size_t)wk.frame * L.seq_cap + B.seq_out;
             nseq = B.nseq;
             const uint32_t end = B.src + B.size;
@@ -457,26 +435,61 @@ __global__ void __launch_bounds__(64) k_zs_sequences(Launch L) {
             rep[0] = rep_entry(0);
             rep[1] = rep_entry(1);
             rep[2] = rep_entry(2);
-            if (st == kOk) {
-                r.p = f + B.seq_src;
-                r.n = B.seq_size;
-                r.ok_lo = f;
-                r.ok_hi = f + end;
-                const uint32_t lastb = B.seq_size ? f[B.seq_src + B.seq_size - 1] : 0u;
-                if (lastb == 0) {
-                    st = kErrSequences;
-                } else {
-                    r.pos = 8 * (int32_t)(B.seq_size - 1) + highbit32(lastb);
-                    r.load();
+            sp = f + B.seq_src;
+            flo = f;
+            fhi = f + end;
+            const uint32_t lastb = B.seq_size ? load_byte(sp + B.seq_size - 1) : 0u;
+            if (st == kOk && lastb == 0) st = kErrSequences;
+            if (st == kOk) r.pos = 8 * (int32_t)(B.seq_size - 1) + highbit32(lastb);
+        }
+        bool first = true;
+        for (;;) {
+            // each lane's window: stream bytes [wb, wb + kSeqWin), wb word-aligned
+            // in global memory, reaching kSeqBack bytes below the read position
+            int32_t wb = 0;
+            const bool reading = mine && st == kOk;
+            if (reading) {
+                int32_t lo_b = ((r.pos + 7) >> 3) - 8 - kSeqBack;
+                lo_b = lo_b < 0 ? 0 : lo_b;
+                wb = lo_b - (int32_t)(reinterpret_cast<uintptr_t>(sp + lo_b) & 3);
+            }
+            if (lane < kSeqLanes) {
+                s_wb[lane] = wb;
+                s_src[lane] = reading ? sp : nullptr;
+                s_flo[lane] = flo;
+                s_fhi[lane] = fhi;
+            }
+            __syncthreads();
+            {
+                const int ln = lane >> 3, sub = lane & 7;  // 8 threads per lane's window
+                const uint8_t* src = s_src[ln];
+                if (src) {
+                    const uint8_t* a0 = src + s_wb[ln];
+                    const uint8_t* lo = s_flo[ln];
+                    const uint8_t* hi = s_fhi[ln];
+                    for (int j = sub; j < kSeqWin / 4; j += 8) {
+                        const uint8_t* a = a0 + 4 * j;
+                        uint32_t v = 0;
+                        if (a >= lo && a + 4 <= hi) {
+                            v = load_word(a);
+                        } else {
+                            for (int k = 0; k < 4; ++k)
+                                if (a + k >= lo && a + k < hi) v |= (uint32_t)load_byte(a + k) << (8 * k);
+                        }
+                        *reinterpret_cast<uint32_t*>(&win[ln][4 * j]) = v;
+                    }
+                }
+            }
+            __syncthreads();
+            uint32_t k = 0;
+            if (reading) {
+                r.p = win[lane] - wb;
+                r.load();
+                if (first) {
                     sll = r.read(lg[0]);
                     sof = r.read(lg[1]);
                     sml = r.read(lg[2]);
                 }
-            }
-        }
-        for (;;) {
-            uint32_t k = 0;
-            if (mine && st == kOk) {
                 const FseEntry* tll_ = tl;
                 const FseEntry* tof_ = tl + 512;
                 const FseEntry* tml_ = tl + 768;
@@ -486,7 +499,7 @@ __global__ void __launch_bounds__(64) k_zs_sequences(Launch L) {
                     const FseEntry ell = tll_[sll], eof = tof_[sof], eml = tml_[sml];
                     const uint32_t mc = mlcode[eml.sym], lc = llcode[ell.sym];
                     r.refill();
-                    const uint64_t ov = (1ull << eof.sym) + r.read(eof.sym);
+                    const uint32_t ov = (1u << eof.sym) + r.read(eof.sym);
                     const uint32_t ml = (mc & 0xffffff) + r.read(mc >> 24);
                     r.refill();
                     const uint32_t ll = (lc & 0xffffff) + r.read(lc >> 24);
@@ -494,15 +507,15 @@ __global__ void __launch_bounds__(64) k_zs_sequences(Launch L) {
                     // take history entry idx (idx from the code and ll == 0),
                     // 3 = entry 0 minus one, 4 = a new offset
                     const bool fresh = ov > 3;
-                    const uint32_t idx = fresh ? 4u : (uint32_t)ov - 1u + (ll == 0);
+                    const uint32_t idx = fresh ? 4u : ov - 1u + (ll == 0);
                     uint32_t m1;
                     const bool m1ok = rep_minus_one(rep[0], &m1);
                     const uint32_t off = idx == 0 ? rep[0]
                                          : idx == 1 ? rep[1]
                                          : idx == 2 ? rep[2]
                                          : idx == 3 ? m1
-                                                    : (uint32_t)(ov - 3);
-                    if ((fresh && ov - 3 >= (1ull << 27)) || (idx == 3 && !m1ok)) {
+                                                    : ov - 3;
+                    if ((fresh && ov - 3 >= (1u << 27)) || (idx == 3 && !m1ok)) {
                         st = kErrOffset;
                         break;
                     }
@@ -523,6 +536,7 @@ __global__ void __launch_bounds__(64) k_zs_sequences(Launch L) {
                 // the literal lengths only grow: one check per batch
                 if (tll > Bp->lit_size) st = kErrSequences;
             }
+            first = false;
             if (lane < kSeqLanes) {
                 s_n[lane] = k;
                 s_i[lane] = i;
