@@ -47,6 +47,20 @@ def _compile(args: list[str], verbose: bool) -> None:
         raise RuntimeError(f"hipcc failed ({res.returncode}):\n{res.stderr[-6000:]}")
 
 
+HOST_CHECK = PKG / "_build" / "zstd_host_check"
+
+
+def host_check(verbose: bool = False) -> Path:
+    """Compile tests/zstd_host_check.cpp (fw_zstd.h's format core on the host,
+    g++ with AddressSanitizer) into _build/."""
+    (PKG / "_build").mkdir(exist_ok=True)
+    rocm = Path(hipcc()).resolve().parent.parent
+    _compile(["g++", "-std=c++17", "-O1", "-g", "-fsanitize=address", "-fno-omit-frame-pointer",
+              "-D__HIP_PLATFORM_AMD__", "-I", str(rocm / "include"), "-I", str(CSRC),
+              str(ROOT / "tests" / "zstd_host_check.cpp"), "-o", str(HOST_CHECK)], verbose)
+    return HOST_CHECK
+
+
 def build(verbose: bool = False) -> Path:
     """Compile the host/stateless translation unit and one decode-kernel unit
     per token count in parallel, then link the shared library in place."""
@@ -70,6 +84,8 @@ def build(verbose: bool = False) -> Path:
     _compile([hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", *[str(o) for _, _, o in units], "-o", str(tmp)],
              verbose)
     os.replace(tmp, LIB)
+    # the zstd format core on the host under AddressSanitizer, for tests/test_zstd_host.py
+    host_check(verbose)
     # stand-alone C++ driver of the decode step (for profilers), next to the library
     drv = PKG / "fw_decode_bench"
     _compile([hipcc(), "-O2", "-std=c++17", *include, str(CSRC / "fw_decode_bench.cpp"), "-o", str(drv),
