@@ -655,7 +655,6 @@ struct ExecLds {
     uint32_t pend[kChunk / 32];
     uint32_t ready[kChunk / 32];
     uint64_t scan[kExecThreads / 64];
-    uint32_t flag;
     uint32_t err;
     uint8_t far[kFar];         // the chunk's match-source bytes from earlier blocks
 };
