@@ -111,9 +111,30 @@ def format_cases():
     return cases
 
 
+def pyarrow_cases():
+    # frames from another encoder: pyarrow's bundled libzstd (a newer release
+    # than the system's), when pyarrow is importable
+    try:
+        import pyarrow as pa
+    except ImportError:
+        return []
+    rng = np.random.default_rng(17)
+    w = bf16_weights(rng, 300_000).tobytes()
+    words = [b"expert ", b"router ", b"gate ", b"token "]
+    text = b"".join(words[i] for i in rng.integers(0, len(words), size=60_000))
+    out = []
+    for name, data, lvl in (("pa-weights-shuffled-1", fz.shuffle_bf16(w), 1), ("pa-weights-9", w, 9),
+                            ("pa-text-19", text, 19), ("pa-text-neg", text, -3)):
+        out.append((name, data, pa.Codec("zstd", compression_level=lvl).compress(data, asbytes=True)))
+    return out
+
+
 def test_format_features():
     cases = format_cases()
     frames = [fz.compress(data, **kw) for _, data, kw in cases]
+    extra = pyarrow_cases()
+    cases += [(name, data, {}) for name, data, _ in extra]
+    frames += [f for _, _, f in extra]
     for (_, data, _), f in zip(cases, frames):
         assert fz.decompress(f, len(data)) == data  # the frames are good
     st, out = run_decode(frames, [len(d) for _, d, _ in cases], False, max_frames=len(cases))

@@ -36,7 +36,14 @@ def cases():
             (b"", dict(level=3))]
     for n in (1, 17, 256, 1000, 4097, 131_073):
         out.append((bytes(((np.arange(n) * 7) & 0x3F).astype(np.uint8)), dict(level=3)))
-    return [(data, fz.compress(data, **kw)) for data, kw in out]
+    made = [(data, fz.compress(data, **kw)) for data, kw in out]
+    try:  # frames from another encoder: pyarrow's bundled libzstd
+        import pyarrow as pa
+        for data, lvl in ((fz.shuffle_bf16(weights), 1), (text, 19), (weights, -3)):
+            made.append((data, pa.Codec("zstd", compression_level=lvl).compress(data, asbytes=True)))
+    except ImportError:
+        pass
+    return made
 
 
 def write_cases(path, items):
