@@ -4,7 +4,10 @@
 // decoder's frame capacity; per chunk:
 //   k_zs_reset      clears the chunk's work-list counters (a kernel, not a
 //                   memset, so a captured graph replays it correctly);
-//   k_zs_index      one thread per frame: headers, block list, work lists;
+//   k_zs_walk       one thread per frame: frame and block headers;
+//   k_zs_parse      one thread per compressed block: its section headers;
+//   k_zs_link       one thread per frame: inherited tables, scratch offsets,
+//                   the work lists;
 //   k_zs_literals   one workgroup per Huffman literal section, a wave per
 //                   stream, every lane decoding a segment of it;
 //   k_zs_sequences  eight blocks with sequences per wave, a lane each;
@@ -62,7 +65,8 @@ struct Launch {
     Work* huf_work;  // [count * max_blocks] each
     Work* seq_work;
     Work* raw_work;      // raw and RLE blocks
-    uint32_t* counters;  // [0] Huffman work, [1] sequence work, [2] raw/RLE work
+    Work* parse_work;    // compressed blocks to parse
+    uint32_t* counters;  // [0] Huffman work, [1] sequence work, [2] raw/RLE work, [3] parse work
 };
 
 constexpr int kExecThreads = 512;
@@ -71,7 +75,7 @@ constexpr int kFar = 7168;    // LDS bytes for a chunk's sources in earlier bloc
 constexpr uint32_t kShort = 64;  // matches up to this long are copied by their own thread
 
 __global__ void k_zs_reset(uint32_t* counters) {
-    if (threadIdx.x < 3) counters[threadIdx.x] = 0;
+    if (threadIdx.x < 4) counters[threadIdx.x] = 0;
 }
 
 // A byte of global memory (a global, not flat, load).
@@ -92,21 +96,57 @@ __device__ __forceinline__ uint32_t load4(const uint8_t* q, const uint8_t* ok_lo
            ((uint32_t)load_byte(q + 3) << 24);
 }
 
-__global__ void __launch_bounds__(64) k_zs_index(Launch L) {
+// One thread per frame: the frame header and the block headers; the
+// compressed blocks go to the parse work list.
+__global__ void __launch_bounds__(64) k_zs_walk(Launch L) {
     const uint32_t f = blockIdx.x * 64 + threadIdx.x;
     if (f >= L.count) return;
     DevFrame& F = L.frames[f];
     Block* bl = L.blocks + (size_t)f * L.max_blocks;
     FrameInfo info;
-    uint32_t st = F.content > L.out_cap ? (uint32_t)kErrContentSize
-                                        : index_frame(F.src, F.size, F.content, bl, L.max_blocks, L.lit_cap,
-                                                      L.seq_cap, info);
+    const uint32_t st = F.content > L.out_cap ? (uint32_t)kErrContentSize
+                                              : walk_frame(F.src, F.size, F.content, bl, L.max_blocks, info);
     F.status = st;
-    F.err_block = info.err_block;
+    F.err_block = st == kOk ? 0 : info.err_block;
     F.nblocks = st == kOk ? info.nblocks : 0;
     if (st != kOk) return;
+    uint32_t nc = 0;
+    for (uint32_t b = 0; b < info.nblocks; ++b) nc += bl[b].type == 2;
+    uint32_t pb = nc ? atomicAdd(&L.counters[3], nc) : 0;
+    for (uint32_t b = 0; b < info.nblocks; ++b)
+        if (bl[b].type == 2) L.parse_work[pb++] = Work{f, b};
+}
+
+// One thread per compressed block: its literal and sequence section headers.
+__global__ void __launch_bounds__(64) k_zs_parse(Launch L) {
+    const uint32_t total = L.counters[3];
+    for (uint32_t w = blockIdx.x * 64 + threadIdx.x; w < total; w += gridDim.x * 64) {
+        const Work wk = L.parse_work[w];
+        const DevFrame& F = L.frames[wk.frame];
+        Block& B = L.blocks[(size_t)wk.frame * L.max_blocks + wk.block];
+        const uint32_t st = parse_block(F.src, B.src, B.size, B);
+        if (st != kOk) B.status = st;
+    }
+}
+
+// One thread per frame: the blocks linked in order (inherited tables,
+// scratch offsets), then the work lists of the decode passes.
+__global__ void __launch_bounds__(64) k_zs_link(Launch L) {
+    const uint32_t f = blockIdx.x * 64 + threadIdx.x;
+    if (f >= L.count) return;
+    DevFrame& F = L.frames[f];
+    if (F.status != kOk) return;
+    Block* bl = L.blocks + (size_t)f * L.max_blocks;
+    FrameInfo info;
+    const uint32_t st = link_frame(bl, F.nblocks, L.lit_cap, L.seq_cap, info);
+    if (st != kOk) {
+        F.status = st;
+        F.err_block = info.err_block;
+        F.nblocks = 0;
+        return;
+    }
     uint32_t nh = 0, ns = 0, nr = 0;
-    for (uint32_t b = 0; b < info.nblocks; ++b) {
+    for (uint32_t b = 0; b < F.nblocks; ++b) {
         Block& B = bl[b];
         B.rep_end[0] = rep_entry(0);
         B.rep_end[1] = rep_entry(1);
@@ -125,7 +165,7 @@ __global__ void __launch_bounds__(64) k_zs_index(Launch L) {
     }
     uint32_t hb = nh ? atomicAdd(&L.counters[0], nh) : 0, sb = ns ? atomicAdd(&L.counters[1], ns) : 0;
     uint32_t rb = nr ? atomicAdd(&L.counters[2], nr) : 0;
-    for (uint32_t b = 0; b < info.nblocks; ++b) {
+    for (uint32_t b = 0; b < F.nblocks; ++b) {
         const Block& B = bl[b];
         if (B.type != 2) {
             if (B.regen) L.raw_work[rb++] = Work{f, b};
@@ -135,6 +175,7 @@ __global__ void __launch_bounds__(64) k_zs_index(Launch L) {
         if (B.nseq) L.seq_work[sb++] = Work{f, b};
     }
 }
+
 
 constexpr uint32_t kLitStage = 32 * 1024;  // LDS copy of a block's Huffman streams (larger: read in place)
 
@@ -1106,8 +1147,8 @@ Decoder::Decoder(int device, size_t max_frames, uint64_t max_content) : device_(
         lit_ = dev_alloc<uint8_t>(max_frames * lit_cap_);
         seq_ = dev_alloc<uint64_t>(max_frames * seq_cap_ * sizeof(uint64_t));
         out_ = dev_alloc<uint8_t>(max_frames * out_cap_);
-        work_ = dev_alloc<void>(3 * max_frames * (size_t)max_blocks_ * sizeof(Work));
-        counters_ = dev_alloc<uint32_t>(3 * sizeof(uint32_t));
+        work_ = dev_alloc<void>(4 * max_frames * (size_t)max_blocks_ * sizeof(Work));
+        counters_ = dev_alloc<uint32_t>(4 * sizeof(uint32_t));
         hcheck(hipEventCreateWithFlags(&last_, hipEventDisableTiming), "hipEventCreate");
         hcheck(hipEventCreateWithFlags(&copied_, hipEventDisableTiming), "hipEventCreate");
         hcheck(hipFuncSetAttribute((const void*)k_zs_execute, hipFuncAttributeMaxDynamicSharedMemorySize,
@@ -1220,9 +1261,12 @@ bool Decoder::queue(const std::vector<FrameJob>& jobs, hipStream_t s, std::strin
         L.huf_work = static_cast<Work*>(work_);
         L.seq_work = static_cast<Work*>(work_) + max_frames_ * (size_t)max_blocks_;
         L.raw_work = static_cast<Work*>(work_) + 2 * max_frames_ * (size_t)max_blocks_;
+        L.parse_work = static_cast<Work*>(work_) + 3 * max_frames_ * (size_t)max_blocks_;
         L.counters = counters_;
         hipLaunchKernelGGL(k_zs_reset, dim3(1), dim3(64), 0, s, counters_);
-        hipLaunchKernelGGL(k_zs_index, dim3((count + 63) / 64), dim3(64), 0, s, L);
+        hipLaunchKernelGGL(k_zs_walk, dim3((count + 63) / 64), dim3(64), 0, s, L);
+        hipLaunchKernelGGL(k_zs_parse, dim3(grid_), dim3(64), 0, s, L);
+        hipLaunchKernelGGL(k_zs_link, dim3((count + 63) / 64), dim3(64), 0, s, L);
         hipLaunchKernelGGL(k_zs_literals, dim3(grid_), dim3(256), 0, s, L);
         hipLaunchKernelGGL(k_zs_sequences, dim3(grid_), dim3(64), 0, s, L);  // kSeqLanes blocks per workgroup
         hipLaunchKernelGGL(k_zs_layout, dim3((count + 63) / 64), dim3(64), 0, s, L);

@@ -62,7 +62,7 @@ class Decoder {
     uint8_t* lit_ = nullptr;
     uint64_t* seq_ = nullptr;
     uint8_t* out_ = nullptr;
-    void* work_ = nullptr;         // three work lists of max_frames * max_blocks entries
+    void* work_ = nullptr;         // four work lists of max_frames * max_blocks entries
     uint32_t* counters_ = nullptr;  // the work lists' lengths
     void* frames_ = nullptr;        // device frame records of the last call
     void* frames_host_ = nullptr;   // pinned staging of the frame records
