@@ -215,6 +215,44 @@ __device__ __forceinline__ uint64_t lds_load8(const uint8_t* q) {
     return sh ? (x >> sh) | ((uint64_t)w2 << (64 - sh)) : x;
 }
 
+// 8 bytes of an LDS buffer at q as a little-endian word without a branch:
+// three aligned word reads (the buffer is padded so they stay inside it)
+// joined by byte alignment.
+typedef const __attribute__((address_space(3))) uint8_t* LdsBytes;
+__device__ __forceinline__ uint64_t lds_word8(LdsBytes q) {
+    typedef const __attribute__((address_space(3))) uint32_t* lp;
+    const uint32_t sb = (uint32_t)(uintptr_t)q & 3u;
+    const lp a = (lp)(q - sb);
+    const uint32_t w0 = a[0], w1 = a[1], w2 = a[2];
+    const uint32_t lo = __builtin_amdgcn_alignbyte(w1, w0, sb), hi = __builtin_amdgcn_alignbyte(w2, w1, sb);
+    return (uint64_t)lo | ((uint64_t)hi << 32);
+}
+
+// Backward bit reader of the sequence pass: every refill reloads the word at
+// the read position (no branch), leaving at least 57 bits above `lo` (or
+// the stream's start), and a read is two shifts (zeros below the stream's
+// start; a malformed stream drives pos negative and fails the end check).
+struct SeqBits {
+    LdsBytes p;  // stream byte 0 in the lane's window (an LDS address)
+    int32_t pos, lo;
+    uint64_t c;
+    __device__ __forceinline__ void refill() {
+        int32_t b = ((pos + 7) >> 3) - 8;
+        b = b < 0 ? 0 : b;
+        lo = 8 * b;
+        c = lds_word8(p + b);
+    }
+    // nb <= 31 bits below pos
+    __device__ __forceinline__ uint32_t read(int nb) {
+        const int32_t sh = pos - lo - nb;
+        const uint32_t s1 = (uint32_t)(sh > 0 ? (sh < 63 ? sh : 63) : 0);
+        const uint32_t s2 = (uint32_t)(sh < 0 ? -sh : 0) & 63u;
+        const uint32_t v = (uint32_t)((c >> s1) << s2) & ((1u << nb) - 1u);
+        pos -= nb;
+        return v;
+    }
+};
+
 // Backward bit reader over a stream staged in LDS (at most 128 KB, so bit
 // positions fit 32 bits). refill() leaves at least 57 bits in the word (or
 // the stream's start), and reads between refills take no checks; a read past
@@ -454,7 +492,7 @@ __global__ void __launch_bounds__(64) k_zs_sequences(Launch L) {
         const uint8_t* flo = nullptr;
         const uint8_t* fhi = nullptr;
         uint32_t st = kOk, nseq = 0, i = 0;
-        LdsBits r{};
+        SeqBits r{};
         int lg[3] = {0, 0, 0};
         uint32_t sll = 0, sof = 0, sml = 0, rep[3] = {0, 0, 0};
         uint64_t tll = 0, tml = 0;
@@ -524,8 +562,8 @@ __global__ void __launch_bounds__(64) k_zs_sequences(Launch L) {
             __syncthreads();
             uint32_t k = 0;
             if (reading) {
-                r.p = win[lane] - wb;
-                r.load();
+                r.p = (LdsBytes)(win[lane]) - wb;
+                r.refill();
                 if (first) {
                     sll = r.read(lg[0]);
                     sof = r.read(lg[1]);
@@ -536,10 +574,14 @@ __global__ void __launch_bounds__(64) k_zs_sequences(Launch L) {
                 const FseEntry* tml_ = tl + 768;
                 // symbols are in range by construction (table_for: counts of
                 // at most kMaxSym[kind] symbols, RLE symbols checked)
+                // No branch in a step: the first refill goes out with the
+                // table reads, a failed offset is noted and ends the lane's
+                // batch, and the last sequence reads zero state bits.
+                bool bad = false;
                 for (; k < (uint32_t)kSeqFlush && i < nseq; ++k) {
+                    r.refill();
                     const FseEntry ell = tll_[sll], eof = tof_[sof], eml = tml_[sml];
                     const uint32_t mc = mlcode[eml.sym], lc = llcode[ell.sym];
-                    r.refill();
                     const uint32_t ov = (1u << eof.sym) + r.read(eof.sym);
                     const uint32_t ml = (mc & 0xffffff) + r.read(mc >> 24);
                     r.refill();
@@ -551,15 +593,13 @@ __global__ void __launch_bounds__(64) k_zs_sequences(Launch L) {
                     const uint32_t idx = fresh ? 4u : ov - 1u + (ll == 0);
                     uint32_t m1;
                     const bool m1ok = rep_minus_one(rep[0], &m1);
-                    const uint32_t off = idx == 0 ? rep[0]
-                                         : idx == 1 ? rep[1]
-                                         : idx == 2 ? rep[2]
-                                         : idx == 3 ? m1
-                                                    : ov - 3;
-                    if ((fresh && ov - 3 >= (1u << 27)) || (idx == 3 && !m1ok)) {
-                        st = kErrOffset;
-                        break;
-                    }
+                    // one of five by masks (a chain of selects on idx is
+                    // compiled to a switch, branches in a divergent loop)
+                    const uint32_t off = (rep[0] & (0u - (uint32_t)(idx == 0))) |
+                                         (rep[1] & (0u - (uint32_t)(idx == 1))) |
+                                         (rep[2] & (0u - (uint32_t)(idx == 2))) | (m1 & (0u - (uint32_t)(idx == 3))) |
+                                         ((ov - 3) & (0u - (uint32_t)(idx == 4)));
+                    bad |= (fresh && ov - 3 >= (1u << 27)) || (idx == 3 && !m1ok);
                     const uint32_t n1 = idx == 0 ? rep[1] : rep[0];
                     const uint32_t n2 = idx <= 1 ? rep[2] : rep[1];
                     rep[0] = off;
@@ -568,12 +608,12 @@ __global__ void __launch_bounds__(64) k_zs_sequences(Launch L) {
                     tll += ll;
                     tml += ml;
                     recs[lane][k] = seq_pack(ll, ml, off);
-                    if (++i < nseq) {
-                        sll = ell.base + r.read(ell.nb);
-                        sml = eml.base + r.read(eml.nb);
-                        sof = eof.base + r.read(eof.nb);
-                    }
+                    const bool more = ++i < nseq;
+                    sll = ell.base + r.read(more ? ell.nb : 0);
+                    sml = eml.base + r.read(more ? eml.nb : 0);
+                    sof = eof.base + r.read(more ? eof.nb : 0);
                 }
+                if (bad) st = kErrOffset;
                 // the literal lengths only grow: one check per batch
                 if (tll > Bp->lit_size) st = kErrSequences;
             }
@@ -596,7 +636,7 @@ __global__ void __launch_bounds__(64) k_zs_sequences(Launch L) {
             if (!s_active) break;
         }
         if (mine) {
-            if (st == kOk && nseq && r.pos > 0) st = kErrSequences;
+            if (st == kOk && nseq && r.pos != 0) st = kErrSequences;  // the stream ends exactly
             if (st == kOk && Bp->lit_size + tml > kBlockMax) st = kErrBlock;
             Bp->sum_ll = tll;
             Bp->regen = Bp->lit_size + tml;
