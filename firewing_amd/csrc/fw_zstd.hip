@@ -733,12 +733,16 @@ struct ExecLds {
     uint32_t off[kChunk];
     uint32_t rpre[kChunk];     // this round's ready match bytes before sequence i
     uint32_t fpre[kChunk];     // first byte of sequence i's earlier-block source in far
-    uint32_t pend[kChunk / 32];
+    // pending matches (a bit per sequence): pq[0] for the general rounds; the
+    // rounds of a chunk without shared-out matches rotate over all three
+    alignas(16) uint32_t pq[3][kChunk / 32];
     uint32_t ready[kChunk / 32];
     uint64_t scan[kExecThreads / 64];
     uint32_t err;
-    uint8_t far[kFar];         // the chunk's match-source bytes from earlier blocks
+    uint8_t far[kFar + 20];    // the chunk's match-source bytes from earlier blocks (+ room for the
+                               // word reads of a short match's source)
 };
+static_assert(sizeof(ExecLds) <= 160 * 1024, "the execute pass's LDS fits a workgroup");
 
 // exclusive prefix over the workgroup of a 64-bit value; *total = the sum
 __device__ uint64_t wg_scan(uint64_t v, uint64_t* tmp, uint64_t* total) {
@@ -827,15 +831,19 @@ __device__ void copy_literals(ExecLds& S, const Block& B, const uint8_t* litp, c
             const uint32_t r = load_byte(litp) * 0x01010101u;
             v[0] = v[1] = v[2] = v[3] = r;
         }
+        // the current sequence's literal end and output shift (byte j goes
+        // to shift + j) in registers: stores to obuf do not force re-reads
         int i = cnt ? last_le(S.lit, cnt, b) : 0;
+        uint32_t nxt = cnt ? S.lit[i + 1] : 0xffffffffu;
+        uint32_t shift = cnt ? S.mst[i] - nxt : tail_pos - j0;
         for (uint32_t j = b; j < e; ++j) {
             const uint8_t x = (uint8_t)(v[(j - a) >> 2] >> (8 * ((j - a) & 3)));
-            if (cnt) {
-                while (j >= S.lit[i + 1]) ++i;
-                S.obuf[S.mst[i] - (S.lit[i + 1] - j)] = x;
-            } else {
-                S.obuf[tail_pos + (j - j0)] = x;
+            while (j >= nxt) {
+                ++i;
+                nxt = S.lit[i + 1];
+                shift = S.mst[i] - nxt;
             }
+            S.obuf[shift + j] = x;
         }
     }
 }
@@ -883,7 +891,7 @@ __device__ void exec_block(ExecLds& S, const DevFrame& F, const Launch& L, uint3
         const uint64_t pre = wg_scan(mine, S.scan, &tot);
         const uint32_t lit_pre = lp + (uint32_t)(pre >> 32), out_pre = pos + (uint32_t)pre;
         uint32_t li = lit_pre, oi = out_pre;
-        if (t < kChunk / 32) S.pend[t] = 0;
+        if (t < kChunk / 32) S.pq[0][t] = S.pq[1][t] = 0;
         __syncthreads();
 #pragma unroll
         for (int q = 0; q < 2; ++q) {
@@ -895,7 +903,7 @@ __device__ void exec_block(ExecLds& S, const DevFrame& F, const Launch& L, uint3
                 S.off[i] = off[q];
                 if (ml[q]) {
                     if (off[q] == 0 || (uint64_t)off[q] > base + oi + ll[q]) atomicOr(&S.err, 1u);
-                    atomicOr(&S.pend[i >> 5], 1u << (i & 31));
+                    atomicOr(&S.pq[0][i >> 5], 1u << (i & 31));
                 }
             }
             li += ll[q];
@@ -987,30 +995,86 @@ __device__ void exec_block(ExecLds& S, const DevFrame& F, const Launch& L, uint3
         bool left[2] = {false, false};
 #pragma unroll
         for (int q = 0; q < 2; ++q) left[q] = (2 * t + q) < cnt && ml[q] > 0;
-        for (;;) {
+        // a match copied by its own thread (short, and its source in this
+        // block or in far)
+        auto copy_own = [&](int q) {
+            const uint32_t m = S.mst[2 * t + q], o = off[q], n = ml[q];
+            const int64_t src = srcq[q];
+            const uint32_t fb = S.fpre[2 * t + q];
+            if (o >= n && n <= 16 && (src >= 0 || (far_ok && src + n <= 0))) {
+                // not overlapping its output, the source wholly in this
+                // block or wholly staged in far (far[fb + k] = source byte
+                // k): the five aligned words around it in one round trip
+                // (bytes outside the source may change meanwhile; they are
+                // not used)
+                typedef const __attribute__((address_space(3))) uint32_t* lw;
+                const uint8_t* sbase = src >= 0 ? S.obuf : S.far;
+                const uint32_t s0 = src >= 0 ? (uint32_t)src : fb, sb = s0 & 3u;
+                const lw wp = (lw)(sbase + (s0 - sb));
+                const uint32_t w0 = wp[0], w1 = wp[1], w2 = wp[2], w3 = wp[3], w4 = wp[4];
+                const uint32_t v[4] = {__builtin_amdgcn_alignbyte(w1, w0, sb), __builtin_amdgcn_alignbyte(w2, w1, sb),
+                                       __builtin_amdgcn_alignbyte(w3, w2, sb), __builtin_amdgcn_alignbyte(w4, w3, sb)};
+#pragma unroll
+                for (int k = 0; k < 16; ++k)
+                    if ((uint32_t)k < n) S.obuf[m + k] = (uint8_t)(v[k >> 2] >> (8 * (k & 3)));
+            } else {
+                uint32_t k2 = 0;
+                for (uint32_t k = 0; k < n; ++k) {
+                    // source byte src + k2 (k2 = k mod o): in this block, or staged in far
+                    const int64_t si = src + k2;
+                    S.obuf[m + k] = si >= 0 ? S.obuf[si] : S.far[fb + k2];
+                    if (++k2 == o) k2 = 0;
+                }
+            }
+        };
+        // long matches, and earlier-block sources that did not fit in far, are
+        // shared out bytewise by the general rounds; a chunk without them runs
+        // rounds of one barrier each: a round reads pq[r % 3], marks the
+        // matches still to run in pq[(r + 1) % 3] and clears pq[(r + 2) % 3],
+        // which nobody reads in that round
+        bool shared_out = false;
+#pragma unroll
+        for (int q = 0; q < 2; ++q) shared_out |= left[q] && (ml[q] > kShort || (srcq[q] < 0 && !far_ok));
+        const bool general = __syncthreads_or(shared_out);
+        for (int r = 0; !general; ++r) {
+            const uint32_t* cur = S.pq[r % 3];
+            uint32_t* nxt = S.pq[(r + 1) % 3];
+            uint32_t* clr = S.pq[(r + 2) % 3];
+            bool rdy[2];
+#pragma unroll
+            for (int q = 0; q < 2; ++q) rdy[q] = left[q] && !any_pending(cur, clo[q], chi[q]);
+#pragma unroll
+            for (int q = 0; q < 2; ++q)
+                if (rdy[q]) copy_own(q);
+#pragma unroll
+            for (int q = 0; q < 2; ++q) {
+                if (left[q] && !rdy[q]) atomicOr(&nxt[(2 * t + q) >> 5], 1u << ((2 * t + q) & 31));
+                left[q] = left[q] && !rdy[q];
+            }
+            if (t < kChunk / 32) clr[t] = 0;
+            __syncthreads();
+            // the earliest pending match is always ready, so each round ends one
+            const uint4* nv = reinterpret_cast<const uint4*>(nxt);
+            uint32_t anyw = 0;
+#pragma unroll
+            for (int w = 0; w < kChunk / 128; ++w) {
+                const uint4 x = nv[w];
+                anyw |= x.x | x.y | x.z | x.w;
+            }
+            if (anyw == 0) break;
+        }
+        for (; general;) {
             bool rdy[2], coop[2];
 #pragma unroll
             for (int q = 0; q < 2; ++q) {
-                rdy[q] = left[q] && !any_pending(S.pend, clo[q], chi[q]);
+                rdy[q] = left[q] && !any_pending(S.pq[0], clo[q], chi[q]);
                 // long matches, and earlier-block sources that did not fit in
                 // far, are shared out bytewise; the rest stay with their thread
                 coop[q] = rdy[q] && (ml[q] > kShort || (srcq[q] < 0 && !far_ok));
             }
 #pragma unroll
-            for (int q = 0; q < 2; ++q) {
-                if (rdy[q] && !coop[q]) {
-                    const uint32_t m = S.mst[2 * t + q], o = off[q], n = ml[q];
-                    const int64_t src = srcq[q];
-                    const uint32_t fb = S.fpre[2 * t + q];
-                    uint32_t k2 = 0;
-                    for (uint32_t k = 0; k < n; ++k) {
-                        // source byte src + k2 (k2 = k mod o): in this block, or staged in far
-                        const int64_t si = src + k2;
-                        S.obuf[m + k] = si >= 0 ? S.obuf[si] : S.far[fb + k2];
-                        if (++k2 == o) k2 = 0;
-                    }
-                }
-            }
+            for (int q = 0; q < 2; ++q)
+                if (rdy[q] && !coop[q]) copy_own(q);
             if (__syncthreads_or(coop[0] || coop[1])) {
                 const uint64_t mlen = (coop[0] ? ml[0] : 0) + (coop[1] ? ml[1] : 0);
                 uint64_t rtot;
@@ -1051,7 +1115,7 @@ __device__ void exec_block(ExecLds& S, const DevFrame& F, const Launch& L, uint3
 #pragma unroll
             for (int q = 0; q < 2; ++q)
                 if (rdy[q]) {
-                    atomicAnd(&S.pend[(2 * t + q) >> 5], ~(1u << ((2 * t + q) & 31)));
+                    atomicAnd(&S.pq[0][(2 * t + q) >> 5], ~(1u << ((2 * t + q) & 31)));
                     left[q] = false;
                 }
             if (!__syncthreads_or(left[0] || left[1])) break;
