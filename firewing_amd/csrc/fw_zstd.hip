@@ -465,10 +465,17 @@ constexpr int kSeqWin = 400;     // a lane's window of its bitstream (>= kSeqBac
 // 47, literal-length extra bits + the three state updates <= 42). The wave
 // also writes the staged records out between batches.
 __global__ void __launch_bounds__(64) k_zs_sequences(Launch L) {
-    __shared__ FseEntry tabs[kSeqLanes][kSeqTable];
-    __shared__ int16_t norms[kSeqLanes][64];
-    __shared__ uint16_t nexts[kSeqLanes][64];
-    __shared__ uint64_t recs[kSeqLanes][kSeqFlush];
+    // two-byte table entries (build_fse16) and the table build's counts
+    // sharing the record staging: 3.2 KB of LDS a block, so that six
+    // workgroups fit a CU and a 256-frame call's blocks all run at once
+    __shared__ uint16_t tabs[kSeqLanes][kSeqTable];
+    __shared__ union {
+        struct {
+            int16_t norm[64];
+            uint16_t next[64];
+        } b;
+        uint64_t recs[kSeqFlush];
+    } lane_lds[kSeqLanes];
     __shared__ __attribute__((aligned(16))) uint8_t win[kSeqLanes][kSeqWin + 16];
     __shared__ uint32_t llcode[36], mlcode[53];  // value | extra bits << 24
     __shared__ uint32_t s_n[kSeqLanes], s_i[kSeqLanes];
@@ -496,7 +503,7 @@ __global__ void __launch_bounds__(64) k_zs_sequences(Launch L) {
         int lg[3] = {0, 0, 0};
         uint32_t sll = 0, sof = 0, sml = 0, rep[3] = {0, 0, 0};
         uint64_t tll = 0, tml = 0;
-        FseEntry* tl = tabs[lane < kSeqLanes ? lane : 0];
+        uint16_t* tl = tabs[lane < kSeqLanes ? lane : 0];
         if (mine) {
             const Work wk = L.seq_work[w];
             const DevFrame& F = L.frames[wk.frame];
@@ -508,7 +515,7 @@ __global__ void __launch_bounds__(64) k_zs_sequences(Launch L) {
             const uint32_t end = B.src + B.size;
             const int off3[3] = {0, 512, 768};
             for (int k = 0; k < 3 && st == kOk; ++k) {
-                lg[k] = table_for(f, end, B.table[k], k, tl + off3[k], norms[lane], nexts[lane]);
+                lg[k] = table_for16(f, end, B.table[k], k, tl + off3[k], lane_lds[lane].b.norm, lane_lds[lane].b.next);
                 if (lg[k] < 0) st = kErrFse;
             }
             rep[0] = rep_entry(0);
@@ -569,9 +576,9 @@ __global__ void __launch_bounds__(64) k_zs_sequences(Launch L) {
                     sof = r.read(lg[1]);
                     sml = r.read(lg[2]);
                 }
-                const FseEntry* tll_ = tl;
-                const FseEntry* tof_ = tl + 512;
-                const FseEntry* tml_ = tl + 768;
+                const uint16_t* tll_ = tl;
+                const uint16_t* tof_ = tl + 512;
+                const uint16_t* tml_ = tl + 768;
                 // symbols are in range by construction (table_for: counts of
                 // at most kMaxSym[kind] symbols, RLE symbols checked)
                 // No branch in a step: the first refill goes out with the
@@ -580,9 +587,12 @@ __global__ void __launch_bounds__(64) k_zs_sequences(Launch L) {
                 bool bad = false;
                 for (; k < (uint32_t)kSeqFlush && i < nseq; ++k) {
                     r.refill();
-                    const FseEntry ell = tll_[sll], eof = tof_[sof], eml = tml_[sml];
-                    const uint32_t mc = mlcode[eml.sym], lc = llcode[ell.sym];
-                    const uint32_t ov = (1u << eof.sym) + r.read(eof.sym);
+                    uint32_t ll_sym, ll_nb, ll_base, of_sym, of_nb, of_base, ml_sym, ml_nb, ml_base;
+                    fse16_unpack(tll_[sll], lg[0], &ll_sym, &ll_nb, &ll_base);
+                    fse16_unpack(tof_[sof], lg[1], &of_sym, &of_nb, &of_base);
+                    fse16_unpack(tml_[sml], lg[2], &ml_sym, &ml_nb, &ml_base);
+                    const uint32_t mc = mlcode[ml_sym], lc = llcode[ll_sym];
+                    const uint32_t ov = (1u << of_sym) + r.read(of_sym);
                     const uint32_t ml = (mc & 0xffffff) + r.read(mc >> 24);
                     r.refill();
                     const uint32_t ll = (lc & 0xffffff) + r.read(lc >> 24);
@@ -607,11 +617,11 @@ __global__ void __launch_bounds__(64) k_zs_sequences(Launch L) {
                     rep[2] = n2;
                     tll += ll;
                     tml += ml;
-                    recs[lane][k] = seq_pack(ll, ml, off);
+                    lane_lds[lane].recs[k] = seq_pack(ll, ml, off);
                     const bool more = ++i < nseq;
-                    sll = ell.base + r.read(more ? ell.nb : 0);
-                    sml = eml.base + r.read(more ? eml.nb : 0);
-                    sof = eof.base + r.read(more ? eof.nb : 0);
+                    sll = ll_base + r.read(more ? (int)ll_nb : 0);
+                    sml = ml_base + r.read(more ? (int)ml_nb : 0);
+                    sof = of_base + r.read(more ? (int)of_nb : 0);
                 }
                 if (bad) st = kErrOffset;
                 // the literal lengths only grow: one check per batch
@@ -630,7 +640,7 @@ __global__ void __launch_bounds__(64) k_zs_sequences(Launch L) {
             for (int q = lane; q < kSeqLanes * kSeqFlush; q += 64) {
                 const int ln = q / kSeqFlush, kk = q % kSeqFlush;
                 const uint32_t nl = s_n[ln];
-                if ((uint32_t)kk < nl) s_out[ln][s_i[ln] - nl + kk] = recs[ln][kk];
+                if ((uint32_t)kk < nl) s_out[ln][s_i[ln] - nl + kk] = lane_lds[ln].recs[kk];
             }
             __syncthreads();
             if (!s_active) break;

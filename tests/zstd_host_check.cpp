@@ -104,6 +104,22 @@ uint32_t decode(const std::vector<uint8_t>& fr, uint64_t content, std::vector<ui
             SeqTables T;
             for (int k = 0; k < 3; ++k) {
                 const int lg = table_for(f, B.src + B.size, B.table[k], k, t, norm, next);
+                // the GPU's two-byte tables (build_fse16) fail alike and unpack
+                // to the same entries
+                uint16_t t16[512];
+                const int lg16 = table_for16(f, B.src + B.size, B.table[k], k, t16, norm, next);
+                if (lg16 != lg) {
+                    std::fprintf(stderr, "table_for16 log %d, table_for %d\n", lg16, lg);
+                    std::abort();
+                }
+                for (int u = 0; lg >= 0 && u < (1 << lg); ++u) {
+                    uint32_t sym, nb, base;
+                    fse16_unpack(t16[u], lg, &sym, &nb, &base);
+                    if (sym != t[u].sym || nb != t[u].nb || base != t[u].base) {
+                        std::fprintf(stderr, "table_for16 entry %d differs\n", u);
+                        std::abort();
+                    }
+                }
                 if (lg < 0 || !seq_entries(t, lg, k, se[k])) return kErrFse;
                 T.t[k] = se[k];
                 T.log[k] = lg;
