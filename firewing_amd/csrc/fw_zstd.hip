@@ -189,30 +189,30 @@ __device__ const uint8_t* stage_bytes(uint8_t* lds, const uint8_t* g, uint32_t n
     const uint32_t phase = (uint32_t)(g - a0);
     const uint32_t words = (phase + n + 3) / 4;
     uint32_t* dst = reinterpret_cast<uint32_t*>(lds);
-    for (uint32_t w = threadIdx.x; w < words; w += threads) {
-        const uint8_t* a = a0 + 4 * w;
-        uint32_t v;
-        if (a >= ok_lo && a + 4 <= ok_hi) {
-            v = load_word(a);
-        } else {
-            v = 0;
-            for (int k = 0; k < 4; ++k)
-                if (a + k >= ok_lo && a + k < ok_hi) v |= (uint32_t)load_byte(a + k) << (8 * k);
+    // eight words a thread in flight, then their stores (one word at a time
+    // would wait a memory latency per word)
+    for (uint32_t w0 = threadIdx.x; w0 < words; w0 += 8 * (uint32_t)threads) {
+        uint32_t v[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+            const uint32_t w = w0 + (uint32_t)(u * threads);
+            const uint8_t* a = a0 + 4 * w;
+            v[u] = (w < words && a >= ok_lo && a + 4 <= ok_hi) ? load_word(a) : 0u;
         }
-        dst[w] = v;
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+            const uint32_t w = w0 + (uint32_t)(u * threads);
+            if (w >= words) break;
+            const uint8_t* a = a0 + 4 * w;
+            if (!(a >= ok_lo && a + 4 <= ok_hi)) {
+                // a frame edge word: its bytes inside the frame
+                for (int k = 0; k < 4; ++k)
+                    if (a + k >= ok_lo && a + k < ok_hi) v[u] |= (uint32_t)load_byte(a + k) << (8 * k);
+            }
+            dst[w] = v[u];
+        }
     }
     return lds + phase;
-}
-
-// 8 bytes of an LDS buffer at q as a little-endian word (three aligned word
-// reads; the buffer is padded so they stay inside it).
-__device__ __forceinline__ uint64_t lds_load8(const uint8_t* q) {
-    typedef const __attribute__((address_space(3))) uint32_t* lp;
-    const uint8_t* a = reinterpret_cast<const uint8_t*>(reinterpret_cast<uintptr_t>(q) & ~uintptr_t(3));
-    const uint32_t w0 = *(lp)(a), w1 = *(lp)(a + 4), w2 = *(lp)(a + 8);
-    const uint32_t sh = 8u * (uint32_t)(q - a);
-    const uint64_t x = (uint64_t)w0 | ((uint64_t)w1 << 32);
-    return sh ? (x >> sh) | ((uint64_t)w2 << (64 - sh)) : x;
 }
 
 // 8 bytes of an LDS buffer at q as a little-endian word without a branch:
@@ -242,6 +242,13 @@ struct SeqBits {
         lo = 8 * b;
         c = lds_word8(p + b);
     }
+    // nb <= 31 bits below pos, not consumed
+    __device__ __forceinline__ uint32_t peek(int nb) const {
+        const int32_t sh = pos - lo - nb;
+        const uint32_t s1 = (uint32_t)(sh > 0 ? (sh < 63 ? sh : 63) : 0);
+        const uint32_t s2 = (uint32_t)(sh < 0 ? -sh : 0) & 63u;
+        return (uint32_t)((c >> s1) << s2) & ((1u << nb) - 1u);
+    }
     // nb <= 31 bits below pos
     __device__ __forceinline__ uint32_t read(int nb) {
         const int32_t sh = pos - lo - nb;
@@ -253,48 +260,15 @@ struct SeqBits {
     }
 };
 
-// Backward bit reader over a stream staged in LDS (at most 128 KB, so bit
-// positions fit 32 bits). refill() leaves at least 57 bits in the word (or
-// the stream's start), and reads between refills take no checks; a read past
-// the stream's start (a malformed stream) returns garbage, never touches
-// memory outside the buffer, and drives pos negative.
-struct LdsBits {
-    const uint8_t* p;
-    int32_t pos, lo;
-    uint64_t c;
-    __device__ __forceinline__ void load() {
-        int32_t b = ((pos + 7) >> 3) - 8;
-        b = b < 0 ? 0 : b;
-        lo = 8 * b;
-        c = lds_load8(p + b);
-    }
-    __device__ __forceinline__ void seek(int32_t at) {
-        pos = at;
-        load();
-    }
-    __device__ __forceinline__ void refill() {
-        if (pos - lo < 57 && lo > 0) load();
-    }
-    // nb <= 32 bits below pos (zeros below the stream's start)
-    __device__ __forceinline__ uint32_t peek(int nb) const {
-        const int32_t sh = pos - lo - nb;
-        const uint64_t v = sh >= 0 ? (c >> (sh & 63)) : (c << ((-sh) & 63));
-        return (uint32_t)v & (uint32_t)((1ull << nb) - 1);
-    }
-    __device__ __forceinline__ uint32_t read(int nb) {
-        const uint32_t v = peek(nb);
-        pos -= nb;
-        return v;
-    }
-};
-
 // One stream of `count` Huffman symbols decoded by a whole wave: lane l
 // starts at bit pos0 - l*S (S = pos0/64 rounded up) as if a codeword began
 // there and decodes until it passes its segment's end. A prefix code
 // resynchronises within a few codewords, so once lane l-1's true end is
 // known, lane l redoes its segment from there only if its guess differed,
 // and the fix travels up the lanes until nothing changes. Counts then give
-// each lane's output offset and a last pass writes the symbols.
+// each lane's output offset and a last pass writes the symbols. For a
+// stream read in place (too large to stage); staged streams take
+// huf_stream_wave_lds.
 template <class Mem>
 __device__ bool huf_stream_wave(const uint8_t* s, uint32_t size, const uint8_t* ok_lo, const uint8_t* ok_hi,
                                 const uint16_t* dt, int log, uint32_t count, uint8_t* out) {
@@ -317,37 +291,16 @@ __device__ bool huf_stream_wave(const uint8_t* s, uint32_t size, const uint8_t* 
         cnt = 0;
         end = from;
         if (from <= stop) return true;
-        if constexpr (std::is_same<Mem, LdsMem>::value) {
-            // up to 4 codewords (4 x 12 bits) per refill
-            LdsBits q{s, (int32_t)from, 0, 0};
-            q.load();
-            const int32_t st = (int32_t)stop;
-            while (q.pos > st) {
-                q.refill();
-#pragma unroll
-                for (int u = 0; u < 4; ++u) {
-                    if (q.pos <= st) break;
-                    if (cnt >= count) return false;
-                    const uint16_t e = dt[q.peek(log)];
-                    if (dst) dst[cnt] = (uint8_t)e;
-                    q.pos -= e >> 8;
-                    ++cnt;
-                }
-            }
-            end = q.pos;
-            return true;
-        } else {
-            r.seek(from);
-            while (r.pos > stop) {
-                if (cnt >= count) return false;
-                const uint16_t e = dt[r.peek(log)];
-                if (dst) dst[cnt] = (uint8_t)e;
-                r.skip(e >> 8);
-                ++cnt;
-            }
-            end = r.pos;
-            return true;
+        r.seek(from);
+        while (r.pos > stop) {
+            if (cnt >= count) return false;
+            const uint16_t e = dt[r.peek(log)];
+            if (dst) dst[cnt] = (uint8_t)e;
+            r.skip(e >> 8);
+            ++cnt;
         }
+        end = r.pos;
+        return true;
     };
     uint32_t c = 0;
     int64_t e = 0;
@@ -384,6 +337,148 @@ __device__ bool huf_stream_wave(const uint8_t* s, uint32_t size, const uint8_t* 
     return true;
 }
 
+// huf_stream_wave for a stream staged in LDS. A lane's first pass from its
+// guessed start remembers the first kHufRec codeword boundaries it passes; a
+// lane whose guess was wrong decodes from its true start only until it lands
+// on its guessed start or one of those boundaries (a prefix code
+// resynchronises within a few codewords) and takes the first pass's count
+// from there, else it decodes its whole segment again. Steps have no
+// branch: the bit word is reloaded at every group of four codewords (4 x 12
+// bits <= 57) and a lane past its segment's end stops moving. Every step
+// consumes at least one bit (a valid table has no zero-length code), so
+// each loop ends.
+constexpr int kHufRec = 8;
+__device__ bool huf_stream_wave_lds(LdsBytes s, uint32_t size, const uint16_t* dt, int log, uint32_t count,
+                                    uint8_t* out) {
+    const int lane = (int)(threadIdx.x & 63);
+    if (size == 0) return false;
+    const uint32_t lastb = s[size - 1];
+    if (lastb == 0) return false;
+    const int32_t pos0 = 8 * (int32_t)(size - 1) + highbit32(lastb);
+    const int32_t S = (pos0 + 63) / 64;
+    int32_t stop = pos0 - (lane + 1) * S;
+    if (stop < 0) stop = 0;
+    int32_t p = pos0 - lane * S;
+    if (p < 0) p = 0;
+    // the symbols from `from` down to stop (count only); q.pos ends at or below stop
+    auto rest = [&](SeqBits& q, uint32_t cnt) -> uint32_t {
+        while (q.pos > stop) {
+            q.refill();
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                const bool live = q.pos > stop;
+                const uint32_t e = dt[q.peek(log)];
+                q.pos -= live ? max((int32_t)(e >> 8), 1) : 0;
+                cnt += live ? 1u : 0u;
+            }
+        }
+        return cnt;
+    };
+    // first pass
+    const int32_t p1 = p;
+    int32_t rec[kHufRec];
+    uint32_t c1;
+    int32_t e1;
+    {
+        SeqBits q{s, p, 0, 0};
+        uint32_t cnt = 0;
+#pragma unroll
+        for (int g = 0; g < kHufRec / 4; ++g) {
+            q.refill();
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                const bool live = q.pos > stop;
+                const uint32_t e = dt[q.peek(log)];
+                q.pos -= live ? max((int32_t)(e >> 8), 1) : 0;
+                cnt += live ? 1u : 0u;
+                rec[4 * g + u] = live ? q.pos : INT32_MAX;  // INT32_MAX: no boundary (never a position)
+            }
+        }
+        c1 = rest(q, cnt);
+        e1 = q.pos;
+    }
+    uint32_t c = c1;
+    int32_t e = e1;
+    bool synced = false;
+    for (int it = 0; it <= 64; ++it) {
+        const int32_t tr = __shfl_up(e, 1);
+        const int32_t t = lane == 0 ? pos0 : tr;
+        const bool redo = t != p;
+        if (!__any(redo)) {
+            synced = true;
+            break;
+        }
+        if (redo) {
+            p = t;
+            // position x on the first pass's path: the symbols it has left
+            auto on_path = [&](int32_t x, uint32_t* left) -> bool {
+                bool hit = x == p1;
+                uint32_t l = c1;
+#pragma unroll
+                for (int k = 0; k < kHufRec; ++k) {
+                    const bool h = x == rec[k];
+                    l = h ? c1 - (uint32_t)(k + 1) : l;
+                    hit = hit || h;
+                }
+                *left = l;
+                return hit;
+            };
+            SeqBits q{s, t, 0, 0};
+            uint32_t j = 0, left = 0;
+            bool found = on_path(t, &left);
+#pragma unroll
+            for (int g = 0; g < kHufRec / 4; ++g) {
+                q.refill();
+#pragma unroll
+                for (int u = 0; u < 4; ++u) {
+                    const bool live = !found && q.pos > stop;
+                    const uint32_t en = dt[q.peek(log)];
+                    q.pos -= live ? max((int32_t)(en >> 8), 1) : 0;
+                    j += live ? 1u : 0u;
+                    uint32_t l2;
+                    const bool h = live && on_path(q.pos, &l2);
+                    left = h ? l2 : left;
+                    found = found || h;
+                }
+            }
+            if (found) {
+                c = j + left;
+                e = e1;
+            } else {
+                c = rest(q, j);
+                e = q.pos;
+            }
+        }
+    }
+    // exclusive prefix of the counts
+    uint32_t x = c;
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) {
+        const uint32_t y = __shfl_up(x, d);
+        if (lane >= d) x += y;
+    }
+    const uint32_t total = __shfl(x, 63);
+    const uint32_t base = x - c;
+    const int32_t last_end = __shfl(e, 63);
+    if (!(synced && total == count && last_end == 0)) return false;
+    // final pass: the lane's c symbols from p
+    SeqBits q{s, p, 0, 0};
+    uint8_t* dst = out + base;
+    uint32_t cnt = 0;
+    while (q.pos > stop && cnt < c) {
+        q.refill();
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const bool live = q.pos > stop && cnt < c;
+            const uint32_t en = dt[q.peek(log)];
+            if (live) dst[cnt] = (uint8_t)en;
+            q.pos -= live ? max((int32_t)(en >> 8), 1) : 0;
+            cnt += live ? 1u : 0u;
+        }
+    }
+    return true;
+}
+
 // One workgroup per Huffman literal section: thread 0 builds the decoding
 // table in LDS, the streams are copied into LDS when they fit, and wave k
 // decodes stream k.
@@ -394,7 +489,10 @@ __global__ void __launch_bounds__(256) k_zs_literals(Launch L) {
     __shared__ int16_t norm[256];
     __shared__ uint16_t next[256];
     __shared__ __attribute__((aligned(16))) uint8_t stage[kLitStage + 16];
-    __shared__ int s_log;
+    __shared__ uint8_t hdesc[128];  // the tree description (at most 128 bytes)
+    __shared__ uint16_t s_carry[4];
+    __shared__ uint16_t s_wcount[4][kMaxHufBits + 1];  // symbols of each weight, per wave
+    __shared__ int s_log, s_nsym;
     __shared__ uint32_t s_bad;
     const int wave = (int)(threadIdx.x >> 6);
     const uint32_t total = L.counters[0];
@@ -408,27 +506,74 @@ __global__ void __launch_bounds__(256) k_zs_literals(Launch L) {
         const uint32_t span = B.stream_off[B.nstreams - 1] + B.stream_size[B.nstreams - 1] - s0;
         const bool staged = span + 8 <= kLitStage;
         const uint8_t* sbase = staged ? stage_bytes(stage, F.src + s0, span, ok_lo, ok_hi, 256) : F.src + s0;
+        // the description copied to LDS: thread 0's serial weight decoding
+        // reads it there (an empty readable window sends every read of the
+        // bit readers down their byte path, which LDS serves)
+        const uint32_t dn = (uint32_t)min<uint64_t>(sizeof(hdesc), F.size - B.huf_desc);
+        if (threadIdx.x < dn) hdesc[threadIdx.x] = load_byte(F.src + B.huf_desc + threadIdx.x);
+        __syncthreads();
         if (threadIdx.x == 0) {
             s_bad = 0;
             int log = 0;
-            const int nsym = huf_weights(F.src + B.huf_desc, (uint32_t)(F.size - B.huf_desc), wt, &log, ft, norm,
-                                         next, ok_lo, ok_hi);
-            if (nsym) {
-                uint32_t start[kMaxHufBits + 2];
-                huf_rank_starts(wt, nsym, start);
-                for (int sy = 0; sy < nsym; ++sy) {
-                    const int wgt = wt[sy];
-                    if (!wgt) continue;
-                    const uint32_t len = (1u << wgt) >> 1;
-                    const uint16_t e = huf_entry(sy, wgt, log);
-                    for (uint32_t i = 0; i < len; ++i) dt[start[wgt] + i] = e;
-                    start[wgt] += len;
-                }
-            }
+            const int nsym = huf_weights(hdesc, dn, wt, &log, ft, norm, next, nullptr, nullptr);
             s_log = nsym ? log : -1;
+            s_nsym = nsym;
         }
         __syncthreads();
         const int log = s_log;
+        if (log >= 0) {
+            // The table in parallel: zeros, then each symbol's entry at its
+            // range start (an entry is never 0: its bit count is >= 1), then
+            // every entry takes the last range start at or before it (a
+            // workgroup scan of "last nonzero" over contiguous pieces).
+            const int size = 1 << log, nsym = s_nsym, t = (int)threadIdx.x, lane = t & 63;
+            for (int u = t; u < size; u += 256) dt[u] = 0;
+            // symbol t's range (weights ascending, symbols ascending within a
+            // weight): its rank among the symbols of its weight from a ballot
+            // per weight, the weight's first entry from the weights' counts
+            const int mw = t < nsym ? wt[t] : 0;
+            uint32_t rank = 0;
+            for (int w1 = 1; w1 <= kMaxHufBits; ++w1) {
+                const uint64_t m = __ballot(mw == w1);
+                if (lane == 0) s_wcount[wave][w1] = (uint16_t)__popcll(m);
+                if (mw == w1) rank = (uint32_t)__popcll(m & ((1ull << lane) - 1));
+            }
+            __syncthreads();
+            if (mw) {
+                uint32_t first = 0;
+                for (int w1 = 1; w1 <= kMaxHufBits; ++w1) {
+                    const uint32_t n = (uint32_t)s_wcount[0][w1] + s_wcount[1][w1] + s_wcount[2][w1] + s_wcount[3][w1];
+                    if (w1 < mw) first += n * ((1u << w1) >> 1);
+                }
+                for (int w2 = 0; w2 < wave; ++w2) rank += s_wcount[w2][mw];
+                dt[first + rank * ((1u << mw) >> 1)] = huf_entry(t, mw, log);
+            }
+            __syncthreads();
+            const int per = (size + 255) / 256, u0 = min(t * per, size), u1 = min(u0 + per, size);
+            uint32_t last = 0;
+            for (int u = u0; u < u1; ++u)
+                if (dt[u]) last = dt[u];
+            uint32_t x = last;
+#pragma unroll
+            for (int d = 1; d < 64; d <<= 1) {
+                const uint32_t y = (uint32_t)__shfl_up((int)x, d);
+                if (lane >= d && x == 0) x = y;
+            }
+            if (lane == 63) s_carry[wave] = (uint16_t)x;
+            uint32_t before = (uint32_t)__shfl_up((int)x, 1);
+            if (lane == 0) before = 0;
+            __syncthreads();
+            for (int w2 = wave - 1; w2 >= 0 && before == 0; --w2) before = s_carry[w2];
+            uint32_t cur = before;
+            for (int u = u0; u < u1; ++u) {
+                const uint32_t e = dt[u];
+                if (e)
+                    cur = e;
+                else
+                    dt[u] = (uint16_t)cur;
+            }
+            __syncthreads();
+        }
         if (log < 0) {
             if (threadIdx.x == 0) B.status = kErrHuffman;
         } else if (wave < (int)B.nstreams) {
@@ -438,8 +583,7 @@ __global__ void __launch_bounds__(256) k_zs_literals(Launch L) {
             const uint32_t off = B.stream_off[wave] - s0;
             bool ok;
             if (staged)
-                ok = huf_stream_wave<LdsMem>(sbase + off, B.stream_size[wave], stage, stage + kLitStage + 16, dt,
-                                             log, cnt, o);
+                ok = huf_stream_wave_lds((LdsBytes)(sbase + off), B.stream_size[wave], dt, log, cnt, o);
             else
                 ok = huf_stream_wave<GlobalMem>(sbase + off, B.stream_size[wave], ok_lo, ok_hi, dt, log, cnt, o);
             if (!ok && (threadIdx.x & 63) == 0) s_bad = 1;
@@ -553,16 +697,27 @@ __global__ void __launch_bounds__(64) k_zs_sequences(Launch L) {
                     const uint8_t* a0 = src + s_wb[ln];
                     const uint8_t* lo = s_flo[ln];
                     const uint8_t* hi = s_fhi[ln];
-                    for (int j = sub; j < kSeqWin / 4; j += 8) {
+                    // every word of this thread in flight, then the stores (a
+                    // word at a time would wait a memory latency per word)
+                    constexpr int kPer = (kSeqWin / 4 + 7) / 8;
+                    uint32_t v[kPer];
+#pragma unroll
+                    for (int u = 0; u < kPer; ++u) {
+                        const int j = sub + 8 * u;
                         const uint8_t* a = a0 + 4 * j;
-                        uint32_t v = 0;
-                        if (a >= lo && a + 4 <= hi) {
-                            v = load_word(a);
-                        } else {
+                        v[u] = (j < kSeqWin / 4 && a >= lo && a + 4 <= hi) ? load_word(a) : 0u;
+                    }
+#pragma unroll
+                    for (int u = 0; u < kPer; ++u) {
+                        const int j = sub + 8 * u;
+                        if (j >= kSeqWin / 4) break;
+                        const uint8_t* a = a0 + 4 * j;
+                        if (!(a >= lo && a + 4 <= hi)) {
+                            // a frame edge word: its bytes inside the frame
                             for (int k = 0; k < 4; ++k)
-                                if (a + k >= lo && a + k < hi) v |= (uint32_t)load_byte(a + k) << (8 * k);
+                                if (a + k >= lo && a + k < hi) v[u] |= (uint32_t)load_byte(a + k) << (8 * k);
                         }
-                        *reinterpret_cast<uint32_t*>(&win[ln][4 * j]) = v;
+                        *reinterpret_cast<uint32_t*>(&win[ln][4 * j]) = v[u];
                     }
                 }
             }
