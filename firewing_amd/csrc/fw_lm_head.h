@@ -132,13 +132,15 @@ __global__ void __launch_bounds__(256) k_lm_topk_chunks(const uint16_t* __restri
 // candidates. Candidate p (= c * k + r) gets the key key16 << 16 | (0xffff - p):
 // among equal values a lower p is a lower chunk, or the same chunk and a lower
 // rank, so a lower vocabulary index. Writes ids (c * kTopkChunk + position)
-// and bf16 values in rank order.
+// and bf16 values in rank order. kPerLane candidates a lane: n <= 256 *
+// kPerLane (the launch takes the smallest of 8, 16, 32 that holds n; the
+// lanes' sorts cost kPerLane^2 / 2 compare-exchanges).
+template <int kPerLane>
 __global__ void __launch_bounds__(256) k_lm_topk_merge(const uint16_t* __restrict__ key16,
                                                         const uint16_t* __restrict__ pos, int n, int k,
                                                         int32_t* __restrict__ ids, uint16_t* __restrict__ values) {
     __shared__ uint32_t lists[4 * 64];
     __shared__ uint32_t best[64];
-    constexpr int kPerLane = 32;  // n <= 4 * 64 * 32 = 8,192
     const int t = (int)blockIdx.x;
     const int w = (int)threadIdx.x / kWave, lane = lane_id();
     const uint16_t* kk = key16 + (size_t)t * n;

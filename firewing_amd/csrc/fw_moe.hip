@@ -2307,8 +2307,17 @@ void queue_lm_head(firewing_hip_context* c, const uint16_t* x, int T, int k, uin
     hipLaunchKernelGGL(k_lm_topk_chunks, dim3((unsigned)chunks, (unsigned)T), dim3(256), 0, s, out, V, k, m.cand_key,
                        m.cand_pos);
     check(hipGetLastError(), "k_lm_topk_chunks launch");
-    hipLaunchKernelGGL(k_lm_topk_merge, dim3((unsigned)T), dim3(256), 0, s, m.cand_key, m.cand_pos, chunks * k, k, ids,
-                       values);
+    // the merge's candidates a lane: the fewest that hold chunks * k
+    const int n = chunks * k;
+    if (n <= 256 * 8)
+        hipLaunchKernelGGL(k_lm_topk_merge<8>, dim3((unsigned)T), dim3(256), 0, s, m.cand_key, m.cand_pos, n, k, ids,
+                           values);
+    else if (n <= 256 * 16)
+        hipLaunchKernelGGL(k_lm_topk_merge<16>, dim3((unsigned)T), dim3(256), 0, s, m.cand_key, m.cand_pos, n, k, ids,
+                           values);
+    else
+        hipLaunchKernelGGL(k_lm_topk_merge<32>, dim3((unsigned)T), dim3(256), 0, s, m.cand_key, m.cand_pos, n, k, ids,
+                           values);
     check(hipGetLastError(), "k_lm_topk_merge launch");
 }
 
