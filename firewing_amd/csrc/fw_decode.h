@@ -1054,6 +1054,10 @@ __device__ __forceinline__ bool stage_acts_direct(const DecodeParams& p, int li,
                     }
                 }
                 if (stale == 0) break;
+                // a pause between polls: 512 workgroups re-reading past the
+                // caches while the layer's rows still stream slow the stream
+                // (1,331 µs per step against 1,342 without it)
+                __builtin_amdgcn_s_sleep(1);
                 if (((++polls & 7) == 0 && coherent_load(p.error) != 0) || wall_clock64() - start > p.limit_ticks) {
                     int32_t expected = 0;
                     __hip_atomic_compare_exchange_strong(p.error, &expected, 1, __ATOMIC_RELAXED, __ATOMIC_RELAXED,
