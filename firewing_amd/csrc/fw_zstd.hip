@@ -23,6 +23,8 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <cstdlib>
+#include <cstring>
 #include <stdexcept>
 #include <type_traits>
 
@@ -608,11 +610,18 @@ constexpr int kSeqWin = 400;     // a lane's window of its bitstream (>= kSeqBac
 // refills of the bit word per sequence (offset + match-length extra bits <=
 // 47, literal-length extra bits + the three state updates <= 42). The wave
 // also writes the staged records out between batches.
+//
+// Table entries: with kWide the four-byte FseEntry (state bits and base read
+// directly; 6 KB of LDS a block, three workgroups a CU), else two bytes
+// (build_fse16: symbol and state counter, the bits and base recomputed per
+// step; 3.2 KB a block, six workgroups a CU). The decoder takes the wide form
+// when the call's blocks fit three workgroups a CU and the narrow one when
+// more blocks must run at once.
+template <bool kWide>
 __global__ void __launch_bounds__(64) k_zs_sequences(Launch L) {
-    // two-byte table entries (build_fse16) and the table build's counts
-    // sharing the record staging: 3.2 KB of LDS a block, so that six
-    // workgroups fit a CU and a 256-frame call's blocks all run at once
-    __shared__ uint16_t tabs[kSeqLanes][kSeqTable];
+    // the table build's counts share the record staging
+    using Entry = std::conditional_t<kWide, FseEntry, uint16_t>;
+    __shared__ Entry tabs[kSeqLanes][kSeqTable];
     __shared__ union {
         struct {
             int16_t norm[64];
@@ -647,7 +656,7 @@ __global__ void __launch_bounds__(64) k_zs_sequences(Launch L) {
         int lg[3] = {0, 0, 0};
         uint32_t sll = 0, sof = 0, sml = 0, rep[3] = {0, 0, 0};
         uint64_t tll = 0, tml = 0;
-        uint16_t* tl = tabs[lane < kSeqLanes ? lane : 0];
+        Entry* tl = tabs[lane < kSeqLanes ? lane : 0];
         if (mine) {
             const Work wk = L.seq_work[w];
             const DevFrame& F = L.frames[wk.frame];
@@ -659,7 +668,11 @@ __global__ void __launch_bounds__(64) k_zs_sequences(Launch L) {
             const uint32_t end = B.src + B.size;
             const int off3[3] = {0, 512, 768};
             for (int k = 0; k < 3 && st == kOk; ++k) {
-                lg[k] = table_for16(f, end, B.table[k], k, tl + off3[k], lane_lds[lane].b.norm, lane_lds[lane].b.next);
+                if constexpr (kWide)
+                    lg[k] = table_for(f, end, B.table[k], k, tl + off3[k], lane_lds[lane].b.norm, lane_lds[lane].b.next);
+                else
+                    lg[k] = table_for16(f, end, B.table[k], k, tl + off3[k], lane_lds[lane].b.norm,
+                                        lane_lds[lane].b.next);
                 if (lg[k] < 0) st = kErrFse;
             }
             rep[0] = rep_entry(0);
@@ -731,9 +744,9 @@ __global__ void __launch_bounds__(64) k_zs_sequences(Launch L) {
                     sof = r.read(lg[1]);
                     sml = r.read(lg[2]);
                 }
-                const uint16_t* tll_ = tl;
-                const uint16_t* tof_ = tl + 512;
-                const uint16_t* tml_ = tl + 768;
+                const Entry* tll_ = tl;
+                const Entry* tof_ = tl + 512;
+                const Entry* tml_ = tl + 768;
                 // symbols are in range by construction (table_for: counts of
                 // at most kMaxSym[kind] symbols, RLE symbols checked)
                 // No branch in a step: the first refill goes out with the
@@ -743,9 +756,16 @@ __global__ void __launch_bounds__(64) k_zs_sequences(Launch L) {
                 for (; k < (uint32_t)kSeqFlush && i < nseq; ++k) {
                     r.refill();
                     uint32_t ll_sym, ll_nb, ll_base, of_sym, of_nb, of_base, ml_sym, ml_nb, ml_base;
-                    fse16_unpack(tll_[sll], lg[0], &ll_sym, &ll_nb, &ll_base);
-                    fse16_unpack(tof_[sof], lg[1], &of_sym, &of_nb, &of_base);
-                    fse16_unpack(tml_[sml], lg[2], &ml_sym, &ml_nb, &ml_base);
+                    if constexpr (kWide) {
+                        const FseEntry ell = tll_[sll], eof = tof_[sof], eml = tml_[sml];
+                        ll_sym = ell.sym, ll_nb = ell.nb, ll_base = ell.base;
+                        of_sym = eof.sym, of_nb = eof.nb, of_base = eof.base;
+                        ml_sym = eml.sym, ml_nb = eml.nb, ml_base = eml.base;
+                    } else {
+                        fse16_unpack(tll_[sll], lg[0], &ll_sym, &ll_nb, &ll_base);
+                        fse16_unpack(tof_[sof], lg[1], &of_sym, &of_nb, &of_base);
+                        fse16_unpack(tml_[sml], lg[2], &ml_sym, &ml_nb, &ml_base);
+                    }
                     const uint32_t mc = mlcode[ml_sym], lc = llcode[ll_sym];
                     const uint32_t ov = (1u << of_sym) + r.read(of_sym);
                     const uint32_t ml = (mc & 0xffffff) + r.read(mc >> 24);
@@ -1426,6 +1446,8 @@ Decoder::Decoder(int device, size_t max_frames, uint64_t max_content) : device_(
         int cus = 0;
         hcheck(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device), "hipDeviceGetAttribute");
         grid_ = std::max(1, cus) * 16;
+        if (const char* e = std::getenv("FIREWING_ZSTD_SEQ_TABLES"))
+            seq_tables_ = std::strcmp(e, "wide") == 0 ? 1 : std::strcmp(e, "narrow") == 0 ? 2 : 0;
     } catch (...) {
         this->~Decoder();
         throw;
@@ -1537,7 +1559,16 @@ bool Decoder::queue(const std::vector<FrameJob>& jobs, hipStream_t s, std::strin
         hipLaunchKernelGGL(k_zs_parse, dim3(grid_), dim3(64), 0, s, L);
         hipLaunchKernelGGL(k_zs_link, dim3((count + 63) / 64), dim3(64), 0, s, L);
         hipLaunchKernelGGL(k_zs_literals, dim3(grid_), dim3(256), 0, s, L);
-        hipLaunchKernelGGL(k_zs_sequences, dim3(grid_), dim3(64), 0, s, L);  // kSeqLanes blocks per workgroup
+        // kSeqLanes blocks per workgroup; the wide tables while the call's
+        // compressed blocks fit three workgroups a CU (estimated as one block
+        // per kBlockMax of the largest content: a performance choice only,
+        // both forms decode alike)
+        const uint64_t blocks_est = (uint64_t)count * ((max_content_ + kBlockMax - 1) / kBlockMax);
+        const bool wide = seq_tables_ == 1 || (seq_tables_ == 0 && blocks_est <= (uint64_t)(grid_ / 16) * 3 * kSeqLanes);
+        if (wide)
+            hipLaunchKernelGGL(k_zs_sequences<true>, dim3(grid_), dim3(64), 0, s, L);
+        else
+            hipLaunchKernelGGL(k_zs_sequences<false>, dim3(grid_), dim3(64), 0, s, L);
         hipLaunchKernelGGL(k_zs_layout, dim3((count + 63) / 64), dim3(64), 0, s, L);
         hipLaunchKernelGGL(k_zs_raw, dim3(grid_), dim3(256), 0, s, L);
         hipLaunchKernelGGL(k_zs_execute, dim3(count), dim3(kExecThreads), sizeof(ExecLds), s, L);

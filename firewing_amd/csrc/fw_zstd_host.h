@@ -74,6 +74,10 @@ class Decoder {
     size_t src_bytes_ = 0;
     hipEvent_t last_ = nullptr;
     int grid_ = 0;  // workgroups of the per-block passes
+    // sequence-pass table entries: 0 chosen per call, 1 four bytes, 2 two
+    // bytes (environment FIREWING_ZSTD_SEQ_TABLES = wide | narrow at creation;
+    // both decode alike, the choice is for speed)
+    int seq_tables_ = 0;
 };
 
 }  // namespace fw::zs

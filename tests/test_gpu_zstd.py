@@ -64,8 +64,15 @@ def run_decode(frames, contents, unshuffle, splits=None, max_frames=8, device_so
     return list(st), out
 
 
+# The sequence pass's table entries: four bytes or two (the decoder picks per
+# call by how many blocks must run at once; both forms are checked here).
+TABLE_FORMS = ["wide", "narrow"]
+
+
+@pytest.mark.parametrize("tables", TABLE_FORMS)
 @pytest.mark.parametrize("level", [1, 3])
-def test_real_shape_expert_frames(level):
+def test_real_shape_expert_frames(level, tables, monkeypatch):
+    monkeypatch.setenv("FIREWING_ZSTD_SEQ_TABLES", tables)
     rng = np.random.default_rng(level)
     H, I = REAL["hidden"], REAL["intermediate"]
     sources, frames = [], []
@@ -129,7 +136,9 @@ def pyarrow_cases():
     return out
 
 
-def test_format_features():
+@pytest.mark.parametrize("tables", TABLE_FORMS)
+def test_format_features(tables, monkeypatch):
+    monkeypatch.setenv("FIREWING_ZSTD_SEQ_TABLES", tables)
     cases = format_cases()
     frames = [fz.compress(data, **kw) for _, data, kw in cases]
     extra = pyarrow_cases()
