@@ -232,8 +232,12 @@ __device__ __forceinline__ uint64_t lds_word8(LdsBytes q) {
 
 // Backward bit reader of the sequence pass: every refill reloads the word at
 // the read position (no branch), leaving at least 57 bits above `lo` (or
-// the stream's start), and a read is two shifts (zeros below the stream's
-// start; a malformed stream drives pos negative and fails the end check).
+// the stream's start). A sequence step reads at most 47 bits between
+// refills, and a valid stream never reads below its start, so read() is one
+// clamped shift; a malformed stream that does gets arbitrary bits (masked to
+// the count, so table states stay in range) and drives pos negative, which
+// fails the end check. peek() shifts in zeros below the start (the Huffman
+// readers' last codewords look past it).
 struct SeqBits {
     LdsBytes p;  // stream byte 0 in the lane's window (an LDS address)
     int32_t pos, lo;
@@ -255,8 +259,7 @@ struct SeqBits {
     __device__ __forceinline__ uint32_t read(int nb) {
         const int32_t sh = pos - lo - nb;
         const uint32_t s1 = (uint32_t)(sh > 0 ? (sh < 63 ? sh : 63) : 0);
-        const uint32_t s2 = (uint32_t)(sh < 0 ? -sh : 0) & 63u;
-        const uint32_t v = (uint32_t)((c >> s1) << s2) & ((1u << nb) - 1u);
+        const uint32_t v = (uint32_t)(c >> s1) & ((1u << nb) - 1u);
         pos -= nb;
         return v;
     }
