@@ -234,7 +234,7 @@ __device__ __forceinline__ uint64_t lds_word8(LdsBytes q) {
 // the read position (no branch), leaving at least 57 bits above `lo` (or
 // the stream's start). A sequence step reads at most 47 bits between
 // refills, and a valid stream never reads below its start, so read() is one
-// clamped shift; a malformed stream that does gets arbitrary bits (masked to
+// shift; a malformed stream that does gets arbitrary bits (masked to
 // the count, so table states stay in range) and drives pos negative, which
 // fails the end check. peek() shifts in zeros below the start (the Huffman
 // readers' last codewords look past it).
@@ -255,13 +255,12 @@ struct SeqBits {
         const uint32_t s2 = (uint32_t)(sh < 0 ? -sh : 0) & 63u;
         return (uint32_t)((c >> s1) << s2) & ((1u << nb) - 1u);
     }
-    // nb <= 31 bits below pos
+    // nb <= 31 bits below pos. After a refill pos - lo <= 64 (64 only when
+    // pos is a multiple of 8, where a read of 0 bits gives 0 through the
+    // mask), so the shift is (pos - lo) mod 64, what the shift unit takes.
     __device__ __forceinline__ uint32_t read(int nb) {
-        const int32_t sh = pos - lo - nb;
-        const uint32_t s1 = (uint32_t)(sh > 0 ? (sh < 63 ? sh : 63) : 0);
-        const uint32_t v = (uint32_t)(c >> s1) & ((1u << nb) - 1u);
         pos -= nb;
-        return v;
+        return (uint32_t)(c >> ((uint32_t)(pos - lo) & 63u)) & ((1u << nb) - 1u);
     }
 };
 
